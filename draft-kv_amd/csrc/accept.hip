@@ -1,0 +1,368 @@
+// (a10) sampling and (a11) the verify decision.
+// Reference: draftkv/engine.py:36-41 (`_probs`), :101-106 (`_sample`),
+// :188-213 (accept loop, bonus token, residual resample).
+//
+// Pipeline (rows of `vocab` float32 logits, cut in chunks of VCH):
+//   1. stats   grid (chunk, row, seq): chunk max, first argmax and
+//              sum exp(x/T - max/T) in float64.
+//   2. decide  grid (seq): merge chunk stats per row, run the accept tests
+//              with the supplied uniforms, choose the final distribution:
+//              p of the bonus row, or the residual clip(p - q) (falling back
+//              to p when it sums to 0); greedy mode: argmax comparisons.
+//   3. sums    grid (chunk, seq): per chunk mass of the final distribution.
+//   4. pick    grid (seq): first index whose cumulative mass exceeds u*total
+//              (numpy Generator.choice semantics: searchsorted 'right').
+// Sampling one row (dkv_sample) is the gamma = 0 case: the bonus row is it.
+#include "dkv_common.h"
+
+namespace dkv {
+
+constexpr int VCH = 4096;
+constexpr int ABLK = 256;
+
+struct ChunkStat {
+    float mx;
+    int arg;
+    double sum;   // sum exp((x - mx)/T) over the chunk (T > 0)
+};
+
+struct SeqState {
+    int mode;        // 0: done (greedy), 1: sample p of row `row`, 2: residual of row `row`
+    int row;
+    double u;        // uniform for the final draw
+};
+
+__device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int s, int row, int gamma,
+                                                int vocab) {
+    // rows 0..gamma: target; gamma+1..2*gamma: draft rows 0..gamma-1
+    if (row <= gamma) return target + ((int64_t)s * (gamma + 1) + row) * vocab;
+    return draft + ((int64_t)s * gamma + (row - gamma - 1)) * vocab;
+}
+
+__global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ target, const float* __restrict__ draft,
+                                                     int gamma, int vocab, float T, int n_chunks,
+                                                     ChunkStat* __restrict__ stats) {
+    const int chunk = blockIdx.x, row = blockIdx.y, s = blockIdx.z;
+    const int n_rows = T > 0.0f ? 2 * gamma + 1 : gamma + 1;
+    if (row >= n_rows) return;
+    const float* x = row_ptr(target, draft, s, row, gamma, vocab);
+    const int i0 = chunk * VCH, i1 = min(vocab, i0 + VCH);
+    __shared__ float smx[ABLK / WAVE];
+    __shared__ int sarg[ABLK / WAVE];
+    __shared__ double ssum[ABLK / WAVE];
+    __shared__ float bmx;
+    float mx = -INFINITY;
+    int arg = INT_MAX;
+    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) {
+        const float v = x[i];
+        if (v > mx || (v == mx && i < arg)) { mx = v; arg = i; }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(mx, o);
+        const int oa = __shfl_xor(arg, o);
+        if (om > mx || (om == mx && oa < arg)) { mx = om; arg = oa; }
+    }
+    const int w = threadIdx.x / WAVE;
+    if (threadIdx.x % WAVE == 0) { smx[w] = mx; sarg[w] = arg; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = smx[0];
+        int a = sarg[0];
+        for (int i = 1; i < ABLK / WAVE; ++i)
+            if (smx[i] > m || (smx[i] == m && sarg[i] < a)) { m = smx[i]; a = sarg[i]; }
+        bmx = m;
+        ChunkStat& cs = stats[((int64_t)s * (2 * gamma + 1) + row) * n_chunks + chunk];
+        cs.mx = m;
+        cs.arg = a;
+        cs.sum = 0.0;
+    }
+    __syncthreads();
+    if (T <= 0.0f) return;
+    const double mT = (double)bmx / (double)T;
+    double sum = 0.0;
+    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) sum += exp((double)x[i] / (double)T - mT);
+    sum = wave_sum_d(sum);
+    if (threadIdx.x % WAVE == 0) ssum[w] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int i = 0; i < ABLK / WAVE; ++i) t += ssum[i];
+        stats[((int64_t)s * (2 * gamma + 1) + row) * n_chunks + chunk].sum = t;
+    }
+}
+
+struct RowNorm {
+    double m;   // max(x)/T
+    double S;   // sum exp(x/T - m)
+    int arg;
+};
+
+__device__ RowNorm merge_row(const ChunkStat* st, int n_chunks, float T) {
+    float mx = -INFINITY;
+    int arg = INT_MAX;
+    for (int c = 0; c < n_chunks; ++c)
+        if (st[c].mx > mx || (st[c].mx == mx && st[c].arg < arg)) { mx = st[c].mx; arg = st[c].arg; }
+    RowNorm r{0.0, 0.0, arg};
+    if (T > 0.0f) {
+        r.m = (double)mx / (double)T;
+        for (int c = 0; c < n_chunks; ++c) r.S += st[c].sum * exp((double)st[c].mx / (double)T - r.m);
+    }
+    return r;
+}
+
+__device__ __forceinline__ double prob(float x, const RowNorm& r, float T) {
+    return exp((double)x / (double)T - r.m) / r.S;
+}
+
+__global__ void decide_kernel(const float* __restrict__ target, const float* __restrict__ draft,
+                              const int32_t* __restrict__ draft_tokens, int gamma, int vocab, float T,
+                              const double* __restrict__ u, int n_chunks, const ChunkStat* __restrict__ stats,
+                              RowNorm* __restrict__ norms, SeqState* __restrict__ state, int32_t* accepted,
+                              int32_t* next_token, int32_t* n_uniforms) {
+    const int s = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    const int R = 2 * gamma + 1;
+    const ChunkStat* st = stats + (int64_t)s * R * n_chunks;
+    const int n_rows = T > 0.0f ? R : gamma + 1;
+    RowNorm* nr = norms + (int64_t)s * R;
+    for (int r = 0; r < n_rows; ++r) nr[r] = merge_row(st + (int64_t)r * n_chunks, n_chunks, T);
+    int acc = 0, used = 0;
+    const double* us = u + (int64_t)s * (gamma + 1);
+    for (int i = 0; i < gamma; ++i) {
+        const int d = draft_tokens[(int64_t)s * gamma + i];
+        bool ok;
+        if (d < 0 || d >= vocab) {
+            ok = false;              // not a token of this vocabulary: never read past the row
+            if (T > 0.0f) ++used;
+        } else if (T <= 0.0f) {
+            ok = nr[i].arg == d;
+        } else {
+            const double p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], nr[i], T);
+            const double q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], nr[gamma + 1 + i], T);
+            const double ratio = q > 0.0 ? p / q : 0.0;
+            ok = us[used] < fmin(1.0, ratio);
+            ++used;
+        }
+        if (!ok) break;
+        ++acc;
+    }
+    SeqState ss{0, acc, 0.0};
+    if (T <= 0.0f) {
+        next_token[s] = nr[acc].arg;
+        if (acc == gamma) ++used;   // the bonus draw is taken even though p is one-hot
+    } else {
+        ss.mode = (acc == gamma) ? 1 : 2;
+        ss.u = us[used];
+        ++used;
+    }
+    state[s] = ss;
+    accepted[s] = acc;
+    n_uniforms[s] = used;
+}
+
+// probability of index i under the final distribution of sequence s
+__device__ __forceinline__ double final_mass(const float* p_row, const float* q_row, const RowNorm& pn,
+                                             const RowNorm& qn, int mode, int i, float T) {
+    const double p = prob(p_row[i], pn, T);
+    if (mode == 1) return p;
+    const double r = p - prob(q_row[i], qn, T);
+    return r > 0.0 ? r : 0.0;
+}
+
+__global__ void __launch_bounds__(ABLK) sums_kernel(const float* __restrict__ target, const float* __restrict__ draft,
+                                                    int gamma, int vocab, float T, int n_chunks,
+                                                    const RowNorm* __restrict__ norms,
+                                                    const SeqState* __restrict__ state, double* __restrict__ csum) {
+    const int chunk = blockIdx.x, s = blockIdx.y;
+    const SeqState ss = state[s];
+    if (ss.mode == 0) return;
+    const int R = 2 * gamma + 1;
+    const RowNorm* nr = norms + (int64_t)s * R;
+    const float* pr = row_ptr(target, draft, s, ss.row, gamma, vocab);
+    const float* qr = ss.mode == 2 ? row_ptr(target, draft, s, gamma + 1 + ss.row, gamma, vocab) : pr;
+    const RowNorm pn = nr[ss.row], qn = ss.mode == 2 ? nr[gamma + 1 + ss.row] : pn;
+    const int i0 = chunk * VCH, i1 = min(vocab, i0 + VCH);
+    double sum = 0.0;
+    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) sum += final_mass(pr, qr, pn, qn, ss.mode, i, T);
+    sum = wave_sum_d(sum);
+    __shared__ double ssum[ABLK / WAVE];
+    if (threadIdx.x % WAVE == 0) ssum[threadIdx.x / WAVE] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int i = 0; i < ABLK / WAVE; ++i) t += ssum[i];
+        csum[(int64_t)s * n_chunks + chunk] = t;
+    }
+}
+
+__global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ target, const float* __restrict__ draft,
+                                                    int gamma, int vocab, float T, int n_chunks,
+                                                    const ChunkStat* __restrict__ stats,
+                                                    const RowNorm* __restrict__ norms,
+                                                    const SeqState* __restrict__ state,
+                                                    const double* __restrict__ csum, int32_t* next_token) {
+    const int s = blockIdx.x;
+    const SeqState ss = state[s];
+    if (ss.mode == 0) return;
+    const int R = 2 * gamma + 1;
+    const RowNorm* nr = norms + (int64_t)s * R;
+    const double* cs = csum + (int64_t)s * n_chunks;
+    const ChunkStat* pst = stats + ((int64_t)s * R + ss.row) * n_chunks;
+    __shared__ int s_chunk, s_mode;
+    __shared__ double s_before, s_target;
+    if (threadIdx.x == 0) {
+        int mode = ss.mode;
+        double total = 0.0;
+        for (int c = 0; c < n_chunks; ++c) total += cs[c];
+        // an all-zero residual falls back to p itself (engine.py:210-211); p's
+        // chunk masses then come from the row statistics
+        const bool from_p = (mode == 2 && !(total > 0.0));
+        if (from_p) mode = 1;
+        const RowNorm pn = nr[ss.row];
+        auto chunk_mass = [&](int c) -> double {
+            return from_p ? pst[c].sum * exp((double)pst[c].mx / (double)T - pn.m) / pn.S : cs[c];
+        };
+        if (from_p) {
+            total = 0.0;
+            for (int c = 0; c < n_chunks; ++c) total += chunk_mass(c);
+        }
+        const double tgt = ss.u * total;
+        double run = 0.0;
+        int chosen = n_chunks - 1;
+        bool hit = false;
+        for (int c = 0; c < n_chunks; ++c) {
+            const double cm = chunk_mass(c);
+            if (run + cm > tgt) {
+                chosen = c;
+                hit = true;
+                break;
+            }
+            run += cm;
+        }
+        // rounding carried the draw past the end: scan the last chunk from its start
+        if (!hit) run -= chunk_mass(chosen);
+        s_chunk = chosen;
+        s_mode = mode;
+        s_before = run;
+        s_target = tgt;
+    }
+    __syncthreads();
+    const int mode = s_mode;
+    const float* pr = row_ptr(target, draft, s, ss.row, gamma, vocab);
+    const float* qr = mode == 2 ? row_ptr(target, draft, s, gamma + 1 + ss.row, gamma, vocab) : pr;
+    const RowNorm pn = nr[ss.row], qn = mode == 2 ? nr[gamma + 1 + ss.row] : pn;
+    const int c = s_chunk;
+    const int i0 = c * VCH, i1 = min(vocab, i0 + VCH);
+    const double tgt = s_target;
+    // block-wide inclusive scan over the chunk, ABLK elements at a time
+    __shared__ double wsum[ABLK / WAVE];
+    __shared__ int found, last_pos;
+    __shared__ double run;
+    if (threadIdx.x == 0) {
+        found = INT_MAX;
+        last_pos = -1;
+        run = s_before;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
+    for (int base = i0; base < i1; base += ABLK) {
+        const int i = base + threadIdx.x;
+        const double v = i < i1 ? final_mass(pr, qr, pn, qn, mode, i, T) : 0.0;
+        double x = v;
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const double y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (lane == WAVE - 1) wsum[w] = x;
+        __syncthreads();
+        double off = run;
+        for (int k = 0; k < w; ++k) off += wsum[k];
+        if (i < i1 && v > 0.0) {
+            if (off + x > tgt) atomicMin(&found, i);
+            atomicMax(&last_pos, i);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double t = run;
+            for (int k = 0; k < ABLK / WAVE; ++k) t += wsum[k];
+            run = t;
+        }
+        __syncthreads();
+        if (found != INT_MAX) break;
+    }
+    if (threadIdx.x == 0) {
+        // a draw that rounding pushes past the end of the cdf takes the last
+        // index with positive mass (the reference's cdf ends at exactly 1)
+        next_token[s] = found != INT_MAX ? found : (last_pos >= 0 ? last_pos : i1 - 1);
+    }
+}
+
+}  // namespace dkv
+
+using namespace dkv;
+
+static int chunks_of(int vocab) { return (vocab + VCH - 1) / VCH; }
+
+extern "C" size_t dkv_accept_workspace(int32_t batch, int32_t gamma, int32_t vocab) {
+    if (batch <= 0 || gamma < 0 || vocab <= 0) return 0;
+    const size_t nc = chunks_of(vocab), R = 2 * (size_t)gamma + 1;
+    return sizeof(ChunkStat) * batch * R * nc + sizeof(RowNorm) * batch * R + sizeof(SeqState) * batch +
+           sizeof(double) * batch * nc + 256;
+}
+
+extern "C" int dkv_accept(const float* target, const float* draft, const int32_t* draft_tokens, int32_t batch,
+                          int32_t gamma, int32_t vocab, float temperature, const double* u, int32_t* accepted,
+                          int32_t* next_token, int32_t* n_uniforms, void* work, size_t work_bytes,
+                          dkv_stream_t stream) {
+    DKV_REQUIRE(target && accepted && next_token && n_uniforms && u, "dkv_accept: NULL argument");
+    DKV_REQUIRE(batch > 0 && gamma >= 0 && vocab > 0, "dkv_accept: bad sizes");
+    DKV_REQUIRE(gamma == 0 || draft_tokens, "dkv_accept: draft_tokens is NULL");
+    DKV_REQUIRE(temperature <= 0.0f || gamma == 0 || draft, "dkv_accept: draft logits needed when T > 0");
+    const size_t need = dkv_accept_workspace(batch, gamma, vocab);
+    if (!work || work_bytes < need)
+        return fail(DKV_EWORKSPACE, "dkv_accept: workspace too small (need " + std::to_string(need) + ")");
+    const int nc = chunks_of(vocab), R = 2 * gamma + 1;
+    char* w = static_cast<char*>(work);
+    ChunkStat* stats = reinterpret_cast<ChunkStat*>(w);
+    w += sizeof(ChunkStat) * batch * R * nc;
+    RowNorm* norms = reinterpret_cast<RowNorm*>(w);
+    w += sizeof(RowNorm) * batch * R;
+    SeqState* state = reinterpret_cast<SeqState*>(w);
+    w += sizeof(SeqState) * batch;
+    double* csum = reinterpret_cast<double*>(w);
+    hipStream_t st = as_stream(stream);
+    const int rows = temperature > 0.0f ? R : gamma + 1;
+    hipLaunchKernelGGL(stats_kernel, dim3(nc, rows, batch), dim3(ABLK), 0, st, target, draft, gamma, vocab,
+                       temperature, nc, stats);
+    int rc = check_launch("dkv_accept(stats)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(decide_kernel, dim3(batch), dim3(64), 0, st, target, draft, draft_tokens, gamma, vocab,
+                       temperature, u, nc, stats, norms, state, accepted, next_token, n_uniforms);
+    if ((rc = check_launch("dkv_accept(decide)"))) return rc;
+    if (temperature <= 0.0f) return DKV_OK;
+    hipLaunchKernelGGL(sums_kernel, dim3(nc, batch), dim3(ABLK), 0, st, target, draft, gamma, vocab, temperature, nc,
+                       norms, state, csum);
+    if ((rc = check_launch("dkv_accept(sums)"))) return rc;
+    hipLaunchKernelGGL(pick_kernel, dim3(batch), dim3(ABLK), 0, st, target, draft, gamma, vocab, temperature, nc,
+                       stats, norms, state, csum, next_token);
+    return check_launch("dkv_accept(pick)");
+}
+
+extern "C" size_t dkv_sample_workspace(int32_t batch, int32_t vocab) {
+    // gamma = 0 accept plus room for the per-row counters it returns
+    return dkv_accept_workspace(batch, 0, vocab) + 2 * sizeof(int32_t) * (size_t)batch + 256;
+}
+
+extern "C" int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t vocab, float temperature,
+                          const double* u, int32_t* tokens, void* work, size_t work_bytes, dkv_stream_t stream) {
+    DKV_REQUIRE(logits && u && tokens, "dkv_sample: NULL argument");
+    DKV_REQUIRE(row_stride == vocab, "dkv_sample: rows must be contiguous (row_stride == vocab)");
+    const size_t need = dkv_sample_workspace(batch, vocab);
+    if (!work || work_bytes < need)
+        return fail(DKV_EWORKSPACE, "dkv_sample: workspace too small (need " + std::to_string(need) + ")");
+    char* w = static_cast<char*>(work);
+    const size_t acc_ws = dkv_accept_workspace(batch, 0, vocab);
+    int32_t* scratch_i = reinterpret_cast<int32_t*>(w + ((acc_ws + 255) / 256) * 256);
+    return dkv_accept(logits, nullptr, nullptr, batch, 0, vocab, temperature, u, scratch_i, tokens,
+                      scratch_i + batch, work, acc_ws, stream);
+}

@@ -1,0 +1,187 @@
+// Shared device/host helpers for the DRAFTKV gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/draftkv_hip.h"
+
+namespace dkv {
+
+// ------------------------------------------------------------ error state
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+#define DKV_REQUIRE(cond, msg)                                   \
+    do {                                                         \
+        if (!(cond)) return ::dkv::fail(DKV_EINVAL, (msg));      \
+    } while (0)
+
+inline hipStream_t as_stream(dkv_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------ numerics
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f32_to_half_bits_rne(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+// load element i of a row stored as f32 or bf16
+__device__ __forceinline__ float load_elem(const void* base, int64_t i, int dtype) {
+    return dtype == DKV_BF16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[i])
+                             : reinterpret_cast<const float*>(base)[i];
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// ------------------------------------------------------------ quantizer
+// Bit-exact restatement of the reference's float32 op order
+// (draftkv/compress.py:38-43): lo/hi = group min/max (zero padding of a short
+// last group takes part), scale = max((hi-lo)/levels, 1e-8), q = rint((x-lo)/
+// scale) clipped to [0, levels], deq = q*scale + lo with two roundings.
+// With fp16 meta the stored (rounded) lo/scale are used for the codes.
+struct GroupMeta {
+    float scale, lo;
+};
+
+__device__ __forceinline__ GroupMeta group_meta(float lo, float hi, int bits, int meta_f16) {
+#pragma clang fp contract(off)
+    const float levels = static_cast<float>((1 << bits) - 1);
+    float scale = fmaxf(__fdiv_rn(__fsub_rn(hi, lo), levels), 1e-8f);
+    if (meta_f16) {
+        lo = half_bits_to_f32(f32_to_half_bits_rne(lo));
+        scale = half_bits_to_f32(f32_to_half_bits_rne(scale));
+        if (scale == 0.0f) scale = 5.9604644775390625e-08f;  // 2^-24, smallest half
+    }
+    return {scale, lo};
+}
+
+__device__ __forceinline__ int quant_code(float x, GroupMeta m, int bits) {
+#pragma clang fp contract(off)
+    const float levels = static_cast<float>((1 << bits) - 1);
+    float q = rintf(__fdiv_rn(__fsub_rn(x, m.lo), m.scale));
+    q = fminf(fmaxf(q, 0.0f), levels);
+    return static_cast<int>(q);
+}
+
+__device__ __forceinline__ float dequant(int code, GroupMeta m) {
+    // the empty asm hides the product from the optimizer so it cannot be
+    // contracted into an FMA: the reference rounds the product, then the sum
+    float prod = __fmul_rn(static_cast<float>(code), m.scale);
+    asm volatile("" : "+v"(prod));
+    return __fadd_rn(prod, m.lo);
+}
+
+// bytes one head-row of codes occupies for a given bit width
+__host__ __device__ inline int64_t code_row_bytes(int bits, int d) {
+    return bits >= 16 ? 4 * (int64_t)d : (bits == 8 ? (int64_t)d : ((int64_t)d + 1) / 2);
+}
+__host__ __device__ inline int n_groups(int d, int group) { return (d + group - 1) / group; }
+__host__ __device__ inline int64_t meta_row_bytes(int bits, int d, int group, int meta_f16) {
+    return bits >= 16 ? 0 : (int64_t)n_groups(d, group) * (meta_f16 ? 4 : 8);
+}
+
+// read code j of a packed head-row
+__device__ __forceinline__ int get_code(const uint8_t* row, int j, int bits) {
+    if (bits == 8) return row[j];
+    uint8_t b = row[j >> 1];
+    return (j & 1) ? (b >> 4) : (b & 0xf);
+}
+
+__device__ __forceinline__ GroupMeta get_meta(const uint8_t* mrow, int g, int meta_f16) {
+    if (meta_f16) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(mrow);
+        return {half_bits_to_f32(h[2 * g]), half_bits_to_f32(h[2 * g + 1])};
+    }
+    const float* f = reinterpret_cast<const float*>(mrow);
+    return {f[2 * g], f[2 * g + 1]};
+}
+
+__device__ __forceinline__ void put_meta(uint8_t* mrow, int g, GroupMeta m, int meta_f16) {
+    if (meta_f16) {
+        uint16_t* h = reinterpret_cast<uint16_t*>(mrow);
+        h[2 * g] = f32_to_half_bits_rne(m.scale);
+        h[2 * g + 1] = f32_to_half_bits_rne(m.lo);
+    } else {
+        float* f = reinterpret_cast<float*>(mrow);
+        f[2 * g] = m.scale;
+        f[2 * g + 1] = m.lo;
+    }
+}
+
+// ------------------------------------------------------------ mirror addressing
+struct Seg {
+    uint8_t* kc;
+    uint8_t* vc;
+    uint8_t* km;
+    uint8_t* vm;
+};
+
+__host__ __device__ inline int64_t seg_index(const dkv_drafter_t& m, int s, int L, int h) {
+    return ((int64_t)(s * m.n_layers + L) * m.n_kv_heads + h);
+}
+
+__device__ __forceinline__ Seg seg_of(const dkv_drafter_t& m, int s, int L, int h) {
+    const int64_t i = seg_index(m, s, L, h) * m.cap;
+    return {static_cast<uint8_t*>(m.kc) + i * m.code_stride, static_cast<uint8_t*>(m.vc) + i * m.code_stride,
+            static_cast<uint8_t*>(m.km) + i * m.meta_stride, static_cast<uint8_t*>(m.vm) + i * m.meta_stride};
+}
+
+__host__ __device__ inline int64_t row_index(const dkv_drafter_t& m, int s, int L) {
+    return (int64_t)(s * m.n_layers + L) * m.cap;
+}
+
+// ------------------------------------------------------------ paged addressing
+__host__ __device__ inline int64_t paged_esize(const dkv_paged_t& c) { return c.dtype == DKV_BF16 ? 2 : 4; }
+__host__ __device__ inline int64_t paged_block_elems(const dkv_paged_t& c) {
+    return 2LL * c.n_kv_heads * c.block_size * c.head_dim;
+}
+
+// element offsets (in elements) of K[pos][h][d] and V[pos][h][d] for (s, L)
+__device__ __forceinline__ int32_t paged_block(const dkv_paged_t& c, int s, int L, int pos) {
+    return c.block_table[((int64_t)s * c.n_layers + L) * c.max_blocks + pos / c.block_size];
+}
+__device__ __forceinline__ int64_t paged_k_off(const dkv_paged_t& c, int32_t blk, int off, int h, int d) {
+    return (int64_t)blk * paged_block_elems(c) + ((int64_t)h * c.block_size + off) * c.head_dim + d;
+}
+__device__ __forceinline__ int64_t paged_v_off(const dkv_paged_t& c, int32_t blk, int off, int h, int d) {
+    return (int64_t)blk * paged_block_elems(c) + (int64_t)c.n_kv_heads * c.block_size * c.head_dim +
+           ((int64_t)h * c.head_dim + d) * c.block_size + off;
+}
+
+}  // namespace dkv

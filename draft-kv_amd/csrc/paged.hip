@@ -1,0 +1,273 @@
+// (a7) paged full-cache append and (a8) causal attention over it.
+// Reference: draftkv/paged.py:76-176 (cache), draftkv/llama.py:202-218 and
+// gpt2.py/model.py equivalents (read + masked softmax attention).
+#include "dkv_common.h"
+
+namespace dkv {
+
+// ---------------------------------------------------------------- append
+__global__ void __launch_bounds__(256) paged_append_kernel(dkv_paged_t c, int layer, const void* __restrict__ k,
+                                                           const void* __restrict__ v, int in_dtype, int T,
+                                                           const int32_t* __restrict__ start,
+                                                           const int32_t* __restrict__ count) {
+    const int t = blockIdx.x, s = blockIdx.y;
+    if (count && t >= count[s]) return;
+    const int pos = start[s] + t;
+    const int32_t blk = paged_block(c, s, layer, pos);
+    const int off = pos % c.block_size;
+    const int HD = c.n_kv_heads * c.head_dim;
+    const int64_t src = ((int64_t)s * T + t) * HD;
+    for (int i = threadIdx.x; i < HD; i += blockDim.x) {
+        const int h = i / c.head_dim, d = i % c.head_dim;
+        const float kv = load_elem(k, src + i, in_dtype);
+        const float vv = load_elem(v, src + i, in_dtype);
+        const int64_t ko = paged_k_off(c, blk, off, h, d), vo = paged_v_off(c, blk, off, h, d);
+        if (c.dtype == DKV_BF16) {
+            static_cast<uint16_t*>(c.pool)[ko] = f32_to_bf16_rne(kv);
+            static_cast<uint16_t*>(c.pool)[vo] = f32_to_bf16_rne(vv);
+        } else {
+            static_cast<float*>(c.pool)[ko] = kv;
+            static_cast<float*>(c.pool)[vo] = vv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- attention
+// Grid: x = chunk * n_qtiles + qtile, y = kv head, z = sequence.
+// A block owns QB query rows (query row r -> step t = r / G, head h*G + r%G)
+// and the keys [chunk*CH, min((chunk+1)*CH, len)). Keys are walked in tiles
+// of KT at fixed absolute offsets; per query row the arithmetic (dot order,
+// tile max/sum order, rescale sequence) depends only on absolute key indices,
+// never on T or on how many rows share the block, so a row's partial is
+// bit-identical whether it is computed in a verify pass (T = gamma+1) or in a
+// one-token decode step. Masked keys contribute exact zeros.
+constexpr int QB = 16;
+constexpr int KT = 32;
+constexpr int MAXD = 128;   // LDS tiles stay under 64 KB
+
+__global__ void __launch_bounds__(256) paged_attn_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
+                                                         int T, int Hq, const int32_t* __restrict__ start,
+                                                         int CH, int n_chunks, int n_qtiles, float scale,
+                                                         float* __restrict__ part) {
+    const int chunk = blockIdx.x / n_qtiles, qtile = blockIdx.x % n_qtiles;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int D = c.head_dim, G = Hq / c.n_kv_heads;
+    const int s0 = start[s];
+    const int len = s0 + T;                       // cache holds positions 0..len-1
+    const int k_begin = chunk * CH;
+    if (k_begin >= len) return;
+    const int k_end = min(k_begin + CH, len);
+    const int n_rows = T * G;
+    const int r0 = qtile * QB;
+    if (r0 >= n_rows) return;
+    const int nr = min(QB, n_rows - r0);
+    // last key any of this block's rows may see
+    const int max_qpos = s0 + (r0 + nr - 1) / G;
+    if (k_begin > max_qpos) return;
+
+    extern __shared__ float smem[];
+    float* sQ = smem;                               // [QB][D]
+    float* sK = sQ + QB * D;                        // [KT][D+1]
+    float* sV = sK + KT * (D + 1);                  // [KT][D]
+    float* sS = sV + KT * D;                        // [QB][KT]
+    float* sM = sS + QB * KT;                       // [QB] running max
+    float* sL = sM + QB;                            // [QB] running sum
+    float* sA = sL + QB;                            // [QB] rescale factor of this tile
+
+    const int tid = threadIdx.x;
+    for (int i = tid; i < QB * D; i += blockDim.x) {
+        const int r = i / D, d = i % D;
+        float val = 0.0f;
+        if (r < nr) {
+            const int rr = r0 + r, t = rr / G, hq = h * G + rr % G;
+            val = q[(((int64_t)s * T + t) * Hq + hq) * D + d];
+        }
+        sQ[i] = val;
+    }
+    if (tid < QB) {
+        sM[tid] = -INFINITY;
+        sL[tid] = 0.0f;
+    }
+    // accumulators: outputs o = tid + 256*j (row o / D, dim o % D)
+    constexpr int MAXACC = QB * MAXD / 256;
+    float acc[MAXACC];
+#pragma unroll
+    for (int j = 0; j < MAXACC; ++j) acc[j] = 0.0f;
+    const int n_out = QB * D;
+
+    const int kend_eff = min(k_end, max_qpos + 1);
+    for (int kt = k_begin; kt < kend_eff; kt += KT) {
+        __syncthreads();
+        // load K and V tiles (keys kt .. kt+KT-1, zero past the cache)
+        for (int i = tid; i < KT * D; i += blockDim.x) {
+            const int j = i / D, d = i % D;
+            const int pos = kt + j;
+            float kv = 0.0f, vv = 0.0f;
+            if (pos < len) {
+                const int32_t blk = paged_block(c, s, layer, pos);
+                const int off = pos % c.block_size;
+                kv = load_elem(c.pool, paged_k_off(c, blk, off, h, d), c.dtype);
+                vv = load_elem(c.pool, paged_v_off(c, blk, off, h, d), c.dtype);
+            }
+            sK[j * (D + 1) + d] = kv;
+            sV[j * D + d] = vv;
+        }
+        __syncthreads();
+        // scores
+        for (int i = tid; i < QB * KT; i += blockDim.x) {
+            const int r = i / KT, j = i % KT;
+            const int pos = kt + j;
+            float sc = -INFINITY;
+            if (r < nr) {
+                const int qpos = s0 + (r0 + r) / G;
+                if (pos <= qpos && pos < len) {
+                    float dot = 0.0f;
+                    for (int d = 0; d < D; ++d) dot = fmaf(sQ[r * D + d], sK[j * (D + 1) + d], dot);
+                    sc = dot * scale;
+                }
+            }
+            sS[i] = sc;
+        }
+        __syncthreads();
+        // online softmax per row: 16 lanes per row, fixed reduction tree
+        {
+            const int r = tid / 16, l16 = tid % 16;   // 256 threads = QB rows x 16
+            float mx = -INFINITY;
+            for (int j = l16; j < KT; j += 16) mx = fmaxf(mx, sS[r * KT + j]);
+            for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+            const float m_old = sM[r];
+            const float m_new = fmaxf(m_old, mx);
+            float sum = 0.0f;
+            for (int j = l16; j < KT; j += 16) {
+                const float sc = sS[r * KT + j];
+                const float p = (sc == -INFINITY) ? 0.0f : __expf(sc - m_new);
+                sS[r * KT + j] = p;
+                sum += p;
+            }
+            for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+            __syncthreads();
+            if (l16 == 0) {
+                const float a = (m_old == -INFINITY) ? 0.0f : __expf(m_old - m_new);
+                sA[r] = a;
+                sL[r] = sL[r] * a + sum;
+                sM[r] = m_new;
+            }
+        }
+        __syncthreads();
+        // PV
+#pragma unroll
+        for (int jj = 0; jj < MAXACC; ++jj) {
+            const int o = tid + 256 * jj;
+            if (o < n_out) {
+                const int r = o / D, d = o % D;
+                float a = acc[jj] * sA[r];
+                for (int j = 0; j < KT; ++j) a = fmaf(sS[r * KT + j], sV[j * D + d], a);
+                acc[jj] = a;
+            }
+        }
+    }
+    __syncthreads();
+    // write partials: [((s*T + t)*Hq + hq) * n_chunks + chunk] * (D + 2)
+#pragma unroll
+    for (int jj = 0; jj < MAXACC; ++jj) {
+        const int o = tid + 256 * jj;
+        if (o < n_out) {
+            const int r = o / D, d = o % D;
+            if (r < nr) {
+                const int rr = r0 + r, t = rr / G, hq = h * G + rr % G;
+                float* p = part + ((((int64_t)s * T + t) * Hq + hq) * n_chunks + chunk) * (D + 2);
+                p[d] = acc[jj];
+                if (d == 0) {
+                    p[D] = sM[r];
+                    p[D + 1] = sL[r];
+                }
+            }
+        }
+    }
+}
+
+// Merge the chunk partials of each query row in chunk order; chunks that
+// start past the row's position were never computed for it and are skipped.
+__global__ void __launch_bounds__(256) paged_combine_kernel(const float* __restrict__ part, int T, int Hq, int D,
+                                                            const int32_t* __restrict__ start, int CH,
+                                                            int n_chunks, float* __restrict__ out) {
+    const int hq = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
+    const int qpos = start[s] + t;
+    const int nc = min(qpos / CH + 1, n_chunks);   // never past the workspace
+    const float* p = part + (((int64_t)s * T + t) * Hq + hq) * n_chunks * (D + 2);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float m = -INFINITY, l = 0.0f, o = 0.0f;
+        for (int ch = 0; ch < nc; ++ch) {
+            const float* pc = p + (int64_t)ch * (D + 2);
+            const float mc = pc[D], lc = pc[D + 1];
+            const float mn = fmaxf(m, mc);
+            const float a = (m == -INFINITY) ? 0.0f : __expf(m - mn);
+            const float b = (mc == -INFINITY) ? 0.0f : __expf(mc - mn);
+            l = l * a + lc * b;
+            o = o * a + pc[d] * b;
+            m = mn;
+        }
+        out[(((int64_t)s * T + t) * Hq + hq) * D + d] = o / l;
+    }
+}
+
+static size_t attn_smem(int D) {
+    return sizeof(float) * (QB * D + KT * (D + 1) + KT * D + QB * KT + 3 * QB);
+}
+
+}  // namespace dkv
+
+extern "C" int dkv_paged_append(const dkv_paged_t* cache, int32_t layer, const void* k, const void* v,
+                                int32_t in_dtype, int32_t T, const int32_t* start, const int32_t* count,
+                                dkv_stream_t stream) {
+    DKV_REQUIRE(cache && k && v && start, "dkv_paged_append: NULL argument");
+    const dkv_paged_t c = *cache;
+    DKV_REQUIRE(layer >= 0 && layer < c.n_layers, "dkv_paged_append: layer out of range");
+    DKV_REQUIRE(c.dtype == DKV_F32 || c.dtype == DKV_BF16, "dkv_paged_append: bad cache dtype");
+    DKV_REQUIRE(in_dtype == DKV_F32 || in_dtype == DKV_BF16, "dkv_paged_append: bad input dtype");
+    DKV_REQUIRE(c.batch > 0 && c.block_size > 0 && c.max_blocks > 0, "dkv_paged_append: bad cache shape");
+    if (T <= 0) return DKV_OK;
+    hipLaunchKernelGGL(dkv::paged_append_kernel, dim3(T, c.batch), dim3(256), 0, dkv::as_stream(stream), c, layer,
+                       k, v, in_dtype, T, start, count);
+    return dkv::check_launch("dkv_paged_append");
+}
+
+static int n_chunks_for(int max_len, int chunk_keys) { return (max_len + chunk_keys - 1) / chunk_keys; }
+
+extern "C" size_t dkv_paged_attention_workspace(const dkv_paged_t* cache, int32_t T, int32_t n_q_heads,
+                                                int32_t max_len, int32_t chunk_keys) {
+    if (!cache || T <= 0 || n_q_heads <= 0 || max_len <= 0 || chunk_keys <= 0) return 0;
+    return sizeof(float) * (size_t)cache->batch * T * n_q_heads * n_chunks_for(max_len, chunk_keys) *
+           (cache->head_dim + 2);
+}
+
+extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, const float* q, int32_t T,
+                                   int32_t n_q_heads, const int32_t* start, int32_t max_len, int32_t chunk_keys,
+                                   float* out, void* work, size_t work_bytes, dkv_stream_t stream) {
+    DKV_REQUIRE(cache && q && start && out, "dkv_paged_attention: NULL argument");
+    const dkv_paged_t c = *cache;
+    DKV_REQUIRE(layer >= 0 && layer < c.n_layers, "dkv_paged_attention: layer out of range");
+    DKV_REQUIRE(c.head_dim > 0 && c.head_dim <= dkv::MAXD, "dkv_paged_attention: head_dim must be 1..128");
+    DKV_REQUIRE(n_q_heads > 0 && n_q_heads % c.n_kv_heads == 0,
+                "dkv_paged_attention: query heads must be a multiple of KV heads");
+    DKV_REQUIRE(chunk_keys > 0 && chunk_keys % dkv::KT == 0, "dkv_paged_attention: chunk_keys must be a multiple of 32");
+    DKV_REQUIRE(max_len > 0, "dkv_paged_attention: max_len must be > 0");
+    if (T <= 0) return DKV_OK;
+    const size_t need = dkv_paged_attention_workspace(cache, T, n_q_heads, max_len, chunk_keys);
+    if (!work || work_bytes < need)
+        return dkv::fail(DKV_EWORKSPACE, "dkv_paged_attention: workspace too small (need " + std::to_string(need) + ")");
+    const int n_chunks = n_chunks_for(max_len, chunk_keys);
+    const int G = n_q_heads / c.n_kv_heads;
+    const int n_qtiles = (T * G + dkv::QB - 1) / dkv::QB;
+    DKV_REQUIRE((int64_t)n_chunks * n_qtiles < (1LL << 31), "dkv_paged_attention: grid too large");
+    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(c.head_dim)));
+    hipStream_t st = dkv::as_stream(stream);
+    hipLaunchKernelGGL(dkv::paged_attn_kernel, dim3(n_chunks * n_qtiles, c.n_kv_heads, c.batch), dim3(256),
+                       dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, chunk_keys, n_chunks,
+                       n_qtiles, scale, static_cast<float*>(work));
+    int rc = dkv::check_launch("dkv_paged_attention");
+    if (rc) return rc;
+    hipLaunchKernelGGL(dkv::paged_combine_kernel, dim3(n_q_heads, T, c.batch), dim3(128), 0, st,
+                       static_cast<const float*>(work), T, n_q_heads, c.head_dim, start, chunk_keys, n_chunks, out);
+    return dkv::check_launch("dkv_paged_attention(combine)");
+}

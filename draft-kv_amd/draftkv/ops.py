@@ -1,0 +1,227 @@
+"""Torch-tensor front end of the HIP entry points (device buffers in, device
+buffers out). Every function validates shapes/dtypes on the host, hands raw
+device pointers to the C ABI on torch's current stream, and raises on a
+non-zero status. There is no CPU path."""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import DKV_BF16, DKV_F32, Drafter, Paged, QCfg, check, lib
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, ndim=None) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got {tuple(t.shape)}")
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DKV_F32
+    if t.dtype == torch.bfloat16:
+        return DKV_BF16
+    raise ValueError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+
+
+class Workspace:
+    """Grow-only scratch buffer per device (allocates only when a call needs more)."""
+
+    def __init__(self) -> None:
+        self._buf: dict = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        key = (device.type, device.index)
+        b = self._buf.get(key)
+        if b is None or b.numel() < nbytes:
+            b = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            self._buf[key] = b
+        return b
+
+
+_WS = Workspace()
+
+
+def qcfg(bits: int, group: int = 64, meta_f16: bool = False, sink: int = 4, recent: int = 32) -> QCfg:
+    return QCfg(int(bits), int(group), int(bool(meta_f16)), int(sink), int(recent))
+
+
+# ------------------------------------------------------------------ (a1)
+def quantize_codes(x: torch.Tensor, bits: int, group: int = 64, meta_f16: bool = False):
+    """Group quantization of the last axis (reference compress.py:21-46).
+    Returns (codes u8, scale f32, lo f32, deq f32)."""
+    _need(x, "x", torch.float32)
+    if bits >= 16:
+        raise ValueError("bits >= 16 has no codes")
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    ng = -(-d // group)
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scale = torch.empty(x.shape[:-1] + (ng,), dtype=torch.float32, device=x.device)
+    lo = torch.empty_like(scale)
+    deq = torch.empty_like(x)
+    check(lib().dkv_quantize(x.data_ptr(), rows, d, bits, group, int(bool(meta_f16)), codes.data_ptr(),
+                             scale.data_ptr(), lo.data_ptr(), deq.data_ptr(), _stream()), "dkv_quantize")
+    return codes, scale, lo, deq
+
+
+# ------------------------------------------------------------------ (a7, a8)
+def paged_append(desc: Paged, layer: int, k: torch.Tensor, v: torch.Tensor, start: torch.Tensor,
+                 count: Optional[torch.Tensor] = None) -> None:
+    _need(k, "k", ndim=4)
+    _need(v, "v", ndim=4)
+    _need(start, "start", torch.int32)
+    if k.shape != v.shape or k.dtype != v.dtype:
+        raise ValueError("k and v must match")
+    b, T, H, D = k.shape
+    if b != desc.batch or H != desc.n_kv_heads or D != desc.head_dim:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match the cache")
+    check(lib().dkv_paged_append(C.byref(desc), layer, k.data_ptr(), v.data_ptr(), _dt(k), T,
+                                 start.data_ptr(), _ptr(count), _stream()), "dkv_paged_append")
+
+
+def paged_attention(desc: Paged, layer: int, q: torch.Tensor, start: torch.Tensor, max_len: int,
+                    chunk_keys: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _need(q, "q", torch.float32, 4)
+    _need(start, "start", torch.int32)
+    b, T, Hq, D = q.shape
+    if b != desc.batch or D != desc.head_dim:
+        raise ValueError(f"q shape {tuple(q.shape)} does not match the cache")
+    if out is None:
+        out = torch.empty_like(q)
+    nbytes = lib().dkv_paged_attention_workspace(C.byref(desc), T, Hq, max_len, chunk_keys)
+    ws = _WS.get(q.device, nbytes)
+    check(lib().dkv_paged_attention(C.byref(desc), layer, q.data_ptr(), T, Hq, start.data_ptr(), max_len,
+                                    chunk_keys, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream()),
+          "dkv_paged_attention")
+    return out
+
+
+# ------------------------------------------------------------------ mirror
+def _qarr(cfgs: Sequence[QCfg]):
+    arr = (QCfg * len(cfgs))(*cfgs)
+    return arr
+
+
+def drafter_append(desc: Drafter, layer: int, cfg: QCfg, k: torch.Tensor, v: torch.Tensor,
+                   start: torch.Tensor, budget: torch.Tensor, count: Optional[torch.Tensor] = None) -> None:
+    _need(k, "k", ndim=4)
+    _need(v, "v", ndim=4)
+    _need(start, "start", torch.int32)
+    _need(budget, "budget", torch.int32)
+    b, T, H, D = k.shape
+    if b != desc.batch or H != desc.n_kv_heads or D != desc.head_dim:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match the mirror")
+    check(lib().dkv_drafter_append(C.byref(desc), layer, cfg, k.data_ptr(), v.data_ptr(), _dt(k), T,
+                                   start.data_ptr(), _ptr(count), budget.data_ptr(), _stream()),
+          "dkv_drafter_append")
+
+
+def drafter_truncate(desc: Drafter, cfgs: Sequence[QCfg], start: torch.Tensor) -> None:
+    _need(start, "start", torch.int32)
+    check(lib().dkv_drafter_truncate(C.byref(desc), _qarr(cfgs), start.data_ptr(), _stream()),
+          "dkv_drafter_truncate")
+
+
+def drafter_sync(desc: Drafter, full: Paged, cfgs: Sequence[QCfg], start: torch.Tensor, end: torch.Tensor,
+                 budget: torch.Tensor) -> None:
+    for t, n in ((start, "start"), (end, "end"), (budget, "budget")):
+        _need(t, n, torch.int32)
+    check(lib().dkv_drafter_sync(C.byref(desc), C.byref(full), _qarr(cfgs), start.data_ptr(), end.data_ptr(),
+                                 budget.data_ptr(), _stream()), "dkv_drafter_sync")
+
+
+def drafter_rebuild(desc: Drafter, full: Paged, layers: Sequence[int], cfgs: Sequence[QCfg],
+                    length: torch.Tensor, budget: torch.Tensor) -> None:
+    _need(length, "length", torch.int32)
+    _need(budget, "budget", torch.int32)
+    la = (C.c_int32 * max(1, len(layers)))(*layers)
+    check(lib().dkv_drafter_rebuild(C.byref(desc), C.byref(full), la, len(layers), _qarr(cfgs),
+                                    length.data_ptr(), budget.data_ptr(), _stream()), "dkv_drafter_rebuild")
+
+
+def drafter_attention(desc: Drafter, layer: int, cfg: QCfg, q: torch.Tensor, want_mass: bool,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _need(q, "q", torch.float32, 3)
+    b, Hq, D = q.shape
+    if b != desc.batch or D != desc.head_dim:
+        raise ValueError(f"q shape {tuple(q.shape)} does not match the mirror")
+    if out is None:
+        out = torch.empty_like(q)
+    nbytes = lib().dkv_drafter_attention_workspace(C.byref(desc), Hq, int(want_mass))
+    ws = _WS.get(q.device, nbytes)
+    check(lib().dkv_drafter_attention(C.byref(desc), layer, cfg, q.data_ptr(), Hq, int(want_mass), out.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), _stream()), "dkv_drafter_attention")
+    return out
+
+
+def drafter_gather(desc: Drafter, seq: int, layer: int, cfg: QCfg, rows: int, device) -> dict:
+    H, D = desc.n_kv_heads, desc.head_dim
+    ng = 0 if cfg.bits >= 16 else -(-D // cfg.group)
+    o = {}
+    for kv in ("k", "v"):
+        o[kv + "_codes"] = torch.empty((rows, H, D), dtype=torch.uint8, device=device)
+        o[kv + "_scale"] = torch.empty((rows, H, max(ng, 1)), dtype=torch.float32, device=device)
+        o[kv + "_lo"] = torch.empty((rows, H, max(ng, 1)), dtype=torch.float32, device=device)
+        o[kv + "_deq"] = torch.empty((rows, H, D), dtype=torch.float32, device=device)
+    o["pos"] = torch.empty((rows,), dtype=torch.int32, device=device)
+    check(lib().dkv_drafter_gather(C.byref(desc), seq, layer, cfg, rows,
+                                   *(o[k].data_ptr() for k in ("k_codes", "k_scale", "k_lo", "k_deq",
+                                                               "v_codes", "v_scale", "v_lo", "v_deq", "pos")),
+                                   _stream()), "dkv_drafter_gather")
+    return o
+
+
+# ------------------------------------------------------------------ (a10, a11)
+def sample(logits: torch.Tensor, temperature: float, u: torch.Tensor,
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _need(logits, "logits", torch.float32, 2)
+    _need(u, "u", torch.float64)
+    b, V = logits.shape
+    if out is None:
+        out = torch.empty(b, dtype=torch.int32, device=logits.device)
+    ws = _WS.get(logits.device, lib().dkv_sample_workspace(b, V))
+    check(lib().dkv_sample(logits.data_ptr(), V, b, V, float(temperature), u.data_ptr(), out.data_ptr(),
+                           ws.data_ptr(), ws.numel(), _stream()), "dkv_sample")
+    return out
+
+
+def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: torch.Tensor,
+           temperature: float, u: torch.Tensor):
+    """Returns (accepted, next_token, n_uniforms) int32 [batch] device tensors."""
+    _need(target, "target", torch.float32, 3)
+    _need(draft_tokens, "draft_tokens", torch.int32, 2)
+    _need(u, "u", torch.float64, 2)
+    b, g1, V = target.shape
+    gamma = g1 - 1
+    if draft_tokens.shape != (b, gamma) or u.shape != (b, g1):
+        raise ValueError("draft_tokens must be [batch, gamma] and u [batch, gamma+1]")
+    if temperature > 0.0 and gamma > 0:
+        if draft is None:
+            raise ValueError("draft logits are needed when temperature > 0")
+        _need(draft, "draft", torch.float32, 3)
+        if draft.shape != (b, gamma, V):
+            raise ValueError("draft must be [batch, gamma, vocab]")
+    res = torch.empty((3, b), dtype=torch.int32, device=target.device)
+    ws = _WS.get(target.device, lib().dkv_accept_workspace(b, gamma, V))
+    check(lib().dkv_accept(target.data_ptr(), _ptr(draft), draft_tokens.data_ptr(), b, gamma, V,
+                           float(temperature), u.data_ptr(), res[0].data_ptr(), res[1].data_ptr(),
+                           res[2].data_ptr(), ws.data_ptr(), ws.numel(), _stream()), "dkv_accept")
+    return res[0], res[1], res[2]

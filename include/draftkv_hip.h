@@ -1,0 +1,207 @@
+/*
+ * draftkv_hip.h -- C ABI of the MI355X (gfx950) DRAFTKV decode-round library.
+ *
+ * The reference (aabhimittal/Draft-KV) is pure Python/numpy and has no FFI;
+ * its drop-in boundary is the duck-typed cache protocol the models call
+ * (append / read / note_attention / truncate, plus the mirror's sync_from /
+ * rebuild_layers) and the engine's sampling/accept code. Each entry point
+ * below replaces one piece of that protocol; the comment names the reference
+ * file:line it stands in for. A Python host (draft-kv_amd/draftkv/_lib.py)
+ * binds these with ctypes; INTEGRATION.md shows the binding.
+ *
+ * Conventions
+ *   - All pointers are device pointers unless stated otherwise; the caller
+ *     owns every buffer (the library allocates nothing).
+ *   - Every function is stream-ordered on `stream` and returns 0 on success
+ *     or a negative DKV_E* code; dkv_last_error() then describes the failure
+ *     (thread-local). Sizes are validated on the host before any launch.
+ *   - Positions are absolute token indices. A sequence's full cache always
+ *     holds positions 0..len-1 (the engine never appends out of order).
+ */
+#ifndef DRAFTKV_HIP_H
+#define DRAFTKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* dkv_stream_t; /* a hipStream_t; NULL = default stream */
+
+enum { DKV_OK = 0, DKV_EINVAL = -1, DKV_ELAUNCH = -2, DKV_EWORKSPACE = -3, DKV_ECAPACITY = -4 };
+enum { DKV_F32 = 0, DKV_BF16 = 1 };
+
+/* Paged full (authoritative) cache -- reference draftkv/paged.py:76-176.
+ * pool: n_blocks physical blocks; block b holds one layer's K and V for
+ * block_size consecutive positions of one sequence:
+ *     K part: [n_kv_heads][block_size][head_dim]
+ *     V part: [n_kv_heads][head_dim][block_size]   (transposed)
+ * elements DKV_F32 or DKV_BF16. block_table: int32 [batch][n_layers][max_blocks]
+ * physical block ids (host-managed LIFO pools, paged.py:33-73). */
+typedef struct {
+    void* pool;
+    const int32_t* block_table;
+    int32_t batch, n_layers, n_kv_heads, head_dim, block_size, max_blocks, dtype;
+} dkv_paged_t;
+
+/* Compressed drafter mirror -- reference draftkv/compress.py:95-241.
+ * Per (seq, layer, kv_head) a dense segment of `cap` row slots; rows
+ * 0..n_rows-1 are live (eviction and truncation compact it). Row r of the
+ * segment lives at   seg_base + r * row_bytes(layer cfg)   where
+ *     seg_base = ((seq*n_layers + layer)*n_kv_heads + head) * cap * code_stride
+ * (codes) and likewise with meta_stride for (scale, lo) pairs.
+ * Codes: bits<=4 -> two 4-bit codes per byte (element 2i in the low nibble);
+ * bits==8 -> one byte; bits==16 -> raw float32 values (the reference keeps an
+ * fp32 copy, compress.py:28-29). Meta: per group (scale, lo) as float32 pairs,
+ * or float16 pairs when meta_f16. pos/score/n_rows are per (seq, layer). */
+typedef struct {
+    void* kc; void* vc;          /* codes */
+    void* km; void* vm;          /* per-group (scale, lo) */
+    int32_t* pos;                /* [batch][n_layers][cap] absolute positions */
+    double* score;               /* [batch][n_layers][cap] accumulated attention mass */
+    int32_t* n_rows;             /* [batch][n_layers] live rows */
+    int32_t batch, n_layers, n_kv_heads, head_dim, cap;
+    int64_t code_stride, meta_stride;   /* bytes reserved per row slot */
+} dkv_drafter_t;
+
+/* One layer's compression arm -- reference draftkv/config.py:9-33 plus the
+ * `group` / fp16-meta extension. */
+typedef struct {
+    int32_t bits, group, meta_f16, sink, recent;
+} dkv_qcfg_t;
+
+/* ---------------------------------------------------------------- (a1) */
+/* Group quantizer on contiguous float32 rows x[rows][d] -- replaces
+ * draftkv/compress.py:21-46 (`quantize`). Writes codes u8 [rows][d],
+ * scale/lo f32 [rows][ceil(d/group)], deq f32 [rows][d] (any output may be
+ * NULL). Bit-exact with the reference's float32 op order. */
+int dkv_quantize(const float* x, int64_t rows, int32_t d, int32_t bits, int32_t group,
+                 int32_t meta_f16, uint8_t* codes, float* scale, float* lo, float* deq,
+                 dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a7) */
+/* Write K/V rows into the paged full cache -- replaces
+ * draftkv/paged.py:120-128 (`PagedKVCache.append`). k, v: [batch][T][Hkv][D]
+ * (in_dtype). Sequence s writes rows t < count[s] at positions start[s]+t;
+ * blocks must already be in block_table (the host allocates them,
+ * paged.py:112-117). count may be NULL (= T for all). */
+int dkv_paged_append(const dkv_paged_t* cache, int32_t layer, const void* k, const void* v,
+                     int32_t in_dtype, int32_t T, const int32_t* start, const int32_t* count,
+                     dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a8) */
+/* Causal attention of T query rows per sequence over the paged full cache
+ * (verify pass, baseline decode, prefill) -- replaces the read + einsum +
+ * softmax of draftkv/llama.py:202-218 / gpt2.py:197-206 / model.py:117-127
+ * against FullKVCache/PagedKVCache. q: f32 [batch][T][Hq][D]; query t of
+ * sequence s sits at position start[s]+t and sees positions <= its own.
+ * out: f32 [batch][T][Hq][D]. Keys are split in fixed chunks of
+ * chunk_keys absolute positions and merged in chunk order, so a query's
+ * result does not depend on T or on the cache length (batch invariance).
+ * work: dkv_paged_attention_workspace() bytes. */
+size_t dkv_paged_attention_workspace(const dkv_paged_t* cache, int32_t T, int32_t n_q_heads,
+                                     int32_t max_len, int32_t chunk_keys);
+int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, const float* q, int32_t T,
+                        int32_t n_q_heads, const int32_t* start, int32_t max_len,
+                        int32_t chunk_keys, float* out, void* work, size_t work_bytes,
+                        dkv_stream_t stream);
+
+/* ------------------------------------------------------------ (a1,a3,a4) */
+/* Quantize and append T rows per sequence to one layer of the mirror, then
+ * evict down to budget[s] -- replaces draftkv/compress.py:122-133 (`append`)
+ * with :154-179 (`budget`, `_evict`). k, v: [batch][T][Hkv][D] (in_dtype);
+ * row t < count[s] of sequence s has position start[s]+t. The victims are
+ * the lowest (score, position) rows outside the `sink` lowest and `recent`
+ * highest live positions (recent == 0 protects every row). count may be
+ * NULL. */
+int dkv_drafter_append(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t cfg,
+                       const void* k, const void* v, int32_t in_dtype, int32_t T,
+                       const int32_t* start, const int32_t* count, const int32_t* budget,
+                       dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a9) */
+/* Drop every row at position >= start[s] in all layers -- replaces
+ * draftkv/compress.py:181-188 (`truncate`). cfgs: host array of n_layers
+ * arms (the row width of each layer). */
+int dkv_drafter_truncate(const dkv_drafter_t* mirror, const dkv_qcfg_t* cfgs, const int32_t* start,
+                         dkv_stream_t stream);
+
+/* Per-round resync: truncate each layer to start[s], then quantize the full
+ * cache's rows start[s]..end[s]-1 into it and evict to budget[layer*batch+s]
+ * -- replaces draftkv/compress.py:190-207 (`sync_from`). cfgs: host array of
+ * n_layers arms. */
+int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* full, const dkv_qcfg_t* cfgs,
+                     const int32_t* start, const int32_t* end, const int32_t* budget,
+                     dkv_stream_t stream);
+
+/* --------------------------------------------------------------- (c/a9) */
+/* Requantize the listed layers from the full cache under new arms -- replaces
+ * draftkv/compress.py:209-230 (`rebuild_layers`) and the first build
+ * `sync_from(full, 0)`. All scores restart at 0, so the survivors are the
+ * closed form [0, sink) u [n - (B - sink), n) (n = len[s], B = budget
+ * [layer*batch+s]); only those rows are read and quantized, written densely
+ * in position order. layers/cfgs are host arrays (cfgs indexed by layer). */
+int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_t* full,
+                        const int32_t* layers, int32_t n_changed, const dkv_qcfg_t* cfgs,
+                        const int32_t* len, const int32_t* budget, dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a5,a6) */
+/* Drafter attention: one query position per sequence over the live rows of
+ * one mirror layer, dequantizing in registers -- replaces the read + einsum
+ * + softmax + note_attention of the model forwards against CompressedKVCache
+ * (compress.py:135-151; llama.py:202-218). q: f32 [batch][Hq][D] (GQA groups
+ * of Hq/Hkv query heads share a KV head); out: f32 [batch][Hq][D]. When
+ * want_mass, each live row's score gains the float32 sum over query heads of
+ * its attention probability (compress.py:144-151; llama.py:213-214).
+ * work: dkv_drafter_attention_workspace() bytes. */
+size_t dkv_drafter_attention_workspace(const dkv_drafter_t* mirror, int32_t n_q_heads,
+                                       int32_t want_mass);
+int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t cfg,
+                          const float* q, int32_t n_q_heads, int32_t want_mass, float* out,
+                          void* work, size_t work_bytes, dkv_stream_t stream);
+
+/* Unpack one layer of one sequence to plain arrays (debug/parity `read`,
+ * compress.py:135-142): codes u8 [rows][Hkv][D], scale/lo f32
+ * [rows][Hkv][groups], deq f32 [rows][Hkv][D] for K and V, pos int32 [rows].
+ * Rows are in storage order; `rows` must equal the layer's live row count.
+ * Any output may be NULL. */
+int dkv_drafter_gather(const dkv_drafter_t* mirror, int32_t seq, int32_t layer, dkv_qcfg_t cfg,
+                       int32_t rows, uint8_t* k_codes, float* k_scale, float* k_lo, float* k_deq,
+                       uint8_t* v_codes, float* v_scale, float* v_lo, float* v_deq,
+                       int32_t* pos, dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a10) */
+/* One draw per row from softmax(logits/T) -- replaces draftkv/engine.py:36-41
+ * (`_probs`) + :101-106 (`_sample`). logits f32 rows of length vocab at
+ * row_stride; u: f64 uniforms [batch]. T <= 0: first argmax (u unused).
+ * tokens: int32 [batch]. work: dkv_sample_workspace() bytes. */
+size_t dkv_sample_workspace(int32_t batch, int32_t vocab);
+int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t vocab,
+               float temperature, const double* u, int32_t* tokens, void* work,
+               size_t work_bytes, dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- (a11) */
+/* Verify decision of one round for every sequence -- replaces
+ * draftkv/engine.py:188-213. target: f32 [batch][gamma+1][vocab];
+ * draft: f32 [batch][gamma][vocab] (the drafter's logits; unused when
+ * T <= 0); draft_tokens int32 [batch][gamma]; u: f64 [batch][gamma+1]
+ * uniforms in the order the reference draws them (one per tested position in
+ * sampling mode, then one for the bonus/residual token). Outputs int32
+ * [batch]: accepted, next_token, and n_uniforms (draws consumed).
+ * work: dkv_accept_workspace() bytes. */
+size_t dkv_accept_workspace(int32_t batch, int32_t gamma, int32_t vocab);
+int dkv_accept(const float* target, const float* draft, const int32_t* draft_tokens,
+               int32_t batch, int32_t gamma, int32_t vocab, float temperature, const double* u,
+               int32_t* accepted, int32_t* next_token, int32_t* n_uniforms, void* work,
+               size_t work_bytes, dkv_stream_t stream);
+
+/* ---------------------------------------------------------------- misc */
+const char* dkv_last_error(void);
+int32_t dkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DRAFTKV_HIP_H */

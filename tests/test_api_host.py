@@ -1,0 +1,100 @@
+"""Host-side API of the product package, on CPU: the cost model against the
+reference's published ceilings (README.md:82-86) and its own test
+expectations (tests/test_math.py, tests/test_llama.py:98-132), the arm space,
+and the block pool's allocator semantics (paged.py:33-73)."""
+
+import numpy as np
+import pytest
+
+from draftkv import (BlockPool, BlockPoolExhausted, CompressionConfig, CostModel, LayerPlan, best_gamma,
+                     default_arms, expected_tokens, plan_blocks_needed)
+
+
+@pytest.mark.parametrize("batch,ctxs,want", [(1, (1024, 32768, 262144), (1.008, 1.222, 2.417)),
+                                             (32, (1024, 32768, 262144), (1.222, 4.342, 6.538))])
+def test_ceiling_reproduces_published_rows(batch, ctxs, want):
+    # README.md:82-85: 4b/keep0.5, HBM-resident cache, Llama-3-8B shape, 2 TB/s
+    cm = CostModel(batch=batch)
+    got = tuple(round(cm.ceiling(CompressionConfig(4, 0.5), c), 3) for c in ctxs)
+    assert got == want
+
+
+def test_offloaded_ceiling_row():
+    # README.md:86: full cache offloaded over PCIe5 (64 GB/s), 1 GB HBM budget
+    cm = CostModel(full_kv_bandwidth=6.4e10, hbm_kv_budget=1e9)
+    got = [round(cm.ceiling(CompressionConfig(4, 0.5), c), 2) for c in (1024, 32768, 262144)]
+    assert got == [1.26, 9.04, 7.97]
+
+
+def test_mi355x_target_ceilings():
+    cm = CostModel(bandwidth=8e12, batch=32)
+    assert cm.ceiling(CompressionConfig(4, 0.25), 32768) == pytest.approx(5.967, abs=1e-3)
+    assert cm.ceiling(CompressionConfig(8, 1.0), 32768) == pytest.approx(1.724, abs=1e-3)
+
+
+def test_expected_tokens_and_speedup_bound():          # reference tests/test_math.py:8-55
+    for g in (1, 4, 9):
+        assert expected_tokens(0.0, g) == pytest.approx(1.0)
+        assert expected_tokens(1.0, g) == pytest.approx(g + 1)
+    for a in (0.5, 0.8, 0.95):
+        assert expected_tokens(a, 1000) == pytest.approx(1 / (1 - a), rel=1e-6)
+    cm = CostModel(full_kv_bandwidth=6.4e10, hbm_kv_budget=1e9)
+    for ctx in (512, 8192, 131072):
+        for cfg in (CompressionConfig(16, 1.0), CompressionConfig(4, 0.5), CompressionConfig(2, 0.25)):
+            ceil = cm.ceiling(cfg, ctx)
+            assert all(cm.speedup(cfg, g, 0.999, ctx) <= ceil + 1e-9 for g in range(1, 32))
+    gs = [best_gamma(cm, CompressionConfig(4, 0.5), a, 32768, 16)[0] for a in (0.1, 0.3, 0.5, 0.7, 0.9, 0.99)]
+    assert gs == sorted(gs)
+    assert CostModel().ceiling(CompressionConfig(2, 0.25), 512) < 1.02
+
+
+def test_gqa_breakeven_scales_with_ratio():            # reference tests/test_llama.py:98-122
+    cfg = CompressionConfig(4, 0.5)
+    base = dict(n_layers=32, d_head=128, weight_bytes=16e9, bandwidth=2.0e12)
+
+    def breakeven(n_kv, target=1.5):
+        cm = CostModel(n_kv_heads=n_kv, **base)
+        lo, hi = 128, 8_000_000
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if cm.ceiling(cfg, mid) >= target:
+                hi = mid
+            else:
+                lo = mid + 1
+        return lo
+
+    mha, gqa4, gqa8 = breakeven(32), breakeven(8), breakeven(4)
+    assert gqa4 / mha == pytest.approx(4.0, rel=0.1) and gqa8 / mha == pytest.approx(8.0, rel=0.1)
+
+
+def test_config_validation_and_arms():
+    with pytest.raises(ValueError):
+        CompressionConfig(5, 1.0)
+    with pytest.raises(ValueError):
+        CompressionConfig(4, 0.0)
+    arms = default_arms()
+    assert len(arms) == 15 and arms == sorted(arms)
+    sizes = [CompressionConfig(b, 1.0).bytes_per_entry(128) for b in (2, 3, 4, 8, 16)]
+    assert sizes == sorted(sizes) and sizes[-1] == 256
+    plan = LayerPlan.uniform(CompressionConfig(4, 0.25), 32)
+    cm = CostModel()
+    assert cm.draft_kv_bytes(plan, 32768) == pytest.approx(cm.draft_kv_bytes(CompressionConfig(4, 0.25), 32768))
+
+
+def test_block_pool_semantics():
+    pool = BlockPool(8, 16)
+    got = [pool.allocate() for _ in range(5)]
+    assert got == [7, 6, 5, 4, 3]
+    pool.free(5)
+    assert pool.allocate() == 5
+    for b in got:
+        pool.free(b)
+    pool.check_invariants()
+    p2 = BlockPool(2, 16)
+    a, b = p2.allocate(), p2.allocate()
+    with pytest.raises(BlockPoolExhausted):
+        p2.allocate()
+    p2.free(a)
+    with pytest.raises(RuntimeError, match="double free"):
+        p2.free(a)
+    assert plan_blocks_needed(33, 3, 16) == 9

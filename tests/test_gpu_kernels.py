@@ -1,0 +1,314 @@
+"""HIP kernels against the oracle, through the C ABI (via draftkv.ops and the
+device caches). Integer/byte/index results are compared bit for bit; float
+attention within 2e-3 relative / 1e-3 absolute of the float32 numpy oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import caches as oc
+from oracle.attention import attend, row_mass
+from oracle.config import Cfg
+from oracle.quant import quantize_codes
+from oracle.sampling import accept as o_accept
+from oracle.sampling import probs as o_probs
+from oracle.sampling import sample_u
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 2e-3, 1e-3
+
+
+def _dk():
+    import draftkv
+    from draftkv import ops
+    return draftkv, ops
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).bfloat16().float().numpy()
+
+
+# ------------------------------------------------------------------ (a1)
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("d,group", [(16, 64), (64, 64), (128, 32), (80, 64), (40, 32), (128, 128)])
+@pytest.mark.parametrize("meta", ["f32", "f16"])
+def test_quantize_bit_exact(dev, bits, d, group, meta):
+    _, ops = _dk()
+    rng = np.random.default_rng(bits * 1000 + d + group)
+    x = rng.standard_normal((37, 3, d)).astype(np.float32)
+    x[:, :, rng.integers(0, d, max(1, d // 100))] *= 8.0           # outlier channels
+    x[0, 0, :] = 1.25                                               # a constant row
+    x[1, 1, :] = 0.0
+    codes, scale, lo, deq = ops.quantize_codes(torch.from_numpy(x).to(dev), bits, group, meta == "f16")
+    oc_, os_, ol_, od_ = quantize_codes(x, bits, group, meta)
+    assert np.array_equal(codes.cpu().numpy(), oc_)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(lo.cpu().numpy().view(np.uint32), ol_.view(np.uint32))
+    assert np.array_equal(deq.cpu().numpy().view(np.uint32), od_.view(np.uint32))
+
+
+def test_quantize_api_numpy_roundtrip(dev):
+    draftkv, _ = _dk()
+    from oracle.quant import quantize as oq
+    x = np.random.default_rng(3).standard_normal((16, 8, 64)).astype(np.float32)
+    for b in (2, 3, 4, 8, 16):
+        assert np.array_equal(draftkv.quantize(x, b), oq(x, b))
+
+
+# ------------------------------------------------------------------ (a7)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("block_size", [1, 4, 16, 64])
+def test_paged_tables_and_rows_match_reference(dev, dtype, block_size):
+    draftkv, _ = _dk()
+    L, H, D = 3, 4, 16
+    rng = np.random.default_rng(block_size)
+    ref = oc.PagedKVCache(L, H, D, block_size, 512)
+    pc = draftkv.PagedKVCache(L, H, D, block_size, 512, dtype="bf16" if dtype == "bf16" else np.float32)
+    n = 0
+    for T in (33, 1, 5, 1, 17):
+        for layer in range(L):
+            k = rng.standard_normal((T, H, D)).astype(np.float32)
+            v = rng.standard_normal((T, H, D)).astype(np.float32)
+            if dtype == "bf16":
+                k, v = _bf16(k), _bf16(v)
+            pos = np.arange(n, n + T)
+            ref.append(layer, k, v, pos)
+            pc.append(layer, k, v, pos)
+        n += T
+        if T == 1:
+            ref.truncate(n - 1)
+            pc.truncate(n - 1)
+            n -= 1
+    assert pc.block_table == ref.block_table
+    assert pc.blocks_in_use == ref.blocks_in_use
+    assert pc.fragmentation() == pytest.approx(ref.fragmentation())
+    pc.pool.check_invariants()
+    for layer in range(L):
+        for a, b in zip(pc.read(layer), ref.read(layer)):
+            assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------------------ (a8)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (8, 2, 64), (32, 8, 128), (9, 3, 64)])
+@pytest.mark.parametrize("chunk", [32, 64, 512])
+def test_paged_attention_matches_oracle(dev, dtype, Hq, Hkv, D, chunk):
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(Hq + D + chunk)
+    b, n, T = 3, 150, 5
+    pc = draftkv.PagedKVCache(1, Hkv, D, 16, 64, dtype="bf16" if dtype == "bf16" else np.float32, batch=b,
+                              chunk_keys=chunk)
+    k = rng.standard_normal((b, n + T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((b, n + T, Hkv, D)).astype(np.float32)
+    if dtype == "bf16":
+        k, v = _bf16(k), _bf16(v)
+    # ragged: sequence s holds n - 7*s positions before the T queries
+    starts = [n - 7 * s for s in range(b)]
+    pc.reserve([n + T] * b)
+    st0 = torch.zeros(b, dtype=torch.int32, device=dev)
+    kk = np.zeros_like(k)
+    vv = np.zeros_like(v)
+    for s in range(b):
+        m = starts[s] + T
+        kk[s, :m], vv[s, :m] = k[s, :m], v[s, :m]
+    pc.append_layer(0, torch.from_numpy(kk).to(dev), torch.from_numpy(vv).to(dev), st0,
+                    torch.tensor([starts[s] + T for s in range(b)], dtype=torch.int32, device=dev))
+    q = rng.standard_normal((b, T, Hq, D)).astype(np.float32)
+    st = torch.tensor(starts, dtype=torch.int32, device=dev)
+    out = pc.attend(0, torch.from_numpy(q).to(dev), st, max_len=n + T).cpu().numpy()
+    for s in range(b):
+        m = starts[s] + T
+        ref, _, _ = attend(q[s], kk[s, :m], vv[s, :m], np.arange(m), np.arange(starts[s], m), Hq // Hkv)
+        np.testing.assert_allclose(out[s], ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_verify_is_batch_invariant_with_decode(dev, dtype):
+    """A verify pass over gamma+1 queries gives each row the bit pattern the
+    one-token decode step at that position gives (the losslessness contract)."""
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(7)
+    b, Hq, Hkv, D, n, g = 2, 8, 2, 64, 700, 8
+    pc = draftkv.PagedKVCache(1, Hkv, D, 16, 128, dtype="bf16" if dtype == "bf16" else np.float32, batch=b,
+                              chunk_keys=256)
+    k = rng.standard_normal((b, n + g, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((b, n + g, Hkv, D)).astype(np.float32)
+    pc.reserve([n + g] * b)
+    pc.append_layer(0, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                    torch.zeros(b, dtype=torch.int32, device=dev))
+    q = torch.from_numpy(rng.standard_normal((b, g + 1, Hq, D)).astype(np.float32)).to(dev)
+    start = torch.full((b,), n - 1, dtype=torch.int32, device=dev)
+    ver = pc.attend(0, q, start, max_len=n + g)
+    for t in range(g + 1):
+        one = pc.attend(0, q[:, t:t + 1].contiguous(), start + t, max_len=n + g)
+        assert torch.equal(one[:, 0], ver[:, t]), t
+
+
+# ------------------------------------------------------------------ mirror (a3, a4, a9, c)
+def _full_pair(L, H, D, n, rng, dev, dtype=np.float32):
+    """An oracle FullKVCache and a device PagedKVCache holding the same rows."""
+    import draftkv
+    full_o = oc.FullKVCache(L)
+    full_d = draftkv.PagedKVCache(L, H, D, 16, 4096, dtype=dtype, max_tokens=8192)
+    ks = [rng.standard_normal((n, H, D)).astype(np.float32) for _ in range(L)]
+    vs = [rng.standard_normal((n, H, D)).astype(np.float32) for _ in range(L)]
+    for layer in range(L):
+        full_o.append(layer, ks[layer], vs[layer], np.arange(n))
+        full_d.append(layer, ks[layer], vs[layer], np.arange(n))
+    return full_o, full_d, ks, vs
+
+
+def _same_mirror(mo, md, L, codes=True):
+    for layer in range(L):
+        g = md.read_codes(layer)
+        assert g["pos"].tolist() == mo.pos[layer].tolist(), layer
+        if codes and mo.kq[layer] is not None:
+            assert np.array_equal(g["k_codes"], mo.kq[layer][0])
+            assert np.array_equal(g["v_codes"], mo.vq[layer][0])
+            assert np.array_equal(g["k_scale"], mo.kq[layer][1])
+            assert np.array_equal(g["v_lo"], mo.vq[layer][2])
+        k, v, p = md.read(layer)
+        ko, vo, po = mo.read(layer)
+        assert np.array_equal(k, ko) and np.array_equal(v, vo)
+
+
+ARMS = [Cfg(8, 1.0), Cfg(4, 0.5), Cfg(4, 0.25, group=32, meta="f16"), Cfg(2, 0.25), Cfg(3, 0.5, 2, 5),
+        Cfg(16, 0.5), Cfg(4, 0.3, 4, 0)]
+
+
+def _dcfg(c: Cfg):
+    from draftkv import CompressionConfig
+    return CompressionConfig(c.bits, c.keep_frac, c.sink, c.recent, c.group, c.meta == "f16")
+
+
+@pytest.mark.parametrize("arm", ARMS, ids=lambda c: f"{c.bits}b{c.keep_frac}g{c.group}{c.meta}s{c.sink}r{c.recent}")
+def test_build_and_rebuild_match_reference(dev, arm):
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(arm.bits)
+    L, H, D, n = 3, 2, 64, 300
+    full_o, full_d, _, _ = _full_pair(L, H, D, n, rng, dev)
+    mo = oc.CompressedKVCache(L, [Cfg(8, 1.0)] * L)
+    md = draftkv.CompressedKVCache(L, [_dcfg(Cfg(8, 1.0))] * L)
+    assert md.sync_from(full_d, 0) == mo.sync_from(full_o, 0)
+    _same_mirror(mo, md, L)
+    cfgs_o = [Cfg(8, 1.0)] * L
+    cfgs_o[1] = arm
+    assert md.rebuild_layers(full_d, [1], [_dcfg(c) for c in cfgs_o]) == mo.rebuild_layers(full_o, [1], cfgs_o)
+    _same_mirror(mo, md, L)
+
+
+@pytest.mark.parametrize("arm", ARMS, ids=lambda c: f"{c.bits}b{c.keep_frac}g{c.group}{c.meta}s{c.sink}r{c.recent}")
+def test_steady_state_eviction_truncate_and_resync(dev, arm):
+    """Drafting appends one row at a time with accumulated scores; the
+    victims, the compaction, truncation and the per-round resync must leave
+    the same rows (positions, codes, scores) as the reference."""
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(11 + arm.bits)
+    L, H, D, n = 2, 2, 32, 120
+    full_o, full_d, _, _ = _full_pair(L, H, D, n, rng, dev)
+    mo = oc.CompressedKVCache(L, [arm] * L)
+    md = draftkv.CompressedKVCache(L, [_dcfg(arm)] * L)
+    mo.sync_from(full_o, 0)
+    md.sync_from(full_d, 0)
+    _same_mirror(mo, md, L)
+    pos = n
+    for rnd in range(6):
+        for step in range(5):
+            # identical scores on both sides (distinct values, plus a tie)
+            for layer in range(L):
+                nr = mo.pos[layer].size
+                sc = np.round(rng.random(nr) * 4, 1)
+                mo.score[layer][:] = sc
+                dpos = md.pos[0, layer, :nr].cpu().numpy()
+                # device rows are in storage order: map by position
+                lut = {int(p): float(s) for p, s in zip(mo.pos[layer], sc)}
+                md.score[0, layer, :nr] = torch.tensor([lut[int(p)] for p in dpos], dtype=torch.float64,
+                                                       device=dev)
+            for layer in range(L):
+                k = rng.standard_normal((1, H, D)).astype(np.float32)
+                v = rng.standard_normal((1, H, D)).astype(np.float32)
+                mo.append(layer, k, v, [pos])
+                md.append(layer, k, v, [pos])
+            pos += 1
+            _same_mirror(mo, md, L)
+        # rollback: 2 of the 5 drafted positions accepted; the full cache gets
+        # the 3 true rows (2 accepted + the next one) and the mirror resyncs
+        # from the last committed position
+        full_o.truncate(pos - 5)
+        full_d.truncate(pos - 5)
+        for layer in range(L):
+            k = rng.standard_normal((3, H, D)).astype(np.float32)
+            v = rng.standard_normal((3, H, D)).astype(np.float32)
+            full_o.append(layer, k, v, np.arange(pos - 5, pos - 2))
+            full_d.append(layer, k, v, np.arange(pos - 5, pos - 2))
+        start = pos - 6
+        assert md.sync_from(full_d, start) == mo.sync_from(full_o, start)
+        pos = pos - 2
+        _same_mirror(mo, md, L)
+        assert md.seen_positions == mo.seen_positions
+
+
+# ------------------------------------------------------------------ (a5, a6)
+@pytest.mark.parametrize("arm", [Cfg(8, 1.0), Cfg(4, 0.25, group=32, meta="f16"), Cfg(16, 0.5), Cfg(2, 0.5)],
+                         ids=lambda c: f"{c.bits}b{c.keep_frac}")
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (32, 8, 128), (9, 3, 64)])
+def test_drafter_attention_and_mass(dev, arm, Hq, Hkv, D):
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(Hq * D + arm.bits)
+    L, n = 1, 1500
+    full_o, full_d, _, _ = _full_pair(L, Hkv, D, n, rng, dev)
+    mo = oc.CompressedKVCache(L, [arm])
+    md = draftkv.CompressedKVCache(L, [_dcfg(arm)])
+    mo.sync_from(full_o, 0)
+    md.sync_from(full_d, 0)
+    q = rng.standard_normal((1, Hq, D)).astype(np.float32) * 2.0
+    nr = mo.pos[0].size
+    before = md.read_codes(0)["score"].copy()
+    out = md.attend(0, torch.from_numpy(q).to(dev), want_mass=True).cpu().numpy()
+    ck, cv, cpos = mo.read(0)
+    ref, _, mp = attend(q, ck, cv, cpos, np.array([n - 1]), Hq // Hkv)
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    mass = md.read_codes(0)["score"] - before
+    np.testing.assert_allclose(mass, row_mass(mp).astype(np.float64), rtol=1e-4, atol=1e-7)
+    assert mass.shape == (nr,)
+
+
+# ------------------------------------------------------------------ (a10, a11)
+@pytest.mark.parametrize("V", [128, 50257, 128256])
+@pytest.mark.parametrize("T", [0.0, 0.8, 1.0])
+def test_sample_matches_numpy_choice(dev, V, T):
+    _, ops = _dk()
+    rng = np.random.default_rng(V)
+    b = 6
+    logits = (rng.standard_normal((b, V)) * 3).astype(np.float32)
+    logits[1, 7] = logits[1].max() + 0.0          # tie for argmax -> first index
+    logits[1, 3] = logits[1, 7]
+    u = rng.random(b)
+    tok = ops.sample(torch.from_numpy(logits).to(dev), T, torch.from_numpy(u).to(dev)).cpu().numpy()
+    for s in range(b):
+        assert tok[s] == sample_u(o_probs(logits[s], T), u[s]), s
+
+
+@pytest.mark.parametrize("T", [0.0, 0.8])
+@pytest.mark.parametrize("gamma", [1, 4, 8])
+def test_accept_matches_reference_rule(dev, T, gamma):
+    _, ops = _dk()
+    rng = np.random.default_rng(gamma * 10 + int(T * 10))
+    b, V = 16, 5000
+    base = rng.standard_normal((b, 1, V)).astype(np.float32) * 2
+    target = (base + 0.3 * rng.standard_normal((b, gamma + 1, V))).astype(np.float32)
+    draft = (base[:, :1] + 0.3 * rng.standard_normal((b, gamma, V))).astype(np.float32)
+    toks = np.zeros((b, gamma), np.int32)
+    for s in range(b):
+        for i in range(gamma):
+            # mostly the target argmax so long runs get accepted, sometimes not
+            toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.8 else int(rng.integers(V))
+    u = rng.random((b, gamma + 1))
+    acc, nxt, used = ops.accept(torch.from_numpy(target).to(dev), torch.from_numpy(draft).to(dev),
+                                torch.from_numpy(toks).to(dev), T, torch.from_numpy(u).to(dev))
+    acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
+    for s in range(b):
+        qs = [o_probs(draft[s, i], T) for i in range(gamma)]
+        ra, rn, ru = o_accept(target[s], toks[s].tolist(), qs, T, u[s])
+        assert (acc[s], nxt[s], used[s]) == (ra, rn, ru), s
