@@ -1,6 +1,8 @@
 // (a7) paged full-cache append and (a8) causal attention over it.
 // Reference: draftkv/paged.py:76-176 (cache), draftkv/llama.py:202-218 and
 // gpt2.py/model.py equivalents (read + masked softmax attention).
+#include <algorithm>
+
 #include "dkv_common.h"
 
 namespace dkv {
@@ -186,6 +188,185 @@ __global__ void __launch_bounds__(256) paged_attn_kernel(dkv_paged_t c, int laye
     }
 }
 
+// ---------------------------------------------------------------- MFMA path
+// bf16 cache with 16-token blocks. One wave owns 16 query rows (a "q-tile")
+// and walks its block's key chunk 32 keys (two blocks) at a time:
+//   S^T[16 keys][16 rows] = K[16 keys][D] . Q^T     (v_mfma_f32_16x16x32_bf16)
+//   O^T[16 d][16 rows]   += V^T[16 d][32 keys] . P^T
+// Q and P are split into bf16 hi + lo parts (two MFMAs each), which keeps the
+// products at ~16 mantissa bits against the exact bf16 K/V. In the S^T
+// accumulator a lane holds keys 4*(l/16)+r of one query row l%16; the PV
+// B operand wants 8 keys of one row per lane, so the k-slots of the PV
+// product are ordered {4j..4j+3, 16+4j..16+4j+3} (j = l/16) and the
+// probabilities never leave their lane. V is stored transposed per block, so
+// the matching V^T A operand is two 8-byte loads per lane.
+// Within the QK product lane group j owns d in [j*D/4, (j+1)*D/4): a lane
+// reads D/4 contiguous K elements of its key and the same slice of q.
+// Every per-row operation depends only on absolute key positions, so a
+// row's partial is identical for any T (batch invariance).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __bf16 to_bf16(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16_rne(f)); }
+__device__ __forceinline__ float from_bf16(__bf16 h) { return bf16_to_f32(__builtin_bit_cast(uint16_t, h)); }
+
+template <int D>
+__global__ void __launch_bounds__(256) paged_attn_mfma_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
+                                                              int T, int Hq, const int32_t* __restrict__ start,
+                                                              int CH, int n_chunks, int n_qtiles, float scale,
+                                                              float* __restrict__ part) {
+    constexpr int NSTEP = D / 32;      // k-steps of the QK product
+    constexpr int NDT = D / 16;        // d-tiles of the PV product
+    constexpr int DL = D / 4;          // d elements per lane group in QK
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int qb = blockIdx.x % ((n_qtiles + 3) / 4), chunk = blockIdx.x / ((n_qtiles + 3) / 4);
+    const int qtile = qb * 4 + wave;
+    if (qtile >= n_qtiles) return;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int G = Hq / c.n_kv_heads;
+    const int s0 = start[s];
+    const int len = s0 + T;
+    const int k_begin = chunk * CH;
+    if (k_begin >= len) return;
+    const int col = lane % 16, jj = lane / 16;
+    const int r0 = qtile * 16;
+    const int n_rows = T * G;
+    const int last_row = min(r0 + 15, n_rows - 1);
+    const int max_qpos = s0 + last_row / G;
+    if (k_begin > max_qpos) return;
+    const int k_end = min(min(k_begin + CH, len), max_qpos + 1);
+
+    // this lane's query row
+    const int r = r0 + col;
+    const bool rvalid = r < n_rows;
+    const int t = rvalid ? r / G : 0;
+    const int hq = h * G + (rvalid ? r % G : 0);
+    const int qpos = s0 + t;
+
+    bf16x8_t qhi[NSTEP], qlo[NSTEP];
+    {
+        const float* qr = q + (((int64_t)s * T + t) * Hq + hq) * D + DL * jj;
+#pragma unroll
+        for (int st = 0; st < NSTEP; ++st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = rvalid ? qr[8 * st + e] : 0.0f;
+                const __bf16 hi = to_bf16(v);
+                qhi[st][e] = hi;
+                qlo[st][e] = to_bf16(v - from_bf16(hi));
+            }
+    }
+    f32x4_t acc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const uint16_t* pool = static_cast<const uint16_t*>(c.pool);
+    const int64_t bel = paged_block_elems(c);
+    const int64_t vbase = (int64_t)c.n_kv_heads * 16 * D;
+    const int32_t* btab = c.block_table + ((int64_t)s * c.n_layers + layer) * c.max_blocks;
+
+    for (int kb = k_begin; kb < k_end; kb += 32) {
+        const int32_t blk0 = btab[kb / 16];
+        const bool has1 = kb + 16 < len;
+        const int32_t blk1 = has1 ? btab[kb / 16 + 1] : blk0;
+        // ---- S^T for the two 16-key tiles
+        f32x4_t sacc[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int key = kb + 16 * a + col;
+            const int32_t blk = a ? blk1 : blk0;
+            const uint16_t* kr = pool + (int64_t)blk * bel + ((int64_t)h * 16 + col) * D + DL * jj;
+            const bool kvalid = key < len;
+            f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < NSTEP; ++st) {
+                bf16x8_t kv;
+                if (kvalid) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(kr + 8 * st);
+                    kv = __builtin_bit_cast(bf16x8_t, w);
+                } else {
+                    kv = bf16x8_t{};
+                }
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qhi[st], sa, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qlo[st], sa, 0, 0, 0);
+            }
+            sacc[a] = sa;
+        }
+        // ---- mask, scale, online softmax for this lane's row (keys 4jj+r, 16+4jj+r)
+        float p[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int key = kb + 16 * a + 4 * jj + rr;
+                const float sv = (rvalid && key <= qpos && key < len) ? sacc[a][rr] * scale : -INFINITY;
+                p[4 * a + rr] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p[i] = (p[i] == -INFINITY) ? 0.0f : __expf(p[i] - m_new);
+            sum += p[i];
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
+        l_run = l_run * alpha + sum;
+        m_run = m_new;
+        bf16x8_t phi, plo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const __bf16 hi = to_bf16(p[i]);
+            phi[i] = hi;
+            plo[i] = to_bf16(p[i] - from_bf16(hi));
+        }
+        // ---- O^T += V^T . P^T over the 32 keys
+        const uint16_t* v0 = pool + (int64_t)blk0 * bel + vbase + (int64_t)h * D * 16 + 4 * jj;
+        const uint16_t* v1 = pool + (int64_t)blk1 * bel + vbase + (int64_t)h * D * 16 + 4 * jj;
+        // 4 consecutive keys of V^T row d; keys at or past the cache end read as
+        // zero (their probability is 0, and 0 * garbage could be NaN)
+        auto ld4 = [&](const uint16_t* p, int first_key) -> uint2 {
+            const int nv = len - first_key;
+            if (nv <= 0) return uint2{0u, 0u};
+            uint2 w = *reinterpret_cast<const uint2*>(p);
+            if (nv < 4) {
+                const unsigned long long m = (1ull << (16 * nv)) - 1ull;
+                w.x &= static_cast<unsigned>(m);
+                w.y &= static_cast<unsigned>(m >> 32);
+            }
+            return w;
+        };
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const int d = 16 * dt + col;
+            const uint2 lo2 = ld4(v0 + (int64_t)d * 16, kb + 4 * jj);
+            const uint2 hi2 = ld4(v1 + (int64_t)d * 16, kb + 16 + 4 * jj);
+            const uint4 w = {lo2.x, lo2.y, hi2.x, hi2.y};
+            const bf16x8_t vv = __builtin_bit_cast(bf16x8_t, w);
+            f32x4_t o = acc[dt] * alpha;
+            o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, phi, o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, plo, o, 0, 0, 0);
+            acc[dt] = o;
+        }
+    }
+    if (!rvalid) return;
+    float* pp = part + ((((int64_t)s * T + t) * Hq + hq) * n_chunks + chunk) * (D + 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) pp[16 * dt + 4 * jj + rr] = acc[dt][rr];
+    if (jj == 0) {
+        pp[D] = m_run;
+        pp[D + 1] = l_run;
+    }
+}
+
 // Merge the chunk partials of each query row in chunk order; chunks that
 // start past the row's position were never computed for it and are skipped.
 __global__ void __launch_bounds__(256) paged_combine_kernel(const float* __restrict__ part, int T, int Hq, int D,
@@ -262,9 +443,23 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
     DKV_REQUIRE((int64_t)n_chunks * n_qtiles < (1LL << 31), "dkv_paged_attention: grid too large");
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(c.head_dim)));
     hipStream_t st = dkv::as_stream(stream);
-    hipLaunchKernelGGL(dkv::paged_attn_kernel, dim3(n_chunks * n_qtiles, c.n_kv_heads, c.batch), dim3(256),
-                       dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, chunk_keys, n_chunks,
-                       n_qtiles, scale, static_cast<float*>(work));
+    // the kernel choice depends on the cache only (never on T), so a verify
+    // pass and a one-token decode step take the same arithmetic path
+    const bool mfma = c.dtype == DKV_BF16 && c.block_size == 16 && (c.head_dim == 64 || c.head_dim == 128);
+    if (mfma) {
+        const int qblocks = (n_qtiles + 3) / 4;
+        const dim3 grid(n_chunks * qblocks, c.n_kv_heads, c.batch), blk(64 * std::min(4, n_qtiles));
+        if (c.head_dim == 128)
+            hipLaunchKernelGGL(dkv::paged_attn_mfma_kernel<128>, grid, blk, 0, st, c, layer, q, T, n_q_heads, start,
+                               chunk_keys, n_chunks, n_qtiles, scale, static_cast<float*>(work));
+        else
+            hipLaunchKernelGGL(dkv::paged_attn_mfma_kernel<64>, grid, blk, 0, st, c, layer, q, T, n_q_heads, start,
+                               chunk_keys, n_chunks, n_qtiles, scale, static_cast<float*>(work));
+    } else {
+        hipLaunchKernelGGL(dkv::paged_attn_kernel, dim3(n_chunks * n_qtiles, c.n_kv_heads, c.batch), dim3(256),
+                           dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, chunk_keys, n_chunks,
+                           n_qtiles, scale, static_cast<float*>(work));
+    }
     int rc = dkv::check_launch("dkv_paged_attention");
     if (rc) return rc;
     hipLaunchKernelGGL(dkv::paged_combine_kernel, dim3(n_q_heads, T, c.batch), dim3(128), 0, st,
