@@ -107,59 +107,11 @@ __device__ __forceinline__ float dequant(int code, GroupMeta m) {
     return __fadd_rn(prod, m.lo);
 }
 
-// bytes one head-row of codes occupies for a given bit width
-__host__ __device__ inline int64_t code_row_bytes(int bits, int d) {
-    return bits >= 16 ? 4 * (int64_t)d : (bits == 8 ? (int64_t)d : ((int64_t)d + 1) / 2);
-}
 __host__ __device__ inline int n_groups(int d, int group) { return (d + group - 1) / group; }
-__host__ __device__ inline int64_t meta_row_bytes(int bits, int d, int group, int meta_f16) {
-    return bits >= 16 ? 0 : (int64_t)n_groups(d, group) * (meta_f16 ? 4 : 8);
-}
-
-// read code j of a packed head-row
-__device__ __forceinline__ int get_code(const uint8_t* row, int j, int bits) {
-    if (bits == 8) return row[j];
-    uint8_t b = row[j >> 1];
-    return (j & 1) ? (b >> 4) : (b & 0xf);
-}
-
-__device__ __forceinline__ GroupMeta get_meta(const uint8_t* mrow, int g, int meta_f16) {
-    if (meta_f16) {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(mrow);
-        return {half_bits_to_f32(h[2 * g]), half_bits_to_f32(h[2 * g + 1])};
-    }
-    const float* f = reinterpret_cast<const float*>(mrow);
-    return {f[2 * g], f[2 * g + 1]};
-}
-
-__device__ __forceinline__ void put_meta(uint8_t* mrow, int g, GroupMeta m, int meta_f16) {
-    if (meta_f16) {
-        uint16_t* h = reinterpret_cast<uint16_t*>(mrow);
-        h[2 * g] = f32_to_half_bits_rne(m.scale);
-        h[2 * g + 1] = f32_to_half_bits_rne(m.lo);
-    } else {
-        float* f = reinterpret_cast<float*>(mrow);
-        f[2 * g] = m.scale;
-        f[2 * g + 1] = m.lo;
-    }
-}
 
 // ------------------------------------------------------------ mirror addressing
-struct Seg {
-    uint8_t* kc;
-    uint8_t* vc;
-    uint8_t* km;
-    uint8_t* vm;
-};
-
 __host__ __device__ inline int64_t seg_index(const dkv_drafter_t& m, int s, int L, int h) {
     return ((int64_t)(s * m.n_layers + L) * m.n_kv_heads + h);
-}
-
-__device__ __forceinline__ Seg seg_of(const dkv_drafter_t& m, int s, int L, int h) {
-    const int64_t i = seg_index(m, s, L, h) * m.cap;
-    return {static_cast<uint8_t*>(m.kc) + i * m.code_stride, static_cast<uint8_t*>(m.vc) + i * m.code_stride,
-            static_cast<uint8_t*>(m.km) + i * m.meta_stride, static_cast<uint8_t*>(m.vm) + i * m.meta_stride};
 }
 
 __host__ __device__ inline int64_t row_index(const dkv_drafter_t& m, int s, int L) {

@@ -4,37 +4,58 @@
 // draftkv/llama.py:202-218, gpt2.py:197-206, model.py:117-127).
 //
 // One query position per sequence; the G query heads of a KV head share its
-// rows. Grid: x = split of CH rows, y = KV head, z = sequence. Each block
-// dequantizes its rows tile by tile into LDS and keeps an online softmax per
-// query head; a combine kernel merges the splits. With want_mass the block
-// also spills its scaled logits, and a third kernel turns them into each
-// row's probability mass summed over query heads (added to the row's score).
-#include "dkv_common.h"
+// rows. A split of `rps` rows (a multiple of the 32-row page) is one unit of
+// work; a combine kernel merges the splits' (max, sum, output) partials.
+// With want_mass the scaled logits are spilled and a third kernel turns them
+// into each row's probability mass summed over query heads, added to the
+// row's score.
+//
+// Fast path (4/8-bit codes, D = 64 or 128, groups a multiple of 16,
+// G * groups <= 16): v_mfma_f32_16x16x32_f16 on the raw codes.
+//   QK: S'[16 rows][16 cols] = code . Qg^T, where column j = (group g, head
+//       h) holds q_h restricted to group g (zero elsewhere), split into f16
+//       hi + lo parts. The magic-number conversion (code | 0x6400) gives the
+//       exact f16 value 1024 + code in one and/or per two codes; a packed f16
+//       subtract removes the 1024 exactly. Folding scale and zero in fp32 per
+//       (row, group) and summing the group columns of a head gives its logit:
+//         s_h = sum_g scale_g * S'[g,h] + lo_g * sum_{d in g} q_h[d]
+//   PV: O'[16 d][16 cols] = (1024 + code_V)^T . B with B[row][(g,h)] =
+//       f16(p_h[row] * scaleV_g[row]); then
+//         o_h[d] = O'[d][(g(d),h)] - 1024 * sum_rows B + sum_rows p_h * loV_g
+// The accumulator lanes of the QK product already hold the 8 rows of one
+// column that the PV B operand needs, so probabilities never move between
+// lanes; the V page layout (mirror_layout.h) is the PV A operand.
+#include "mirror_layout.h"
 
 namespace dkv {
 
-constexpr int DQB = 16;     // max query heads per KV head
-constexpr int DKT = 32;     // rows per tile
+constexpr int DQB = 16;     // max query heads per KV head (generic path)
 constexpr int DMAXD = 128;  // LDS tiles stay under 64 KB
-constexpr int DCH = 512;    // rows per split
 
+__host__ __device__ inline int rows_per_split(const dkv_drafter_t& m) {
+    // enough splits to fill the chip at small batch, few partials at large batch
+    return (m.batch * m.n_kv_heads >= 128) ? 512 : 128;
+}
+
+// ---------------------------------------------------------------- generic path
 __global__ void __launch_bounds__(256) draft_attn_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
-                                                         const float* __restrict__ q, int Hq, float scale,
+                                                         const float* __restrict__ q, int Hq, float scale, int rps,
                                                          int n_splits, float* __restrict__ part,
                                                          float* __restrict__ logits) {
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int D = m.head_dim, G = Hq / m.n_kv_heads;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int r_begin = split * DCH;
-    const int r_end = min(r_begin + DCH, n);
+    const int r_begin = split * rps;
+    const int r_end = min(r_begin + rps, n);
     const int tid = threadIdx.x;
+    const PageFmt f = page_fmt(cfg, D);
 
     extern __shared__ float smem[];
     float* sQ = smem;                   // [DQB][D]
-    float* sK = sQ + DQB * D;           // [DKT][D+1]
-    float* sV = sK + DKT * (D + 1);     // [DKT][D]
-    float* sS = sV + DKT * D;           // [DQB][DKT]
-    float* sM = sS + DQB * DKT;
+    float* sK = sQ + DQB * D;           // [PAGE][D+1]
+    float* sV = sK + PAGE * (D + 1);    // [PAGE][D]
+    float* sS = sV + PAGE * D;          // [DQB][PAGE]
+    float* sM = sS + DQB * PAGE;
     float* sL = sM + DQB;
     float* sA = sL + DQB;
 
@@ -52,55 +73,54 @@ __global__ void __launch_bounds__(256) draft_attn_kernel(dkv_drafter_t m, int la
     for (int j = 0; j < MAXACC; ++j) acc[j] = 0.0f;
     const int n_out = DQB * D;
 
-    const Seg sg = seg_of(m, s, layer, h);
-    const int64_t crb = code_row_bytes(cfg.bits, D), mrb = meta_row_bytes(cfg.bits, D, cfg.group, cfg.meta_f16);
-
-    for (int rt = r_begin; rt < r_end; rt += DKT) {
+    for (int rt = r_begin; rt < r_end; rt += PAGE) {
         __syncthreads();
-        for (int i = tid; i < DKT * D; i += blockDim.x) {
-            const int j = i / D, d = i % D;
-            const int r = rt + j;
+        const uint8_t* pg = page_ptr(m, s, layer, h, rt / PAGE);
+        for (int x = tid; x < PAGE * D; x += blockDim.x) {
+            const int i = x / D, d = x % D;
             float kv = 0.0f, vv = 0.0f;
-            if (r < r_end) {
-                if (cfg.bits >= 16) {
-                    kv = reinterpret_cast<const float*>(sg.kc + (int64_t)r * crb)[d];
-                    vv = reinterpret_cast<const float*>(sg.vc + (int64_t)r * crb)[d];
+            if (rt + i < r_end) {
+                if (f.cb == 32) {
+                    kv = reinterpret_cast<const float*>(pg + f.kc)[(int64_t)i * D + d];
+                    vv = reinterpret_cast<const float*>(pg + f.vc)[(int64_t)i * D + d];
                 } else {
-                    const int g = d / cfg.group;
-                    kv = dequant(get_code(sg.kc + (int64_t)r * crb, d, cfg.bits),
-                                 get_meta(sg.km + (int64_t)r * mrb, g, cfg.meta_f16));
-                    vv = dequant(get_code(sg.vc + (int64_t)r * crb, d, cfg.bits),
-                                 get_meta(sg.vm + (int64_t)r * mrb, g, cfg.meta_f16));
+                    const int g = d / f.group;
+                    int64_t w;
+                    int sh;
+                    k_code_loc(f, i, d, &w, &sh);
+                    kv = dequant(read_code(pg + f.kc, w, sh, f.cb), read_meta(pg + k_meta_off(f, i, g), f.meta_f16));
+                    v_code_loc(f, i, d, &w, &sh);
+                    vv = dequant(read_code(pg + f.vc, w, sh, f.cb), read_meta(pg + v_meta_off(f, i, g), f.meta_f16));
                 }
             }
-            sK[j * (D + 1) + d] = kv;
-            sV[j * D + d] = vv;
+            sK[i * (D + 1) + d] = kv;
+            sV[i * D + d] = vv;
         }
         __syncthreads();
-        for (int i = tid; i < DQB * DKT; i += blockDim.x) {
-            const int r = i / DKT, j = i % DKT;
+        for (int x = tid; x < DQB * PAGE; x += blockDim.x) {
+            const int r = x / PAGE, j = x % PAGE;
             float sc = -INFINITY;
             if (r < G && rt + j < r_end) {
                 float dot = 0.0f;
                 for (int d = 0; d < D; ++d) dot = fmaf(sQ[r * D + d], sK[j * (D + 1) + d], dot);
                 sc = dot * scale;
-                if (logits) logits[(((int64_t)s * Hq) + h * G + r) * m.cap + rt + j] = sc;
+                if (logits) logits[((int64_t)s * Hq + h * G + r) * m.cap + rt + j] = sc;
             }
-            sS[i] = sc;
+            sS[x] = sc;
         }
         __syncthreads();
         {
             const int r = tid / 16, l16 = tid % 16;
             float mx = -INFINITY;
-            for (int j = l16; j < DKT; j += 16) mx = fmaxf(mx, sS[r * DKT + j]);
+            for (int j = l16; j < PAGE; j += 16) mx = fmaxf(mx, sS[r * PAGE + j]);
             for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
             const float m_old = sM[r];
             const float m_new = fmaxf(m_old, mx);
             float sum = 0.0f;
-            for (int j = l16; j < DKT; j += 16) {
-                const float sc = sS[r * DKT + j];
+            for (int j = l16; j < PAGE; j += 16) {
+                const float sc = sS[r * PAGE + j];
                 const float p = (sc == -INFINITY) ? 0.0f : __expf(sc - m_new);
-                sS[r * DKT + j] = p;
+                sS[r * PAGE + j] = p;
                 sum += p;
             }
             for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
@@ -119,7 +139,7 @@ __global__ void __launch_bounds__(256) draft_attn_kernel(dkv_drafter_t m, int la
             if (o < n_out) {
                 const int r = o / D, d = o % D;
                 float a = acc[jj] * sA[r];
-                for (int j = 0; j < DKT; ++j) a = fmaf(sS[r * DKT + j], sV[j * D + d], a);
+                for (int j = 0; j < PAGE; ++j) a = fmaf(sS[r * PAGE + j], sV[j * D + d], a);
                 acc[jj] = a;
             }
         }
@@ -142,14 +162,224 @@ __global__ void __launch_bounds__(256) draft_attn_kernel(dkv_drafter_t m, int la
     }
 }
 
+// ---------------------------------------------------------------- MFMA path
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// 8 codes of one word (cb 4) or two words (cb 8) -> f16 (1024 + code) x 8
+template <int CB>
+__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w);
+
+// the same codes as exact f16 integers (one packed f16 subtract per pair):
+// the QK fold multiplies by the group scale, so an uncancelled 1024 offset
+// would cost precision when scales are large
+template <int CB>
+__device__ __forceinline__ f16x8_t codes_to_f16_exact(const uint32_t* w) {
+    f16x8_t x = codes_to_f16<CB>(w);
+    const f16x2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f16x2_t p = {x[2 * i], x[2 * i + 1]};
+        p = p - off;
+        x[2 * i] = p[0];
+        x[2 * i + 1] = p[1];
+    }
+    return x;
+}
+
+template <int CB>
+__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w) {
+    uint4 r;
+    if (CB == 4) {
+        const uint32_t x = w[0];
+        r.x = (x & 0x000F000Fu) | 0x64006400u;
+        r.y = ((x >> 4) & 0x000F000Fu) | 0x64006400u;
+        r.z = ((x >> 8) & 0x000F000Fu) | 0x64006400u;
+        r.w = ((x >> 12) & 0x000F000Fu) | 0x64006400u;
+    } else {
+        r.x = (w[0] & 0x00FF00FFu) | 0x64006400u;
+        r.y = ((w[0] >> 8) & 0x00FF00FFu) | 0x64006400u;
+        r.z = (w[1] & 0x00FF00FFu) | 0x64006400u;
+        r.w = ((w[1] >> 8) & 0x00FF00FFu) | 0x64006400u;
+    }
+    return __builtin_bit_cast(f16x8_t, r);
+}
+
+__device__ __forceinline__ GroupMeta meta_at(const uint8_t* p, int k, int meta_f16) {
+    return read_meta(p + (int64_t)k * (meta_f16 ? 4 : 8), meta_f16);
+}
+
+template <int D, int CB>
+__global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
+                                                              const float* __restrict__ q, int Hq, float scale,
+                                                              int rps, int n_splits, float* __restrict__ part,
+                                                              float* __restrict__ logits) {
+    constexpr int NSTEP = D / 32;     // k-steps of the QK product
+    constexpr int NDT = D / 16;       // d-tiles of the PV product
+    constexpr int DL = D / 4;         // channels per lane group in QK
+    constexpr int WPL = DL * CB / 32; // code words per lane per K row
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int split = blockIdx.x * 4 + wave;
+    if (split >= n_splits) return;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int G = Hq / m.n_kv_heads;
+    const int group = cfg.group, NG = D / group, ncol = G * NG;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    const int r_begin = split * rps;
+    if (r_begin >= n) return;
+    const int r_end = min(r_begin + rps, n);
+    const PageFmt f = page_fmt(cfg, D);
+    const int col = lane % 16, jj = lane / 16;
+    const bool cvalid = col < ncol;
+    const int gcol = cvalid ? col / G : 0, hcol = cvalid ? col % G : 0;
+    const int hq = h * G + hcol;
+
+    // Q^T columns (group, head) in f16 hi + lo, and the column's q sum
+    f16x8_t qhi[NSTEP], qlo[NSTEP];
+    float qsum = 0.0f;
+    {
+        const float* qr = q + ((int64_t)s * Hq + hq) * D + DL * jj;
+#pragma unroll
+        for (int st = 0; st < NSTEP; ++st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = DL * jj + 8 * st + e;
+                const float v = (cvalid && d / group == gcol) ? qr[8 * st + e] : 0.0f;
+                const _Float16 hi = (_Float16)v;
+                const _Float16 lo = (_Float16)(v - (float)hi);
+                qhi[st][e] = hi;
+                qlo[st][e] = lo;
+                qsum += (float)hi + (float)lo;
+            }
+        qsum += __shfl_xor(qsum, 16);
+        qsum += __shfl_xor(qsum, 32);
+    }
+    f32x4_t acc[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f, bsum = 0.0f, zsum = 0.0f;
+    const int mf = f.meta_f16;
+    const int gmeta = min(gcol, NG - 1);
+
+    for (int p0 = r_begin; p0 < r_end; p0 += PAGE) {
+        const uint8_t* pg = page_ptr(m, s, layer, h, p0 / PAGE);
+        // ---- QK over the page's two 16-row tiles
+        float sv[8];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int i = 16 * a + col;   // A operand row of this lane
+            const uint32_t* kw = reinterpret_cast<const uint32_t*>(pg + f.kc + (int64_t)i * (D * CB / 8)) + WPL * jj;
+            uint32_t kr[WPL];
+#pragma unroll
+            for (int x = 0; x < WPL; ++x) kr[x] = kw[x];
+            f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < NSTEP; ++st) {
+                const f16x8_t kv = codes_to_f16_exact<CB>(kr + st * (CB / 4));
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qhi[st], sa, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qlo[st], sa, 0, 0, 0);
+            }
+            // fold this column's group scale/zero for rows 16a + 4jj + r
+            const uint8_t* km = pg + k_meta_off(f, 16 * a + 4 * jj, gmeta);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const GroupMeta mt = meta_at(km, r, mf);
+                const float t = cvalid ? fmaf(mt.scale, sa[r], mt.lo * qsum) : 0.0f;
+                sv[4 * a + r] = t;
+            }
+        }
+        // sum the group columns of each head: lanes (g * G + hcol) of this 16-lane row
+        float sh[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) sh[x] = 0.0f;
+        for (int g = 0; g < NG; ++g) {
+            const int src = (lane & ~15) | (g * G + hcol);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) sh[x] += __shfl(sv[x], src);
+        }
+        // mask, scale, optional spill, online softmax per column
+        float pv[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            const int row = p0 + 16 * (x / 4) + 4 * jj + (x % 4);
+            const bool ok = cvalid && row < r_end;
+            const float v = ok ? sh[x] * scale : -INFINITY;
+            if (logits && ok && gcol == 0) logits[((int64_t)s * Hq + hq) * m.cap + row] = v;
+            pv[x] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            pv[x] = (pv[x] == -INFINITY) ? 0.0f : __expf(pv[x] - m_new);
+            sum += pv[x];
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
+        l_run = l_run * alpha + sum;
+        m_run = m_new;
+        // ---- PV: B[row (jj, e)][col] = f16(p * scaleV), rows e<4: 4jj+e, e>=4: 16+4jj+e-4
+        const uint8_t* vm = pg + f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB;
+        f16x8_t bop;
+        float bs = 0.0f, zs = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const GroupMeta mt = meta_at(vm, e, mf);
+            const int row = p0 + (e < 4 ? 4 * jj + e : 16 + 4 * jj + e - 4);
+            const bool ok = cvalid && row < r_end;
+            const _Float16 b = ok ? (_Float16)(pv[e] * mt.scale) : (_Float16)0.0f;
+            bop[e] = b;
+            bs += (float)b;
+            zs += ok ? pv[e] * mt.lo : 0.0f;
+        }
+        bsum = bsum * alpha + bs;
+        zsum = zsum * alpha + zs;
+        // V^T A operand: lane (d = 16t + col, jj) words ((col*4 + jj)*NDT + t)
+        const uint32_t* vw = reinterpret_cast<const uint32_t*>(pg + f.vc) + ((col * 4 + jj) * NDT) * (CB / 4);
+        uint32_t vr[NDT * (CB / 4)];
+#pragma unroll
+        for (int x = 0; x < NDT * (CB / 4); ++x) vr[x] = vw[x];
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+            const f16x8_t av = codes_to_f16<CB>(vr + t * (CB / 4));
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t] * alpha, 0, 0, 0);
+        }
+    }
+    // totals of the per-column corrections over the 4 lane groups
+    bsum += __shfl_xor(bsum, 16);
+    bsum += __shfl_xor(bsum, 32);
+    zsum += __shfl_xor(zsum, 16);
+    zsum += __shfl_xor(zsum, 32);
+    if (!cvalid) return;
+    float* pp = part + (((int64_t)s * Hq + hq) * n_splits + split) * (D + 2);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+        if ((16 * t) / group != gcol) continue;   // this column's group covers tile t
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pp[16 * t + 4 * jj + r] = acc[t][r] - 1024.0f * bsum + zsum;
+    }
+    if (gcol == 0 && jj == 0) {
+        pp[D] = m_run;
+        pp[D + 1] = l_run;
+    }
+}
+
+// ---------------------------------------------------------------- combine + mass
 // merge splits per (seq, query head); also records the final (max, sum)
 __global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int layer, const float* __restrict__ part,
-                                                            int Hq, int n_splits, float* __restrict__ out,
+                                                            int Hq, int rps, int n_splits, float* __restrict__ out,
                                                             float* __restrict__ stats) {
     const int hq = blockIdx.x, s = blockIdx.y;
     const int D = m.head_dim;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int ns = min((n + DCH - 1) / DCH, n_splits);
+    const int ns = min((n + rps - 1) / rps, n_splits);
     const float* p = part + ((int64_t)s * Hq + hq) * n_splits * (D + 2);
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float mm = -INFINITY, l = 0.0f, o = 0.0f;
@@ -188,14 +418,23 @@ __global__ void __launch_bounds__(256) draft_mass_kernel(dkv_drafter_t m, int la
 }
 
 static size_t smem_bytes(int D) {
-    return sizeof(float) * (DQB * D + DKT * (D + 1) + DKT * D + DQB * DKT + 3 * DQB);
+    return sizeof(float) * (DQB * D + PAGE * (D + 1) + PAGE * D + DQB * PAGE + 3 * DQB);
+}
+
+static bool fast_path(const dkv_drafter_t& m, const dkv_qcfg_t& c, int Hq) {
+    const int D = m.head_dim;
+    if (c.bits >= 16 || (D != 64 && D != 128) || c.group <= 0 || c.group % 16 != 0 || D % c.group != 0) return false;
+    return (Hq / m.n_kv_heads) * (D / c.group) <= 16;
 }
 
 }  // namespace dkv
 
 using namespace dkv;
 
-static int n_splits_of(const dkv_drafter_t* m) { return (m->cap + DCH - 1) / DCH; }
+static int n_splits_of(const dkv_drafter_t* m) {
+    const int rps = rows_per_split(*m);
+    return (m->cap + rps - 1) / rps;
+}
 
 extern "C" size_t dkv_drafter_attention_workspace(const dkv_drafter_t* mirror, int32_t n_q_heads,
                                                   int32_t want_mass) {
@@ -212,26 +451,46 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
                                      size_t work_bytes, dkv_stream_t stream) {
     DKV_REQUIRE(mirror && q && out, "dkv_drafter_attention: NULL argument");
     const dkv_drafter_t m = *mirror;
+    DKV_REQUIRE(m.pages && m.n_rows && m.cap > 0 && m.cap % PAGE == 0, "dkv_drafter_attention: bad mirror");
     DKV_REQUIRE(layer >= 0 && layer < m.n_layers, "dkv_drafter_attention: layer out of range");
     DKV_REQUIRE(m.head_dim > 0 && m.head_dim <= DMAXD, "dkv_drafter_attention: head_dim must be 1..128");
     DKV_REQUIRE(n_q_heads > 0 && n_q_heads % m.n_kv_heads == 0 && n_q_heads / m.n_kv_heads <= DQB,
                 "dkv_drafter_attention: query heads must be 1..16 per KV head");
     DKV_REQUIRE(cfg.bits >= 16 || cfg.group > 0, "dkv_drafter_attention: bad group");
+    DKV_REQUIRE(page_fmt(cfg, m.head_dim).bytes <= m.page_stride,
+                "dkv_drafter_attention: arm needs more bytes per page than the mirror reserves");
     const size_t need = dkv_drafter_attention_workspace(mirror, n_q_heads, want_mass);
     if (!work || work_bytes < need)
         return fail(DKV_EWORKSPACE, "dkv_drafter_attention: workspace too small (need " + std::to_string(need) + ")");
-    const int ns = n_splits_of(mirror);
+    const int ns = n_splits_of(mirror), rps = rows_per_split(m);
     float* part = static_cast<float*>(work);
     float* stats = part + (size_t)m.batch * n_q_heads * ns * (m.head_dim + 2);
     float* logits = want_mass ? stats + (size_t)m.batch * n_q_heads * 2 : nullptr;
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st, m,
-                       layer, cfg, q, n_q_heads, scale, ns, part, logits);
+    if (fast_path(m, cfg, n_q_heads)) {
+        const dim3 grid((ns + 3) / 4, m.n_kv_heads, m.batch);
+        const int cb = cfg.bits == 8 ? 8 : 4;
+        if (m.head_dim == 128 && cb == 4)
+            hipLaunchKernelGGL((draft_attn_mfma_kernel<128, 4>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
+                               scale, rps, ns, part, logits);
+        else if (m.head_dim == 128)
+            hipLaunchKernelGGL((draft_attn_mfma_kernel<128, 8>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
+                               scale, rps, ns, part, logits);
+        else if (cb == 4)
+            hipLaunchKernelGGL((draft_attn_mfma_kernel<64, 4>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
+                               scale, rps, ns, part, logits);
+        else
+            hipLaunchKernelGGL((draft_attn_mfma_kernel<64, 8>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
+                               scale, rps, ns, part, logits);
+    } else {
+        hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
+                           m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
+    }
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
-    hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(128), 0, st, m, layer, part, n_q_heads, ns,
-                       out, stats);
+    hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(128), 0, st, m, layer, part, n_q_heads,
+                       rps, ns, out, stats);
     if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
     if (want_mass) {
         hipLaunchKernelGGL(draft_mass_kernel, dim3((m.cap + 255) / 256, m.batch), dim3(256), 0, st, m, layer,

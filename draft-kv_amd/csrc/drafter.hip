@@ -2,14 +2,14 @@
 // per-round resync, (c) rebuild under a new arm, and a gather for `read`.
 // Reference: draftkv/compress.py:95-241.
 //
-// Storage: per (seq, layer, kv head) a dense segment of row slots; rows
-// 0..n_rows-1 are live, in no particular order (attention is order-free and
-// the eviction order is defined on (score, position), not on slots). Both
-// eviction and truncation keep the segment dense by moving surviving rows
-// from the tail into the holes ("eviction compaction").
+// Storage (mirror_layout.h): per (sequence, layer, kv head) a dense run of
+// 32-row pages; rows 0..n_rows-1 are live, in no particular order (attention
+// is order-free and the eviction order is defined on (score, position), not
+// on slots). Eviction and truncation keep the run dense by moving surviving
+// rows from the tail into the holes ("eviction compaction").
 #include <climits>
 
-#include "dkv_common.h"
+#include "mirror_layout.h"
 
 namespace dkv {
 
@@ -20,41 +20,109 @@ constexpr int WIN = 4096;         // position window scanned for the sink/recent
 constexpr int32_t DEAD = INT_MAX; // position marking an evicted row before compaction
 
 // ------------------------------------------------------------ row quantizer
-// One wave quantizes one head-row of D values fetched by `ld(j)` and writes
-// its packed codes and (scale, lo) pairs.
+// A wave quantizes one head-row of D values. Lane l owns channels [8l, 8l+8);
+// lanes past D stand for the zero padding of a short last group
+// (compress.py:32-35). Group min/max are reduced over the group's group/8
+// lanes, so K words (one row's codes) are written whole by one lane. V words
+// hold codes of 8 rows, so a V code is a read-modify-write: callers give
+// each (sequence, layer, head) segment to one wave at a time.
+struct LaneCodes {
+    int code[8];
+    float raw[8];
+    GroupMeta m;
+};
+
 template <class Load>
-__device__ void quant_head_row(Load ld, int D, dkv_qcfg_t cfg, uint8_t* crow, uint8_t* mrow, int lane) {
-    if (cfg.bits >= 16) {
-        float* f = reinterpret_cast<float*>(crow);
-        for (int j = lane; j < D; j += WAVE) f[j] = ld(j);
+__device__ __forceinline__ void quant_lane(Load ld, const PageFmt& f, int bits, int lane, LaneCodes& lc) {
+    const int d0 = 8 * lane;
+    const bool real = d0 < f.D;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = real ? ld(d0 + e) : 0.0f;
+    if (f.cb == 32) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lc.raw[e] = v[e];
         return;
     }
-    const int ng = n_groups(D, cfg.group);
-    for (int g = 0; g < ng; ++g) {
-        float mn = INFINITY, mx = -INFINITY;
-        for (int e = lane; e < cfg.group; e += WAVE) {
-            const int j = g * cfg.group + e;
-            const float v = j < D ? ld(j) : 0.0f;
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
-        }
-        mn = wave_min(mn);
-        mx = wave_max(mx);
-        const GroupMeta m = group_meta(mn, mx, cfg.bits, cfg.meta_f16);
-        if (lane == 0) put_meta(mrow, g, m, cfg.meta_f16);
-        const int j0 = g * cfg.group, j1 = min(D, j0 + cfg.group);
-        if (cfg.bits == 8) {
-            for (int j = j0 + lane; j < j1; j += WAVE) crow[j] = static_cast<uint8_t>(quant_code(ld(j), m, 8));
-        } else {
-            // two codes per byte; groups start on even elements (group is even or
-            // the row holds a single group)
-            for (int j = j0 + 2 * lane; j < j1; j += 2 * WAVE) {
-                const int lo_c = quant_code(ld(j), m, cfg.bits);
-                const int hi_c = (j + 1 < j1) ? quant_code(ld(j + 1), m, cfg.bits) : 0;
-                crow[j >> 1] = static_cast<uint8_t>(lo_c | (hi_c << 4));
-            }
+    const int gl = f.group / 8;                 // lanes per group
+    float mn = INFINITY, mx = -INFINITY;
+    if (lane < f.NG * gl) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            mn = fminf(mn, v[e]);
+            mx = fmaxf(mx, v[e]);
         }
     }
+    for (int o = 1; o < gl; o <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o));
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    lc.m = group_meta(mn, mx, bits, f.meta_f16);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lc.code[e] = quant_code(v[e], lc.m, bits);
+}
+
+__device__ __forceinline__ void put_k_lane(uint8_t* page, const PageFmt& f, int i, int lane, const LaneCodes& lc) {
+    const int d0 = 8 * lane;
+    if (d0 >= f.D) return;
+    if (f.cb == 32) {
+        float* dst = reinterpret_cast<float*>(page + f.kc) + (int64_t)i * f.D + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = lc.raw[e];
+        return;
+    }
+    uint32_t* sec = reinterpret_cast<uint32_t*>(page + f.kc);
+    if (f.cb == 4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w |= static_cast<uint32_t>(lc.code[e]) << code_shift(4, e);
+        sec[((int64_t)i * f.D + d0) / 8] = w;
+    } else {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            w0 |= static_cast<uint32_t>(lc.code[e]) << code_shift(8, e);
+            w1 |= static_cast<uint32_t>(lc.code[4 + e]) << code_shift(8, e);
+        }
+        sec[((int64_t)i * f.D + d0) / 4] = w0;
+        sec[((int64_t)i * f.D + d0) / 4 + 1] = w1;
+    }
+    if (d0 % f.group == 0) write_meta(page + k_meta_off(f, i, d0 / f.group), lc.m, f.meta_f16);
+}
+
+// V codes of this lane's 8 channels for row i (exclusive access to the words)
+__device__ __forceinline__ void put_v_lane(uint8_t* page, const PageFmt& f, int i, int lane, const LaneCodes& lc) {
+    const int d0 = 8 * lane;
+    if (d0 >= f.D) return;
+    if (f.cb == 32) {
+        float* dst = reinterpret_cast<float*>(page + f.vc) + (int64_t)i * f.D + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = lc.raw[e];
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        int64_t w;
+        int sh;
+        v_code_loc(f, i, d0 + e, &w, &sh);
+        if (f.cb == 8) {
+            page[f.vc + w * 4 + sh / 8] = static_cast<uint8_t>(lc.code[e]);
+        } else {
+            uint32_t* pw = reinterpret_cast<uint32_t*>(page + f.vc) + w;
+            *pw = (*pw & ~(0xfu << sh)) | (static_cast<uint32_t>(lc.code[e]) << sh);
+        }
+    }
+    if (d0 % f.group == 0) write_meta(page + v_meta_off(f, i, d0 / f.group), lc.m, f.meta_f16);
+}
+
+template <class LoadK, class LoadV>
+__device__ __forceinline__ void quant_row(LoadK ldk, LoadV ldv, const PageFmt& f, int bits, uint8_t* page, int i,
+                                          int lane) {
+    LaneCodes lc;
+    quant_lane(ldk, f, bits, lane, lc);
+    put_k_lane(page, f, i, lane, lc);
+    quant_lane(ldv, f, bits, lane, lc);
+    put_v_lane(page, f, i, lane, lc);
 }
 
 // ------------------------------------------------------------ block helpers
@@ -90,33 +158,53 @@ __device__ int block_rank(int flag, int* red, int* total) {
 
 struct RowCtx {
     const dkv_drafter_t* m;
-    int s, L;
-    int64_t crow_bytes, mrow_bytes;   // bytes per head-row for this layer's arm
-    int32_t* pos;                     // this (s, L)'s pos array
+    int s, L, bits;
+    PageFmt f;
+    int32_t* pos;     // this (s, L)'s pos array
     double* score;
 };
 
-// copy one row slot to another (all heads, K and V, codes and meta, pos, score)
-__device__ void copy_row(const RowCtx& c, int from, int to, int part, int nparts) {
+// Copy row slot `from` to slot `to` of head h (codes, meta; pos and score
+// with h == 0). One wave per head: the V words it rewrites belong to this
+// head's segment only.
+__device__ void copy_row_head(const RowCtx& c, int h, int from, int to, int lane) {
     const dkv_drafter_t& m = *c.m;
-    const int H = m.n_kv_heads;
-    const int64_t cw = c.crow_bytes / 4, mw = c.mrow_bytes / 4;
-    const int64_t per_head = 2 * (cw + mw);
-    for (int64_t i = part; i < H * per_head; i += nparts) {
-        const int h = i / per_head;
-        int64_t r = i % per_head;
-        Seg sg = seg_of(m, c.s, c.L, h);
-        uint8_t* base;
-        int64_t rb;
-        if (r < cw) { base = sg.kc; rb = c.crow_bytes; }
-        else if ((r -= cw) < cw) { base = sg.vc; rb = c.crow_bytes; }
-        else if ((r -= cw) < mw) { base = sg.km; rb = c.mrow_bytes; }
-        else { r -= mw; base = sg.vm; rb = c.mrow_bytes; }
-        uint32_t* dst = reinterpret_cast<uint32_t*>(base + (int64_t)to * rb);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(base + (int64_t)from * rb);
-        dst[r] = src[r];
+    const PageFmt& f = c.f;
+    const int D = f.D;
+    const int fi = from % PAGE, ti = to % PAGE;
+    const uint8_t* src = page_ptr(m, c.s, c.L, h, from / PAGE);
+    uint8_t* dst = page_ptr(m, c.s, c.L, h, to / PAGE);
+    if (f.cb == 32) {
+        for (int d = lane; d < D; d += WAVE) {
+            reinterpret_cast<float*>(dst + f.kc)[(int64_t)ti * D + d] =
+                reinterpret_cast<const float*>(src + f.kc)[(int64_t)fi * D + d];
+            reinterpret_cast<float*>(dst + f.vc)[(int64_t)ti * D + d] =
+                reinterpret_cast<const float*>(src + f.vc)[(int64_t)fi * D + d];
+        }
+    } else {
+        const int wpr = D * f.cb / 32;   // K words per row
+        for (int w = lane; w < wpr; w += WAVE)
+            reinterpret_cast<uint32_t*>(dst + f.kc)[(int64_t)ti * wpr + w] =
+                reinterpret_cast<const uint32_t*>(src + f.kc)[(int64_t)fi * wpr + w];
+        for (int d = lane; d < D; d += WAVE) {
+            int64_t ws, wd;
+            int ss, sd;
+            v_code_loc(f, fi, d, &ws, &ss);
+            v_code_loc(f, ti, d, &wd, &sd);
+            const int code = read_code(src + f.vc, ws, ss, f.cb);
+            if (f.cb == 8) {
+                dst[f.vc + wd * 4 + sd / 8] = static_cast<uint8_t>(code);
+            } else {
+                uint32_t* pw = reinterpret_cast<uint32_t*>(dst + f.vc) + wd;
+                *pw = (*pw & ~(0xfu << sd)) | (static_cast<uint32_t>(code) << sd);
+            }
+        }
+        for (int g = lane; g < f.NG; g += WAVE) {
+            write_meta(dst + k_meta_off(f, ti, g), read_meta(src + k_meta_off(f, fi, g), f.meta_f16), f.meta_f16);
+            write_meta(dst + v_meta_off(f, ti, g), read_meta(src + v_meta_off(f, fi, g), f.meta_f16), f.meta_f16);
+        }
     }
-    if (part == 0) {
+    if (h == 0 && lane == 0) {
         c.pos[to] = c.pos[from];
         c.score[to] = c.score[from];
     }
@@ -129,34 +217,32 @@ __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes
     for (int r = threadIdx.x; r < n; r += BLK) keep += (c.pos[r] < thr);
     const int new_n = block_sum_int(keep, red);
     if (new_n == n) return n;
-    // ranks of holes in [0, new_n) and movers in [new_n, n), processed in
-    // windows of MAXMOVE pairs
     for (int base = 0;; base += MAXMOVE) {
-        int nh = 0, nm = 0, seen_h = 0, seen_m = 0;
+        int seen_h = 0, seen_m = 0;
         __syncthreads();
         for (int r0 = 0; r0 < new_n; r0 += BLK) {
             const int r = r0 + threadIdx.x;
-            const int f = (r < new_n) && (c.pos[r] >= thr);
+            const int fl = (r < new_n) && (c.pos[r] >= thr);
             int tot;
-            const int rk = block_rank(f, red, &tot) + seen_h;
-            if (f && rk >= base && rk < base + MAXMOVE) holes[rk - base] = r;
+            const int rk = block_rank(fl, red, &tot) + seen_h;
+            if (fl && rk >= base && rk < base + MAXMOVE) holes[rk - base] = r;
             seen_h += tot;
         }
         for (int r0 = new_n; r0 < n; r0 += BLK) {
             const int r = r0 + threadIdx.x;
-            const int f = (r < n) && (c.pos[r] < thr);
+            const int fl = (r < n) && (c.pos[r] < thr);
             int tot;
-            const int rk = block_rank(f, red, &tot) + seen_m;
-            if (f && rk >= base && rk < base + MAXMOVE) movers[rk - base] = r;
+            const int rk = block_rank(fl, red, &tot) + seen_m;
+            if (fl && rk >= base && rk < base + MAXMOVE) movers[rk - base] = r;
             seen_m += tot;
         }
-        nh = min(MAXMOVE, seen_h - base);
-        nm = min(MAXMOVE, seen_m - base);
+        const int np = min(min(MAXMOVE, seen_h - base), min(MAXMOVE, seen_m - base));
         __syncthreads();
-        const int np = min(nh, nm);
         if (np <= 0) break;
-        // each pair is copied by a slice of the block
-        for (int p = 0; p < np; ++p) copy_row(c, movers[p], holes[p], threadIdx.x, BLK);
+        // sources (>= new_n) and destinations (< new_n) are disjoint; one wave
+        // per head walks the pairs in order
+        for (int h = threadIdx.x / WAVE; h < c.m->n_kv_heads; h += NWAVES)
+            for (int p = 0; p < np; ++p) copy_row_head(c, h, movers[p], holes[p], threadIdx.x % WAVE);
         __syncthreads();
         if (seen_h - base <= MAXMOVE) break;
     }
@@ -166,12 +252,12 @@ __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes
 // Evict down to `budget` (compress.py:159-179): protected = the `sink` lowest
 // and `recent` highest live positions (recent == 0 protects all); drop the
 // n - budget lowest (score, position) of the rest.
-__device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t maxpos, int* red,
-                     int* holes, int* movers, unsigned* bits_lo, unsigned* bits_hi, double* redd) {
+__device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t maxpos, int* red, int* holes,
+                     int* movers, unsigned* bits_lo, unsigned* bits_hi, double* redd) {
     if (n <= budget || cfg.recent == 0) return n;
     const int n_drop = n - budget;
-    // bounds: sink-th smallest and recent-th largest live positions, from
-    // bitmaps of the windows [0, WIN) and (maxpos - WIN, maxpos]
+    // sink-th smallest and recent-th largest live positions, from bitmaps of
+    // the windows [0, WIN) and (maxpos - WIN, maxpos]
     for (int i = threadIdx.x; i < WIN / 32; i += BLK) {
         bits_lo[i] = 0u;
         bits_hi[i] = 0u;
@@ -194,15 +280,15 @@ __device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t
         cnt = 0;
         for (int dt = 0; dt < WIN && cnt < cfg.recent; ++dt)
             if (bits_hi[dt / 32] >> (dt % 32) & 1u) { ++cnt; recent_min = maxpos - dt; }
-        s_bounds[0] = (cnt >= cfg.recent || cnt == n) ? recent_min : -2;   // -2: not found in window
+        s_bounds[0] = (cnt >= cfg.recent || cnt == n) ? recent_min : -2;   // -2: not within the window
         s_bounds[1] = sink_max;
     }
     __syncthreads();
     int32_t recent_min = s_bounds[0];
     const int32_t sink_max = s_bounds[1];
     if (recent_min == -2) {
-        // fall back: binary search the recent-th largest position
-        int32_t lo = 0, hi = maxpos;   // answer in [lo, hi]
+        // binary search the recent-th largest live position
+        int32_t lo = 0, hi = maxpos;
         while (lo < hi) {
             const int32_t mid = lo + (hi - lo + 1) / 2;
             int cnt = 0;
@@ -212,7 +298,6 @@ __device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t
         }
         recent_min = lo;
     }
-    // select victims one at a time: lowest (score, pos) among unprotected
     __shared__ int s_slot[NWAVES];
     __shared__ int32_t s_pos[NWAVES];
     for (int k = 0; k < n_drop; ++k) {
@@ -249,20 +334,19 @@ __device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t
 }
 
 // ------------------------------------------------------------ fused layer op
-// Per (seq, layer): optional truncate (pos >= trunc_at), append of `cnt`
-// rows at positions p0.. from either the input tensors or the full cache,
-// then evict to budget.
+// Per (seq, layer): optional truncate (pos >= start), append of `cnt` rows at
+// positions start.. from the input tensors or the full cache, then evict.
 struct OpArgs {
     dkv_drafter_t m;
     dkv_paged_t full;        // used when src_full
-    dkv_qcfg_t cfgs[64];     // per layer arm (layer index < 64)
+    dkv_qcfg_t cfgs[64];     // per layer arm
     const void* k;           // [batch][T][Hkv][D] when !src_full
     const void* v;
-    int in_dtype, T, src_full, do_trunc, layer0;   // layer0: first layer (grid.y offset)
-    const int32_t* start;    // first appended position per seq (also truncate point)
+    int in_dtype, T, src_full, do_trunc, layer0;
+    const int32_t* start;
     const int32_t* count;    // rows appended per seq (NULL = T) when !src_full
     const int32_t* end;      // end position per seq when src_full
-    const int32_t* budget;   // [layer*batch + s] or [s] when budget_per_layer == 0
+    const int32_t* budget;   // [layer*batch + s], or [s] when budget_per_layer == 0
     int budget_per_layer;
 };
 
@@ -276,8 +360,7 @@ __global__ void __launch_bounds__(BLK) drafter_op_kernel(OpArgs a) {
     __shared__ int holes[MAXMOVE], movers[MAXMOVE];
     __shared__ unsigned bits_lo[WIN / 32], bits_hi[WIN / 32];
 
-    RowCtx c{&a.m, s, L, code_row_bytes(cfg.bits, D), meta_row_bytes(cfg.bits, D, cfg.group, cfg.meta_f16),
-             m.pos + row_index(m, s, L), m.score + row_index(m, s, L)};
+    RowCtx c{&a.m, s, L, cfg.bits, page_fmt(cfg, D), m.pos + row_index(m, s, L), m.score + row_index(m, s, L)};
     int32_t* nrows_p = m.n_rows + (int64_t)s * m.n_layers + L;
     int n = *nrows_p;
     const int32_t p0 = a.start[s];
@@ -287,34 +370,30 @@ __global__ void __launch_bounds__(BLK) drafter_op_kernel(OpArgs a) {
     }
     int cnt = a.src_full ? (a.end[s] - p0) : (a.count ? a.count[s] : a.T);
     if (cnt < 0) cnt = 0;
-    if (n + cnt > m.cap) cnt = max(0, m.cap - n);   // host sizes cap; never write past it
-    // append: one wave per (row, head)
+    if (n + cnt > m.cap) cnt = max(0, m.cap - n);   // the host sizes cap; never write past it
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
-    for (int item = w; item < cnt * H; item += NWAVES) {
-        const int t = item / H, h = item % H;
-        const int slot = n + t;
-        Seg sg = seg_of(m, s, L, h);
-        uint8_t* kr = sg.kc + (int64_t)slot * c.crow_bytes;
-        uint8_t* vr = sg.vc + (int64_t)slot * c.crow_bytes;
-        uint8_t* kmr = sg.km + (int64_t)slot * c.mrow_bytes;
-        uint8_t* vmr = sg.vm + (int64_t)slot * c.mrow_bytes;
-        if (a.src_full) {
-            const dkv_paged_t& f = a.full;
-            const int pos = p0 + t;
-            const int32_t blk = paged_block(f, s, L, pos);
-            const int off = pos % f.block_size;
-            quant_head_row([&](int j) { return load_elem(f.pool, paged_k_off(f, blk, off, h, j), f.dtype); }, D, cfg,
-                           kr, kmr, lane);
-            quant_head_row([&](int j) { return load_elem(f.pool, paged_v_off(f, blk, off, h, j), f.dtype); }, D, cfg,
-                           vr, vmr, lane);
-        } else {
-            const int64_t src = (((int64_t)s * a.T + t) * H + h) * D;
-            quant_head_row([&](int j) { return load_elem(a.k, src + j, a.in_dtype); }, D, cfg, kr, kmr, lane);
-            quant_head_row([&](int j) { return load_elem(a.v, src + j, a.in_dtype); }, D, cfg, vr, vmr, lane);
-        }
-        if (lane == 0 && h == 0) {
-            c.pos[slot] = p0 + t;
-            c.score[slot] = 0.0;
+    for (int h = w; h < H; h += NWAVES) {          // one wave per head segment
+        for (int t = 0; t < cnt; ++t) {
+            const int slot = n + t;
+            uint8_t* page = page_ptr(m, s, L, h, slot / PAGE);
+            const int i = slot % PAGE;
+            if (a.src_full) {
+                const dkv_paged_t& f = a.full;
+                const int pos = p0 + t;
+                const int32_t blk = paged_block(f, s, L, pos);
+                const int off = pos % f.block_size;
+                quant_row([&](int d) { return load_elem(f.pool, paged_k_off(f, blk, off, h, d), f.dtype); },
+                          [&](int d) { return load_elem(f.pool, paged_v_off(f, blk, off, h, d), f.dtype); }, c.f,
+                          cfg.bits, page, i, lane);
+            } else {
+                const int64_t src = (((int64_t)s * a.T + t) * H + h) * D;
+                quant_row([&](int d) { return load_elem(a.k, src + d, a.in_dtype); },
+                          [&](int d) { return load_elem(a.v, src + d, a.in_dtype); }, c.f, cfg.bits, page, i, lane);
+            }
+            if (lane == 0 && h == 0) {
+                c.pos[slot] = p0 + t;
+                c.score[slot] = 0.0;
+            }
         }
     }
     __syncthreads();
@@ -328,7 +407,10 @@ __global__ void __launch_bounds__(BLK) drafter_op_kernel(OpArgs a) {
 }
 
 // ------------------------------------------------------------ rebuild (c)
-// grid: x = row tile, y = sequence, z = index into the changed-layer list.
+// grid: x = page, y = sequence, z = index into the changed-layer list. All
+// scores restart at 0, so the survivors are the closed form
+// [0, sink) u [n - (B - sink), n); only those rows are quantized, densely and
+// in position order. One wave per (row, head).
 struct RebuildArgs {
     dkv_drafter_t m;
     dkv_paged_t full;
@@ -337,8 +419,6 @@ struct RebuildArgs {
     const int32_t* len;
     const int32_t* budget;
 };
-
-constexpr int RB_ROWS = 16;
 
 __global__ void __launch_bounds__(BLK) drafter_rebuild_kernel(RebuildArgs a) {
     const int s = blockIdx.y, L = a.layers[blockIdx.z];
@@ -357,26 +437,54 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_kernel(RebuildArgs a) {
         sink = min(cfg.sink, n);
     }
     kept = min(kept, m.cap);
-    const int64_t crb = code_row_bytes(cfg.bits, D), mrb = meta_row_bytes(cfg.bits, D, cfg.group, cfg.meta_f16);
+    const PageFmt pf = page_fmt(cfg, D);
     int32_t* pos = m.pos + row_index(m, s, L);
     double* score = m.score + row_index(m, s, L);
-    const int r0 = blockIdx.x * RB_ROWS;
-    if (blockIdx.x == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
+    const int page = blockIdx.x;
+    if (page == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
+    if (page * PAGE >= kept) return;
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
-    for (int item = w; item < RB_ROWS * H; item += NWAVES) {
-        const int r = r0 + item / H, h = item % H;
-        if (r >= kept) continue;
-        const int p = r < sink ? r : n - (kept - sink) + (r - sink);
-        const int32_t blk = paged_block(f, s, L, p);
-        const int off = p % f.block_size;
-        Seg sg = seg_of(m, s, L, h);
-        quant_head_row([&](int j) { return load_elem(f.pool, paged_k_off(f, blk, off, h, j), f.dtype); }, D, cfg,
-                       sg.kc + (int64_t)r * crb, sg.km + (int64_t)r * mrb, lane);
-        quant_head_row([&](int j) { return load_elem(f.pool, paged_v_off(f, blk, off, h, j), f.dtype); }, D, cfg,
-                       sg.vc + (int64_t)r * crb, sg.vm + (int64_t)r * mrb, lane);
-        if (lane == 0 && h == 0) {
-            pos[r] = p;
-            score[r] = 0.0;
+    const int d0 = 8 * lane;
+    // one wave per (page, head); rows visited by V word group j so that a
+    // lane's 8 V words (one per channel) collect all their nibbles before
+    // being stored whole
+    for (int h = w; h < H; h += NWAVES) {
+        uint8_t* pg = page_ptr(m, s, L, h, page);
+        for (int j = 0; j < 4; ++j) {
+            uint32_t vw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+            for (int e = 0; e < 8; ++e) {
+                const int i = e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4);
+                const int r = page * PAGE + i;
+                if (r >= kept) continue;
+                const int p = r < sink ? r : n - (kept - sink) + (r - sink);
+                const int32_t blk = paged_block(f, s, L, p);
+                const int off = p % f.block_size;
+                LaneCodes lc;
+                quant_lane([&](int d) { return load_elem(f.pool, paged_k_off(f, blk, off, h, d), f.dtype); }, pf,
+                           cfg.bits, lane, lc);
+                put_k_lane(pg, pf, i, lane, lc);
+                quant_lane([&](int d) { return load_elem(f.pool, paged_v_off(f, blk, off, h, d), f.dtype); }, pf,
+                           cfg.bits, lane, lc);
+                if (pf.cb == 4) {
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) vw[x] |= static_cast<uint32_t>(lc.code[x]) << code_shift(4, e);
+                    if (d0 < D && d0 % pf.group == 0)
+                        write_meta(pg + v_meta_off(pf, i, d0 / pf.group), lc.m, pf.meta_f16);
+                } else {
+                    put_v_lane(pg, pf, i, lane, lc);
+                }
+                if (lane == 0 && h == 0) {
+                    pos[r] = p;
+                    score[r] = 0.0;
+                }
+            }
+            if (pf.cb == 4 && d0 < D) {
+#pragma unroll
+                for (int x = 0; x < 8; ++x) {
+                    const int d = d0 + x;
+                    reinterpret_cast<uint32_t*>(pg + pf.vc)[((int64_t)(d % 16) * 4 + j) * pf.NDT + d / 16] = vw[x];
+                }
+            }
         }
     }
 }
@@ -393,29 +501,30 @@ __global__ void __launch_bounds__(BLK) drafter_gather_kernel(dkv_drafter_t m, in
                                                              GatherOut ko, GatherOut vo, int32_t* pos_out) {
     const int r = blockIdx.x;
     const int D = m.head_dim, H = m.n_kv_heads;
-    const int64_t crb = code_row_bytes(cfg.bits, D), mrb = meta_row_bytes(cfg.bits, D, cfg.group, cfg.meta_f16);
-    const int ng = cfg.bits >= 16 ? 0 : n_groups(D, cfg.group);
+    const PageFmt f = page_fmt(cfg, D);
+    const int p = r / PAGE, i = r % PAGE;
     if (threadIdx.x == 0 && pos_out) pos_out[r] = m.pos[row_index(m, s, L) + r];
-    for (int i = threadIdx.x; i < 2 * H * D; i += blockDim.x) {
-        const int kvsel = i / (H * D), h = (i / D) % H, j = i % D;
-        Seg sg = seg_of(m, s, L, h);
-        const uint8_t* crow = (kvsel ? sg.vc : sg.kc) + (int64_t)r * crb;
-        const uint8_t* mrow = (kvsel ? sg.vm : sg.km) + (int64_t)r * mrb;
-        const GatherOut& o = kvsel ? vo : ko;
-        const int64_t oi = ((int64_t)r * H + h) * D + j;
-        if (cfg.bits >= 16) {
-            const float val = reinterpret_cast<const float*>(crow)[j];
+    for (int x = threadIdx.x; x < 2 * H * D; x += blockDim.x) {
+        const int is_v = x / (H * D), h = (x / D) % H, d = x % D;
+        const uint8_t* pg = page_ptr(m, s, L, h, p);
+        const GatherOut& o = is_v ? vo : ko;
+        const int64_t oi = ((int64_t)r * H + h) * D + d;
+        if (f.cb == 32) {
+            const float val = reinterpret_cast<const float*>(pg + (is_v ? f.vc : f.kc))[(int64_t)i * D + d];
             if (o.codes) o.codes[oi] = 0;
             if (o.deq) o.deq[oi] = val;
             continue;
         }
-        const int g = j / cfg.group;
-        const GroupMeta mt = get_meta(mrow, g, cfg.meta_f16);
-        const int code = get_code(crow, j, cfg.bits);
+        const int g = d / cfg.group;
+        const GroupMeta mt = read_meta(pg + (is_v ? v_meta_off(f, i, g) : k_meta_off(f, i, g)), f.meta_f16);
+        int64_t w;
+        int sh;
+        if (is_v) v_code_loc(f, i, d, &w, &sh); else k_code_loc(f, i, d, &w, &sh);
+        const int code = read_code(pg + (is_v ? f.vc : f.kc), w, sh, f.cb);
         if (o.codes) o.codes[oi] = static_cast<uint8_t>(code);
         if (o.deq) o.deq[oi] = dequant(code, mt);
-        if (j % cfg.group == 0) {
-            const int64_t gi = ((int64_t)r * H + h) * ng + g;
+        if (d % cfg.group == 0) {
+            const int64_t gi = ((int64_t)r * H + h) * f.NG + g;
             if (o.scale) o.scale[gi] = mt.scale;
             if (o.lo) o.lo[gi] = mt.lo;
         }
@@ -425,30 +534,35 @@ __global__ void __launch_bounds__(BLK) drafter_gather_kernel(dkv_drafter_t m, in
 // ------------------------------------------------------------ host checks
 int check_mirror(const dkv_drafter_t* m, const char* fn) {
     DKV_REQUIRE(m != nullptr, std::string(fn) + ": mirror is NULL");
-    DKV_REQUIRE(m->kc && m->vc && m->km && m->vm && m->pos && m->score && m->n_rows,
-                std::string(fn) + ": mirror has a NULL buffer");
-    DKV_REQUIRE(m->batch > 0 && m->n_layers > 0 && m->n_layers <= 64 && m->n_kv_heads > 0 && m->cap > 0,
-                std::string(fn) + ": bad mirror shape (n_layers must be 1..64)");
-    DKV_REQUIRE(m->head_dim > 0 && m->head_dim % 8 == 0, std::string(fn) + ": head_dim must be a multiple of 8");
+    DKV_REQUIRE(m->pages && m->pos && m->score && m->n_rows, std::string(fn) + ": mirror has a NULL buffer");
+    DKV_REQUIRE(m->batch > 0 && m->n_layers > 0 && m->n_layers <= 64 && m->n_kv_heads > 0 && m->cap > 0 &&
+                    m->cap % PAGE == 0,
+                std::string(fn) + ": bad mirror shape (n_layers 1..64, cap a positive multiple of 32)");
+    DKV_REQUIRE(m->head_dim == 8 || (m->head_dim > 0 && m->head_dim % 16 == 0),
+                std::string(fn) + ": head_dim must be 8 or a multiple of 16");
     return DKV_OK;
 }
 
 int check_cfg(const dkv_drafter_t* m, const dkv_qcfg_t& c, const char* fn) {
     DKV_REQUIRE(c.bits == 2 || c.bits == 3 || c.bits == 4 || c.bits == 8 || c.bits == 16,
                 std::string(fn) + ": bits must be 2, 3, 4, 8 or 16");
-    DKV_REQUIRE(c.bits >= 16 || (c.group > 0 && (c.group % 2 == 0 || c.group >= m->head_dim)),
-                std::string(fn) + ": group must be even");
+    DKV_REQUIRE(c.bits >= 16 || (c.group >= 8 && (c.group & (c.group - 1)) == 0 &&
+                                  n_groups(m->head_dim, c.group) * c.group <= 512),
+                std::string(fn) + ": group must be a power of two >= 8 with ceil(d/group)*group <= 512");
     DKV_REQUIRE(c.sink >= 0 && c.recent >= 0, std::string(fn) + ": sink/recent must be >= 0");
-    DKV_REQUIRE(code_row_bytes(c.bits, m->head_dim) <= m->code_stride,
-                std::string(fn) + ": arm needs more code bytes per row than the mirror reserves");
-    DKV_REQUIRE(meta_row_bytes(c.bits, m->head_dim, c.group, c.meta_f16) <= m->meta_stride,
-                std::string(fn) + ": arm needs more meta bytes per row than the mirror reserves");
+    DKV_REQUIRE(page_fmt(c, m->head_dim).bytes <= m->page_stride,
+                std::string(fn) + ": arm needs more bytes per page than the mirror reserves");
     return DKV_OK;
 }
 
 }  // namespace dkv
 
 using namespace dkv;
+
+extern "C" int64_t dkv_page_bytes(int32_t bits, int32_t head_dim, int32_t group, int32_t meta_f16) {
+    if (head_dim <= 0 || (bits < 16 && group <= 0)) return -1;
+    return page_fmt(bits, head_dim, group, meta_f16).bytes;
+}
 
 extern "C" int dkv_drafter_append(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t cfg, const void* k,
                                   const void* v, int32_t in_dtype, int32_t T, const int32_t* start,
@@ -467,13 +581,10 @@ extern "C" int dkv_drafter_append(const dkv_drafter_t* mirror, int32_t layer, dk
     a.v = v;
     a.in_dtype = in_dtype;
     a.T = T;
-    a.src_full = 0;
-    a.do_trunc = 0;
     a.layer0 = layer;
     a.start = start;
     a.count = count;
     a.budget = budget;
-    a.budget_per_layer = 0;
     hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, 1), dim3(BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_append");
 }
@@ -489,14 +600,17 @@ extern "C" int dkv_drafter_truncate(const dkv_drafter_t* mirror, const dkv_qcfg_
         if ((rc = check_cfg(mirror, cfgs[L], "dkv_drafter_truncate"))) return rc;
         a.cfgs[L] = cfgs[L];
     }
-    a.src_full = 0;
     a.do_trunc = 1;
     a.T = 0;              // nothing appended, so no eviction and budget is never read
     a.start = start;
     a.budget = start;
-    a.layer0 = 0;
     hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_truncate");
+}
+
+static int same_shape(const dkv_drafter_t* m, const dkv_paged_t* f) {
+    return f->n_layers == m->n_layers && f->n_kv_heads == m->n_kv_heads && f->head_dim == m->head_dim &&
+           f->batch == m->batch;
 }
 
 extern "C" int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* full, const dkv_qcfg_t* cfgs,
@@ -505,9 +619,7 @@ extern "C" int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* 
     int rc = check_mirror(mirror, "dkv_drafter_sync");
     if (rc) return rc;
     DKV_REQUIRE(full && cfgs && start && end && budget, "dkv_drafter_sync: NULL argument");
-    DKV_REQUIRE(full->n_layers == mirror->n_layers && full->n_kv_heads == mirror->n_kv_heads &&
-                    full->head_dim == mirror->head_dim && full->batch == mirror->batch,
-                "dkv_drafter_sync: full cache and mirror shapes differ");
+    DKV_REQUIRE(same_shape(mirror, full), "dkv_drafter_sync: full cache and mirror shapes differ");
     OpArgs a{};
     a.m = *mirror;
     a.full = *full;
@@ -521,7 +633,6 @@ extern "C" int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* 
     a.end = end;
     a.budget = budget;
     a.budget_per_layer = 1;
-    a.layer0 = 0;
     hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_sync");
 }
@@ -532,9 +643,7 @@ extern "C" int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_
     int rc = check_mirror(mirror, "dkv_drafter_rebuild");
     if (rc) return rc;
     DKV_REQUIRE(full && layers && cfgs && len && budget, "dkv_drafter_rebuild: NULL argument");
-    DKV_REQUIRE(full->n_layers == mirror->n_layers && full->n_kv_heads == mirror->n_kv_heads &&
-                    full->head_dim == mirror->head_dim && full->batch == mirror->batch,
-                "dkv_drafter_rebuild: full cache and mirror shapes differ");
+    DKV_REQUIRE(same_shape(mirror, full), "dkv_drafter_rebuild: full cache and mirror shapes differ");
     DKV_REQUIRE(n_changed >= 0 && n_changed <= mirror->n_layers, "dkv_drafter_rebuild: bad layer count");
     if (n_changed == 0) return DKV_OK;
     RebuildArgs a{};
@@ -548,8 +657,7 @@ extern "C" int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_
     }
     a.len = len;
     a.budget = budget;
-    const int tiles = (mirror->cap + RB_ROWS - 1) / RB_ROWS;
-    hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(tiles, mirror->batch, n_changed), dim3(BLK), 0,
+    hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(mirror->cap / PAGE, mirror->batch, n_changed), dim3(BLK), 0,
                        as_stream(stream), a);
     return check_launch("dkv_drafter_rebuild");
 }

@@ -25,11 +25,9 @@ class Paged(C.Structure):
 
 
 class Drafter(C.Structure):
-    _fields_ = [("kc", C.c_void_p), ("vc", C.c_void_p), ("km", C.c_void_p), ("vm", C.c_void_p),
-                ("pos", C.c_void_p), ("score", C.c_void_p), ("n_rows", C.c_void_p),
+    _fields_ = [("pages", C.c_void_p), ("pos", C.c_void_p), ("score", C.c_void_p), ("n_rows", C.c_void_p),
                 ("batch", C.c_int32), ("n_layers", C.c_int32), ("n_kv_heads", C.c_int32),
-                ("head_dim", C.c_int32), ("cap", C.c_int32),
-                ("code_stride", C.c_int64), ("meta_stride", C.c_int64)]
+                ("head_dim", C.c_int32), ("cap", C.c_int32), ("page_stride", C.c_int64)]
 
 
 class QCfg(C.Structure):
@@ -45,6 +43,7 @@ _SIGS = {
     "dkv_paged_append": (C.c_int, [PPaged, I32, P, P, I32, I32, P, P, P]),
     "dkv_paged_attention_workspace": (SZ, [PPaged, I32, I32, I32, I32]),
     "dkv_paged_attention": (C.c_int, [PPaged, I32, P, I32, I32, P, I32, I32, P, P, SZ, P]),
+    "dkv_page_bytes": (I64, [I32, I32, I32, I32]),
     "dkv_drafter_append": (C.c_int, [PDrafter, I32, QCfg, P, P, I32, I32, P, P, P, P]),
     "dkv_drafter_truncate": (C.c_int, [PDrafter, PQCfg, P, P]),
     "dkv_drafter_sync": (C.c_int, [PDrafter, PPaged, PQCfg, P, P, P, P]),

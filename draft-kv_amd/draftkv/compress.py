@@ -137,55 +137,43 @@ class CompressedKVCache:
             self._alloc(n_kv_heads, d_head, cap or 4096)
 
     # ------------------------------------------------------------ storage
-    def _strides(self, cfgs) -> tuple[int, int]:
-        D = self.d_head
-        cb = mb = 0
-        for c in list(cfgs) + self._reserve:
-            b = 4 * D if c.bits >= 16 else (D if c.bits == 8 else (D + 1) // 2)
-            m = 0 if c.bits >= 16 else (-(-D // c.group)) * (4 if c.scale_fp16 else 8)
-            cb, mb = max(cb, b), max(mb, m)
-        return cb, max(mb, 4)
+    PAGE = 32
+
+    def _page_stride(self, cfgs) -> int:
+        """Bytes per page slot: the widest page among the arms this mirror holds."""
+        from ._lib import lib
+        return max(int(lib().dkv_page_bytes(c.bits, self.d_head, c.group, int(c.scale_fp16)))
+                   for c in list(cfgs) + self._reserve)
 
     def _alloc(self, H: int, D: int, cap: int) -> None:
+        cap = -(-cap // self.PAGE) * self.PAGE
         self.n_kv_heads, self.d_head, self.cap = H, D, cap
-        self.code_stride, self.meta_stride = self._strides(self.cfgs)
+        self.page_stride = self._page_stride(self.cfgs)
         b, L, dev = self.batch, self.n_layers, self.device
-        u8 = torch.uint8
-        self.kc = torch.empty((b, L, H, cap * self.code_stride), dtype=u8, device=dev)
-        self.vc = torch.empty_like(self.kc)
-        self.km = torch.empty((b, L, H, cap * self.meta_stride), dtype=u8, device=dev)
-        self.vm = torch.empty_like(self.km)
+        self.pages = torch.empty((b, L, H, cap // self.PAGE, self.page_stride), dtype=torch.uint8, device=dev)
         self.pos = torch.full((b, L, cap), -1, dtype=torch.int32, device=dev)
         self.score = torch.zeros((b, L, cap), dtype=torch.float64, device=dev)
         self.n_rows = torch.zeros((b, L), dtype=torch.int32, device=dev)
         self._ready = True
 
     def _regrow(self, cap: int, cfgs=None) -> None:
-        """Re-layout for a larger row capacity and/or wider rows, keeping rows."""
+        """Re-layout for a larger row capacity and/or wider pages, keeping rows."""
         cfgs = cfgs if cfgs is not None else self.cfgs
-        ncs, nms = self._strides(cfgs)
-        if cap <= self.cap and ncs <= self.code_stride and nms <= self.meta_stride:
-            return
-        cap = max(cap, self.cap)
-        old = (self.kc, self.vc, self.km, self.vm, self.pos, self.score, self.cap, self.code_stride, self.meta_stride)
-        ncs, nms = max(ncs, self.code_stride), max(nms, self.meta_stride)
         self._reserve = self._reserve + list(cfgs)
+        stride = self._page_stride(cfgs)
+        if cap <= self.cap and stride <= self.page_stride:
+            return
+        old_pages, old_pos, old_score, ocap, ostride = self.pages, self.pos, self.score, self.cap, self.page_stride
         n_rows = self.n_rows
-        self._alloc(self.n_kv_heads, self.d_head, cap)
+        self._alloc(self.n_kv_heads, self.d_head, max(cap, self.cap))
         self.n_rows = n_rows
-        okc, ovc, okm, ovm, opos, oscore, ocap, ocs, oms = old
-        self.kc[..., : ocap * ocs].copy_(okc)
-        self.vc[..., : ocap * ocs].copy_(ovc)
-        self.km[..., : ocap * oms].copy_(okm)
-        self.vm[..., : ocap * oms].copy_(ovm)
-        self.pos[..., :ocap].copy_(opos)
-        self.score[..., :ocap].copy_(oscore)
+        self.pages[:, :, :, : ocap // self.PAGE, :ostride].copy_(old_pages)
+        self.pos[..., :ocap].copy_(old_pos)
+        self.score[..., :ocap].copy_(old_score)
 
     def desc(self) -> Drafter:
-        return Drafter(self.kc.data_ptr(), self.vc.data_ptr(), self.km.data_ptr(), self.vm.data_ptr(),
-                       self.pos.data_ptr(), self.score.data_ptr(), self.n_rows.data_ptr(), self.batch,
-                       self.n_layers, self.n_kv_heads, self.d_head, self.cap, self.code_stride,
-                       self.meta_stride)
+        return Drafter(self.pages.data_ptr(), self.pos.data_ptr(), self.score.data_ptr(), self.n_rows.data_ptr(),
+                       self.batch, self.n_layers, self.n_kv_heads, self.d_head, self.cap, self.page_stride)
 
     def qcfg(self, layer: int) -> QCfg:
         return _cfg_of(self.cfgs[layer], self.d_head)

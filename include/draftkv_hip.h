@@ -47,24 +47,26 @@ typedef struct {
 } dkv_paged_t;
 
 /* Compressed drafter mirror -- reference draftkv/compress.py:95-241.
- * Per (seq, layer, kv_head) a dense segment of `cap` row slots; rows
- * 0..n_rows-1 are live (eviction and truncation compact it). Row r of the
- * segment lives at   seg_base + r * row_bytes(layer cfg)   where
- *     seg_base = ((seq*n_layers + layer)*n_kv_heads + head) * cap * code_stride
- * (codes) and likewise with meta_stride for (scale, lo) pairs.
- * Codes: bits<=4 -> two 4-bit codes per byte (element 2i in the low nibble);
- * bits==8 -> one byte; bits==16 -> raw float32 values (the reference keeps an
- * fp32 copy, compress.py:28-29). Meta: per group (scale, lo) as float32 pairs,
- * or float16 pairs when meta_f16. pos/score/n_rows are per (seq, layer). */
+ * Per (seq, layer, kv_head) a dense segment of `cap` row slots (cap a
+ * multiple of 32) stored as cap/32 pages of 32 rows; rows 0..n_rows-1 are
+ * live (eviction and truncation compact it). Page p of a segment starts at
+ *     pages + (((seq*n_layers + layer)*n_kv_heads + head) * (cap/32) + p) * page_stride
+ * and holds K codes, K (scale, lo) pairs, V codes and V pairs of its rows in
+ * the layout described in draft-kv_amd/csrc/mirror_layout.h (4-bit codes for
+ * bits <= 4, bytes for 8 bits, raw float32 for 16 bits -- the reference
+ * keeps an fp32 copy, compress.py:28-29; pairs in float32, or float16 when
+ * meta_f16). pos/score/n_rows are per (seq, layer). */
 typedef struct {
-    void* kc; void* vc;          /* codes */
-    void* km; void* vm;          /* per-group (scale, lo) */
+    void* pages;
     int32_t* pos;                /* [batch][n_layers][cap] absolute positions */
     double* score;               /* [batch][n_layers][cap] accumulated attention mass */
     int32_t* n_rows;             /* [batch][n_layers] live rows */
     int32_t batch, n_layers, n_kv_heads, head_dim, cap;
-    int64_t code_stride, meta_stride;   /* bytes reserved per row slot */
+    int64_t page_stride;         /* bytes per page slot (>= the widest arm's page) */
 } dkv_drafter_t;
+
+/* Bytes of one 32-row page for an arm (bits, group, meta_f16) at head_dim d. */
+int64_t dkv_page_bytes(int32_t bits, int32_t head_dim, int32_t group, int32_t meta_f16);
 
 /* One layer's compression arm -- reference draftkv/config.py:9-33 plus the
  * `group` / fp16-meta extension. */
