@@ -170,14 +170,14 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 // 8 codes of one word (cb 4) or two words (cb 8) -> f16 (1024 + code) x 8
 template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w);
+__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w, uint32_t magic);
 
 // the same codes as exact f16 integers (one packed f16 subtract per pair):
 // the QK fold multiplies by the group scale, so an uncancelled 1024 offset
 // would cost precision when scales are large
 template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16_exact(const uint32_t* w) {
-    f16x8_t x = codes_to_f16<CB>(w);
+__device__ __forceinline__ f16x8_t codes_to_f16_exact(const uint32_t* w, uint32_t magic) {
+    f16x8_t x = codes_to_f16<CB>(w, magic);
     const f16x2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -189,29 +189,87 @@ __device__ __forceinline__ f16x8_t codes_to_f16_exact(const uint32_t* w) {
     return x;
 }
 
+// (x & mask) | 0x64006400. Written as a bitfield insert of x into an opaque
+// copy of the constant, so it becomes one v_bfi_b32 instead of an and + or
+// (the constant would otherwise fold and the pattern be lost).
+__device__ __forceinline__ uint32_t magic_f16x2() {
+    uint32_t y;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(y));
+    return y;
+}
+__device__ __forceinline__ uint32_t and_or_magic(uint32_t x, uint32_t mask, uint32_t magic) {
+    return (x & mask) | (magic & ~mask);
+}
+
 template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w) {
+__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w, uint32_t magic) {
     uint4 r;
     if (CB == 4) {
         const uint32_t x = w[0];
-        r.x = (x & 0x000F000Fu) | 0x64006400u;
-        r.y = ((x >> 4) & 0x000F000Fu) | 0x64006400u;
-        r.z = ((x >> 8) & 0x000F000Fu) | 0x64006400u;
-        r.w = ((x >> 12) & 0x000F000Fu) | 0x64006400u;
+        r.x = and_or_magic(x, 0x000F000Fu, magic);
+        r.y = and_or_magic(x >> 4, 0x000F000Fu, magic);
+        r.z = and_or_magic(x >> 8, 0x000F000Fu, magic);
+        r.w = and_or_magic(x >> 12, 0x000F000Fu, magic);
     } else {
-        r.x = (w[0] & 0x00FF00FFu) | 0x64006400u;
-        r.y = ((w[0] >> 8) & 0x00FF00FFu) | 0x64006400u;
-        r.z = (w[1] & 0x00FF00FFu) | 0x64006400u;
-        r.w = ((w[1] >> 8) & 0x00FF00FFu) | 0x64006400u;
+        r.x = and_or_magic(w[0], 0x00FF00FFu, magic);
+        r.y = and_or_magic(w[0] >> 8, 0x00FF00FFu, magic);
+        r.z = and_or_magic(w[1], 0x00FF00FFu, magic);
+        r.w = and_or_magic(w[1] >> 8, 0x00FF00FFu, magic);
     }
     return __builtin_bit_cast(f16x8_t, r);
 }
 
-__device__ __forceinline__ GroupMeta meta_at(const uint8_t* p, int k, int meta_f16) {
-    return read_meta(p + (int64_t)k * (meta_f16 ? 4 : 8), meta_f16);
+// Raw registers of one page as a lane needs them; loaded one page ahead so the
+// memory latency of page p+1 overlaps the products of page p.
+template <int D, int CB, int MF>
+struct PageRegs {
+    static constexpr int WPL = D / 4 * CB / 32;   // K code words per lane per 16-row tile
+    static constexpr int NV = D / 16 * CB / 4;    // V code words per lane
+    static constexpr int MW = MF ? 1 : 2;         // words per (scale, lo) pair
+    uint32_t k[2][WPL];
+    uint32_t km[2][4 * MW];
+    uint32_t v[NV];
+    uint32_t vm[8 * MW];
+};
+
+template <int N>
+__device__ __forceinline__ void load_words(uint32_t (&dst)[N], const uint32_t* src) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int x = 0; x < N / 4; ++x) {
+            const uint4 w = reinterpret_cast<const uint4*>(src)[x];
+            dst[4 * x] = w.x;
+            dst[4 * x + 1] = w.y;
+            dst[4 * x + 2] = w.z;
+            dst[4 * x + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int x = 0; x < N; ++x) dst[x] = src[x];
+    }
 }
 
-template <int D, int CB>
+template <int MF>
+__device__ __forceinline__ GroupMeta pair_of(const uint32_t* w, int k) {
+    if (MF) return {half_bits_to_f32(w[k] & 0xffffu), half_bits_to_f32(w[k] >> 16)};
+    return {__uint_as_float(w[2 * k]), __uint_as_float(w[2 * k + 1])};
+}
+
+template <int D, int CB, int MF>
+__device__ __forceinline__ void load_page(PageRegs<D, CB, MF>& r, const uint8_t* pg, const PageFmt& f, int col, int jj,
+                                          int gmeta) {
+    using R = PageRegs<D, CB, MF>;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        load_words(r.k[a], reinterpret_cast<const uint32_t*>(pg + f.kc + (int64_t)(16 * a + col) * (D * CB / 8)) +
+                               R::WPL * jj);
+        load_words(r.km[a], reinterpret_cast<const uint32_t*>(pg + k_meta_off(f, 16 * a + 4 * jj, gmeta)));
+    }
+    load_words(r.v, reinterpret_cast<const uint32_t*>(pg + f.vc) + (col * 4 + jj) * R::NV);
+    load_words(r.vm, reinterpret_cast<const uint32_t*>(pg + f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB));
+}
+
+template <int D, int CB, int MF>
 __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
                                                               const float* __restrict__ q, int Hq, float scale,
                                                               int rps, int n_splits, float* __restrict__ part,
@@ -219,7 +277,6 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     constexpr int NSTEP = D / 32;     // k-steps of the QK product
     constexpr int NDT = D / 16;       // d-tiles of the PV product
     constexpr int DL = D / 4;         // channels per lane group in QK
-    constexpr int WPL = DL * CB / 32; // code words per lane per K row
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int split = blockIdx.x * 4 + wave;
     if (split >= n_splits) return;
@@ -235,6 +292,7 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     const bool cvalid = col < ncol;
     const int gcol = cvalid ? col / G : 0, hcol = cvalid ? col % G : 0;
     const int hq = h * G + hcol;
+    const int gmeta = min(gcol, NG - 1);
 
     // Q^T columns (group, head) in f16 hi + lo, and the column's q sum
     f16x8_t qhi[NSTEP], qlo[NSTEP];
@@ -260,34 +318,25 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
 #pragma unroll
     for (int t = 0; t < NDT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f, bsum = 0.0f, zsum = 0.0f;
-    const int mf = f.meta_f16;
-    const int gmeta = min(gcol, NG - 1);
 
-    for (int p0 = r_begin; p0 < r_end; p0 += PAGE) {
-        const uint8_t* pg = page_ptr(m, s, layer, h, p0 / PAGE);
-        // ---- QK over the page's two 16-row tiles
+    const uint32_t magic = magic_f16x2();
+    // one page of work on registers already loaded
+    auto step = [&](const PageRegs<D, CB, MF>& cur, const int p0) {
+        // ---- QK over the page's two 16-row tiles, folded per (row, group)
         float sv[8];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-            const int i = 16 * a + col;   // A operand row of this lane
-            const uint32_t* kw = reinterpret_cast<const uint32_t*>(pg + f.kc + (int64_t)i * (D * CB / 8)) + WPL * jj;
-            uint32_t kr[WPL];
-#pragma unroll
-            for (int x = 0; x < WPL; ++x) kr[x] = kw[x];
             f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < NSTEP; ++st) {
-                const f16x8_t kv = codes_to_f16_exact<CB>(kr + st * (CB / 4));
+                const f16x8_t kv = codes_to_f16_exact<CB>(cur.k[a] + st * (CB / 4), magic);
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qhi[st], sa, 0, 0, 0);
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qlo[st], sa, 0, 0, 0);
             }
-            // fold this column's group scale/zero for rows 16a + 4jj + r
-            const uint8_t* km = pg + k_meta_off(f, 16 * a + 4 * jj, gmeta);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const GroupMeta mt = meta_at(km, r, mf);
-                const float t = cvalid ? fmaf(mt.scale, sa[r], mt.lo * qsum) : 0.0f;
-                sv[4 * a + r] = t;
+                const GroupMeta mt = pair_of<MF>(cur.km[a], r);
+                sv[4 * a + r] = cvalid ? fmaf(mt.scale, sa[r], mt.lo * qsum) : 0.0f;
             }
         }
         // sum the group columns of each head: lanes (g * G + hcol) of this 16-lane row
@@ -313,25 +362,35 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
+        // Lazy rescale: the reference max only moves when a column's max grows
+        // by more than 6 (so p <= e^6); o, l and the corrections share the
+        // reference, and the combine merges partials on any reference.
+        const bool grow = mx > m_run + 6.0f;
+        if (__any(grow)) {
+            const float m_new = grow ? mx : m_run;
+            const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
+            l_run *= alpha;
+            bsum *= alpha;
+            zsum *= alpha;
+#pragma unroll
+            for (int t = 0; t < NDT; ++t) acc[t] *= alpha;
+            m_run = m_new;
+        }
         float sum = 0.0f;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-            pv[x] = (pv[x] == -INFINITY) ? 0.0f : __expf(pv[x] - m_new);
+            pv[x] = (pv[x] == -INFINITY) ? 0.0f : __expf(pv[x] - m_run);
             sum += pv[x];
         }
         sum += __shfl_xor(sum, 16);
         sum += __shfl_xor(sum, 32);
-        const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
-        l_run = l_run * alpha + sum;
-        m_run = m_new;
+        l_run += sum;
         // ---- PV: B[row (jj, e)][col] = f16(p * scaleV), rows e<4: 4jj+e, e>=4: 16+4jj+e-4
-        const uint8_t* vm = pg + f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB;
         f16x8_t bop;
         float bs = 0.0f, zs = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const GroupMeta mt = meta_at(vm, e, mf);
+            const GroupMeta mt = pair_of<MF>(cur.vm, e);
             const int row = p0 + (e < 4 ? 4 * jj + e : 16 + 4 * jj + e - 4);
             const bool ok = cvalid && row < r_end;
             const _Float16 b = ok ? (_Float16)(pv[e] * mt.scale) : (_Float16)0.0f;
@@ -339,18 +398,30 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
             bs += (float)b;
             zs += ok ? pv[e] * mt.lo : 0.0f;
         }
-        bsum = bsum * alpha + bs;
-        zsum = zsum * alpha + zs;
-        // V^T A operand: lane (d = 16t + col, jj) words ((col*4 + jj)*NDT + t)
-        const uint32_t* vw = reinterpret_cast<const uint32_t*>(pg + f.vc) + ((col * 4 + jj) * NDT) * (CB / 4);
-        uint32_t vr[NDT * (CB / 4)];
-#pragma unroll
-        for (int x = 0; x < NDT * (CB / 4); ++x) vr[x] = vw[x];
+        bsum += bs;
+        zsum += zs;
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-            const f16x8_t av = codes_to_f16<CB>(vr + t * (CB / 4));
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t] * alpha, 0, 0, 0);
+            const f16x8_t av = codes_to_f16<CB>(cur.v + t * (CB / 4), magic);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t], 0, 0, 0);
         }
+    };
+    // pages k and k+1 are in flight while page k is computed: three register
+    // buffers rotate through an unrolled-by-3 loop
+    const int np = (r_end - r_begin + PAGE - 1) / PAGE;
+    const int pg0 = r_begin / PAGE;
+    auto fetch = [&](PageRegs<D, CB, MF>& b, int k) {
+        if (k < np) load_page(b, page_ptr(m, s, layer, h, pg0 + k), f, col, jj, gmeta);
+    };
+    // page k+1 is in flight while page k is computed (two buffers, unrolled by 2)
+    PageRegs<D, CB, MF> b0, b1;
+    fetch(b0, 0);
+    for (int k = 0; k < np; k += 2) {
+        fetch(b1, k + 1);
+        step(b0, r_begin + k * PAGE);
+        if (k + 1 >= np) break;
+        fetch(b0, k + 2);
+        step(b1, r_begin + (k + 1) * PAGE);
     }
     // totals of the per-column corrections over the 4 lane groups
     bsum += __shfl_xor(bsum, 16);
@@ -470,19 +541,21 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     hipStream_t st = as_stream(stream);
     if (fast_path(m, cfg, n_q_heads)) {
         const dim3 grid((ns + 3) / 4, m.n_kv_heads, m.batch);
-        const int cb = cfg.bits == 8 ? 8 : 4;
-        if (m.head_dim == 128 && cb == 4)
-            hipLaunchKernelGGL((draft_attn_mfma_kernel<128, 4>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
-                               scale, rps, ns, part, logits);
-        else if (m.head_dim == 128)
-            hipLaunchKernelGGL((draft_attn_mfma_kernel<128, 8>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
-                               scale, rps, ns, part, logits);
-        else if (cb == 4)
-            hipLaunchKernelGGL((draft_attn_mfma_kernel<64, 4>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
-                               scale, rps, ns, part, logits);
-        else
-            hipLaunchKernelGGL((draft_attn_mfma_kernel<64, 8>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads,
-                               scale, rps, ns, part, logits);
+        const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
+#define DKV_LAUNCH(DD, CC, MM)                                                                                    \
+    hipLaunchKernelGGL((draft_attn_mfma_kernel<DD, CC, MM>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads, \
+                       scale, rps, ns, part, logits)
+        switch (key) {
+            case 0: DKV_LAUNCH(64, 4, 0); break;
+            case 1: DKV_LAUNCH(64, 4, 1); break;
+            case 2: DKV_LAUNCH(64, 8, 0); break;
+            case 3: DKV_LAUNCH(64, 8, 1); break;
+            case 4: DKV_LAUNCH(128, 4, 0); break;
+            case 5: DKV_LAUNCH(128, 4, 1); break;
+            case 6: DKV_LAUNCH(128, 8, 0); break;
+            default: DKV_LAUNCH(128, 8, 1); break;
+        }
+#undef DKV_LAUNCH
     } else {
         hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
                            m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
