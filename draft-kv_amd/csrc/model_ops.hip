@@ -1,0 +1,285 @@
+// Elementwise and normalisation kernels of the three model forwards, plus a
+// batch-invariant float32 GEMM.
+// Reference: draftkv/model.py:18-25,100-133 (RMSNorm, sinusoidal positions,
+// ReLU MLP), draftkv/gpt2.py:114-127,182-213 (LayerNorm, GELU-tanh, learned
+// positions), draftkv/llama.py:93-109,164-172,175-225 (RMSNorm, RoPE, SiLU).
+//
+// Activations are float32 rows; inputs that come out of a bf16 GEMM may be
+// bf16, and outputs that feed a bf16 GEMM may be written as bf16 (RNE).
+#include "dkv_common.h"
+
+namespace dkv {
+
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float v, int dtype) {
+    if (dtype == DKV_BF16)
+        reinterpret_cast<uint16_t*>(base)[i] = f32_to_bf16_rne(v);
+    else
+        reinterpret_cast<float*>(base)[i] = v;
+}
+
+__device__ __forceinline__ float bias_at(const void* bias, int64_t i, int dtype) {
+    return bias ? load_elem(bias, i, dtype) : 0.0f;
+}
+
+// Sum over the block (256 threads = 4 waves); every thread gets the total.
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+// h[r] = table[tok[r]] (+ pos_table[pos[r]])
+__global__ void __launch_bounds__(256) embed_kernel(const void* __restrict__ table, int tdt,
+                                                    const int32_t* __restrict__ tokens, int d,
+                                                    const void* __restrict__ pos_table,
+                                                    const int32_t* __restrict__ positions, float* __restrict__ out) {
+    const int r = blockIdx.x;
+    const int64_t t = tokens[r];
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float v = load_elem(table, t * d + i, tdt);
+        if (pos_table) v += load_elem(pos_table, (int64_t)positions[r] * d + i, tdt);
+        out[(int64_t)r * d + i] = v;
+    }
+}
+
+// out = x / sqrt(mean(x*x) + eps) * w
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, const void* __restrict__ w, int wdt,
+                                                      int d, float eps, void* out, int odt) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float* xr = x + (int64_t)r * d;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) ss += xr[i] * xr[i];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / d + eps);
+    for (int i = threadIdx.x; i < d; i += blockDim.x)
+        store_elem(out, (int64_t)r * d + i, xr[i] * inv * load_elem(w, i, wdt), odt);
+}
+
+// out = (x - mean) / sqrt(var + eps) * w + b
+__global__ void __launch_bounds__(256) layernorm_kernel(const float* __restrict__ x, const void* __restrict__ w,
+                                                        const void* __restrict__ b, int wdt, int d, float eps,
+                                                        void* out, int odt) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float* xr = x + (int64_t)r * d;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) s += xr[i];
+    const float mu = block_sum(s, red) / d;
+    float v = 0.0f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) v += (xr[i] - mu) * (xr[i] - mu);
+    const float var = block_sum(v, red) / d;
+    const float inv = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < d; i += blockDim.x)
+        store_elem(out, (int64_t)r * d + i, (xr[i] - mu) * inv * load_elem(w, i, wdt) + load_elem(b, i, wdt), odt);
+}
+
+// Split a fused projection row [q heads | k heads | v heads] (+ bias) into
+// float32 q [r][hq][d], k [r][hkv][d], v [r][hkv][d], applying rotate-half
+// RoPE to q and k when a cos/sin table is given: out[j] = x[j]c[j] - x[j+h]s[j],
+// out[j+h] = x[j+h]c[j] + x[j]s[j] with h = d/2.
+__global__ void __launch_bounds__(256) qkv_split_kernel(const void* __restrict__ qkv, int xdt,
+                                                        const void* __restrict__ bias, int bdt, int hq, int hkv,
+                                                        int d, const int32_t* __restrict__ positions,
+                                                        const float* __restrict__ cs, int max_pos,
+                                                        float* __restrict__ q, float* __restrict__ k,
+                                                        float* __restrict__ v) {
+    const int r = blockIdx.x;
+    const int n = (hq + 2 * hkv) * d;
+    const int64_t base = (int64_t)r * n;
+    if (!cs) {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float x = load_elem(qkv, base + i, xdt) + bias_at(bias, i, bdt);
+            const int head = i / d, c = i % d;
+            if (head < hq)
+                q[((int64_t)r * hq + head) * d + c] = x;
+            else if (head < hq + hkv)
+                k[((int64_t)r * hkv + head - hq) * d + c] = x;
+            else
+                v[((int64_t)r * hkv + head - hq - hkv) * d + c] = x;
+        }
+        return;
+    }
+    const int half = d / 2;
+    const int64_t p = positions[r];
+    const float* cr = cs + p * half;
+    const float* sr = cs + (int64_t)max_pos * half + p * half;
+    // q and k heads: one thread per rotation pair
+    for (int i = threadIdx.x; i < (hq + hkv) * half; i += blockDim.x) {
+        const int head = i / half, j = i % half;
+        const int c0 = head * d + j, c1 = c0 + half;
+        const float a = load_elem(qkv, base + c0, xdt) + bias_at(bias, c0, bdt);
+        const float b = load_elem(qkv, base + c1, xdt) + bias_at(bias, c1, bdt);
+        const float o0 = a * cr[j] - b * sr[j];
+        const float o1 = b * cr[j] + a * sr[j];
+        float* dst = head < hq ? q + ((int64_t)r * hq + head) * d : k + ((int64_t)r * hkv + head - hq) * d;
+        dst[j] = o0;
+        dst[j + half] = o1;
+    }
+    for (int i = threadIdx.x; i < hkv * d; i += blockDim.x) {
+        const int c = (hq + hkv) * d + i;
+        v[(int64_t)r * hkv * d + i] = load_elem(qkv, base + c, xdt) + bias_at(bias, c, bdt);
+    }
+}
+
+// out = silu(gate) * up, gu = [rows][2*ff] (gate, then up)
+__global__ void __launch_bounds__(256) silu_mul_kernel(const void* __restrict__ gu, int gdt, int ff, void* out,
+                                                       int odt) {
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < ff; i += blockDim.x) {
+        const float g = load_elem(gu, (int64_t)r * 2 * ff + i, gdt);
+        const float u = load_elem(gu, (int64_t)r * 2 * ff + ff + i, gdt);
+        store_elem(out, (int64_t)r * ff + i, g / (1.0f + __expf(-g)) * u, odt);
+    }
+}
+
+// out = gelu_tanh(x + bias)
+__global__ void __launch_bounds__(256) bias_gelu_kernel(const void* __restrict__ x, int xdt,
+                                                        const void* __restrict__ bias, int bdt, int n, void* out,
+                                                        int odt) {
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
+        const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+        store_elem(out, (int64_t)r * n + i, 0.5f * v * (1.0f + tanhf(u)), odt);
+    }
+}
+
+// out = max(x, 0)
+__global__ void __launch_bounds__(256) relu_kernel(const void* __restrict__ x, int xdt, int n, void* out, int odt) {
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        store_elem(out, (int64_t)r * n + i, fmaxf(load_elem(x, (int64_t)r * n + i, xdt), 0.0f), odt);
+}
+
+// h += x (+ bias)
+__global__ void __launch_bounds__(256) add_kernel(float* h, const void* __restrict__ x, int xdt,
+                                                  const void* __restrict__ bias, int bdt, int n) {
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        h[(int64_t)r * n + i] += load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
+}
+
+// out[m][n] (+)= sum_k x[m][k] * w(k, n) (+ bias[n]), one thread per output,
+// k in order, so a row's result never depends on how many rows share the
+// launch. w_layout 0: w[k][n]; 1: w[n][k].
+constexpr int GT = 16;
+__global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       int wl, int M, int N, int K, const void* __restrict__ bias,
+                                                       int bdt, float* out, int accumulate) {
+    __shared__ float sx[GT][GT + 1];
+    __shared__ float sw[GT][GT + 1];
+    const int tm = threadIdx.x / GT, tn = threadIdx.x % GT;
+    const int m = blockIdx.y * GT + tm, n = blockIdx.x * GT + tn;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += GT) {
+        const int kx = k0 + tn;
+        sx[tm][tn] = (m < M && kx < K) ? x[(int64_t)m * K + kx] : 0.0f;
+        // w tile sw[kk][nn]; for layout 1 consecutive threads walk k so the load is row-contiguous
+        if (wl == 0) {
+            const int kw = k0 + tm, nw = blockIdx.x * GT + tn;
+            sw[tm][tn] = (kw < K && nw < N) ? w[(int64_t)kw * N + nw] : 0.0f;
+        } else {
+            const int kw = k0 + tn, nw = blockIdx.x * GT + tm;
+            sw[tn][tm] = (kw < K && nw < N) ? w[(int64_t)nw * K + kw] : 0.0f;
+        }
+        __syncthreads();
+        const int kmax = min(GT, K - k0);
+        for (int kk = 0; kk < kmax; ++kk) acc = fmaf(sx[tm][kk], sw[kk][tn], acc);
+        __syncthreads();
+    }
+    if (m < M && n < N) {
+        const float b = bias_at(bias, n, bdt);
+        const int64_t o = (int64_t)m * N + n;
+        out[o] = accumulate ? out[o] + (acc + b) : acc + b;
+    }
+}
+
+}  // namespace dkv
+
+using namespace dkv;
+
+#define DKV_ROWS_LAUNCH(kernel, rows, ...)                                                         \
+    do {                                                                                           \
+        if ((rows) <= 0) return DKV_OK;                                                            \
+        hipLaunchKernelGGL(kernel, dim3(rows), dim3(256), 0, as_stream(stream), __VA_ARGS__);      \
+        return check_launch(#kernel);                                                              \
+    } while (0)
+
+static bool dtype_ok(int32_t dt) { return dt == DKV_F32 || dt == DKV_BF16; }
+
+extern "C" int dkv_embed(const void* table, int32_t table_dtype, const int32_t* tokens, int32_t rows, int32_t d,
+                         const void* pos_table, const int32_t* positions, float* out, dkv_stream_t stream) {
+    DKV_REQUIRE(table && tokens && out && d > 0 && dtype_ok(table_dtype), "dkv_embed: bad arguments");
+    DKV_REQUIRE(!pos_table || positions, "dkv_embed: positions needed with a position table");
+    DKV_ROWS_LAUNCH(embed_kernel, rows, table, table_dtype, tokens, d, pos_table, positions, out);
+}
+
+extern "C" int dkv_rmsnorm(const float* x, const void* w, int32_t w_dtype, int32_t rows, int32_t d, float eps,
+                           void* out, int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(x && w && out && d > 0 && dtype_ok(w_dtype) && dtype_ok(out_dtype), "dkv_rmsnorm: bad arguments");
+    DKV_ROWS_LAUNCH(rmsnorm_kernel, rows, x, w, w_dtype, d, eps, out, out_dtype);
+}
+
+extern "C" int dkv_layernorm(const float* x, const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d,
+                             float eps, void* out, int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(x && w && b && out && d > 0 && dtype_ok(w_dtype) && dtype_ok(out_dtype),
+                "dkv_layernorm: bad arguments");
+    DKV_ROWS_LAUNCH(layernorm_kernel, rows, x, w, b, w_dtype, d, eps, out, out_dtype);
+}
+
+extern "C" int dkv_qkv_split(const void* qkv, int32_t qkv_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t d, const int32_t* positions,
+                             const float* cos_sin, int32_t max_pos, float* q, float* k, float* v,
+                             dkv_stream_t stream) {
+    DKV_REQUIRE(qkv && q && k && v && d > 0 && n_q_heads > 0 && n_kv_heads > 0 && dtype_ok(qkv_dtype),
+                "dkv_qkv_split: bad arguments");
+    DKV_REQUIRE(!bias || dtype_ok(bias_dtype), "dkv_qkv_split: bad bias dtype");
+    DKV_REQUIRE(!cos_sin || (positions && d % 2 == 0 && max_pos > 0), "dkv_qkv_split: RoPE needs positions, even d");
+    DKV_ROWS_LAUNCH(qkv_split_kernel, rows, qkv, qkv_dtype, bias, bias_dtype, n_q_heads, n_kv_heads, d, positions,
+                    cos_sin, max_pos, q, k, v);
+}
+
+extern "C" int dkv_silu_mul(const void* gate_up, int32_t gate_up_dtype, int32_t rows, int32_t ff, void* out,
+                            int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(gate_up && out && ff > 0 && dtype_ok(gate_up_dtype) && dtype_ok(out_dtype),
+                "dkv_silu_mul: bad arguments");
+    DKV_ROWS_LAUNCH(silu_mul_kernel, rows, gate_up, gate_up_dtype, ff, out, out_dtype);
+}
+
+extern "C" int dkv_bias_gelu(const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
+                             int32_t n, void* out, int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(x && out && n > 0 && dtype_ok(x_dtype) && dtype_ok(out_dtype) && (!bias || dtype_ok(bias_dtype)),
+                "dkv_bias_gelu: bad arguments");
+    DKV_ROWS_LAUNCH(bias_gelu_kernel, rows, x, x_dtype, bias, bias_dtype, n, out, out_dtype);
+}
+
+extern "C" int dkv_relu(const void* x, int32_t x_dtype, int32_t rows, int32_t n, void* out, int32_t out_dtype,
+                        dkv_stream_t stream) {
+    DKV_REQUIRE(x && out && n > 0 && dtype_ok(x_dtype) && dtype_ok(out_dtype), "dkv_relu: bad arguments");
+    DKV_ROWS_LAUNCH(relu_kernel, rows, x, x_dtype, n, out, out_dtype);
+}
+
+extern "C" int dkv_add(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
+                       int32_t n, dkv_stream_t stream) {
+    DKV_REQUIRE(h && x && n > 0 && dtype_ok(x_dtype) && (!bias || dtype_ok(bias_dtype)), "dkv_add: bad arguments");
+    DKV_ROWS_LAUNCH(add_kernel, rows, h, x, x_dtype, bias, bias_dtype, n);
+}
+
+extern "C" int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, int32_t N, int32_t K,
+                            const void* bias, int32_t bias_dtype, float* out, int32_t accumulate,
+                            dkv_stream_t stream) {
+    DKV_REQUIRE(x && w && out && N > 0 && K > 0 && (w_layout == 0 || w_layout == 1), "dkv_gemm_f32: bad arguments");
+    DKV_REQUIRE(!bias || dtype_ok(bias_dtype), "dkv_gemm_f32: bad bias dtype");
+    DKV_REQUIRE(M <= 65535 * GT, "dkv_gemm_f32: too many rows for one launch");
+    if (M <= 0) return DKV_OK;
+    const dim3 grid((N + GT - 1) / GT, (M + GT - 1) / GT);
+    hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(GT * GT), 0, as_stream(stream), x, w, w_layout, M, N, K, bias,
+                       bias_dtype, out, accumulate);
+    return check_launch("dkv_gemm_f32");
+}

@@ -9,13 +9,16 @@ running in a gfx950 HIP library (``_lib/libdraftkv_hip.so``).
 from .compress import CompressedKVCache, FullKVCache, quantize
 from .config import CompressionConfig, LayerPlan, default_arms
 from .controller import DepthThompsonController, FixedPolicy, FlatBandit, OraclePolicy, ThompsonController
+from .engine import DraftKVEngine, GenerationResult, RoundLog
+from .model import TinyTransformer
 from .paged import BlockPool, BlockPoolExhausted, PagedKVCache, plan_blocks_needed
 from .throughput import CostModel, best_gamma, best_gamma_profile, expected_tokens, expected_tokens_profile
 
 __all__ = [
     "BlockPool", "BlockPoolExhausted", "CompressedKVCache", "CompressionConfig", "CostModel",
-    "DepthThompsonController", "FixedPolicy", "FlatBandit", "FullKVCache", "LayerPlan", "OraclePolicy",
-    "PagedKVCache", "ThompsonController", "best_gamma", "best_gamma_profile", "default_arms",
-    "expected_tokens", "expected_tokens_profile", "plan_blocks_needed", "quantize",
+    "DepthThompsonController", "DraftKVEngine", "FixedPolicy", "FlatBandit", "FullKVCache", "GenerationResult",
+    "LayerPlan", "OraclePolicy", "PagedKVCache", "RoundLog", "ThompsonController", "TinyTransformer", "best_gamma",
+    "best_gamma_profile", "default_arms", "expected_tokens", "expected_tokens_profile", "plan_blocks_needed",
+    "quantize",
 ]
 __version__ = "0.1.0"

@@ -55,6 +55,15 @@ _SIGS = {
     "dkv_sample": (C.c_int, [P, I64, I32, I32, F32, P, P, P, SZ, P]),
     "dkv_accept_workspace": (SZ, [I32, I32, I32]),
     "dkv_accept": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P, SZ, P]),
+    "dkv_embed": (C.c_int, [P, I32, P, I32, I32, P, P, P, P]),
+    "dkv_rmsnorm": (C.c_int, [P, P, I32, I32, I32, F32, P, I32, P]),
+    "dkv_layernorm": (C.c_int, [P, P, P, I32, I32, I32, F32, P, I32, P]),
+    "dkv_qkv_split": (C.c_int, [P, I32, P, I32, I32, I32, I32, I32, P, P, I32, P, P, P, P]),
+    "dkv_silu_mul": (C.c_int, [P, I32, I32, I32, P, I32, P]),
+    "dkv_bias_gelu": (C.c_int, [P, I32, P, I32, I32, I32, P, I32, P]),
+    "dkv_relu": (C.c_int, [P, I32, I32, I32, P, I32, P]),
+    "dkv_add": (C.c_int, [P, P, I32, P, I32, I32, I32, P]),
+    "dkv_gemm_f32": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P]),
     "dkv_last_error": (C.c_char_p, []),
     "dkv_version": (I32, []),
 }

@@ -1,0 +1,263 @@
+"""One decoder forward for the three model families, on the GPU.
+
+The reference has three numpy forwards that differ only in their pieces
+(draftkv/model.py:100-133, draftkv/gpt2.py:182-213, draftkv/llama.py:175-225):
+norm (RMSNorm / LayerNorm), positions (sinusoidal or learned table added to the
+embedding / RoPE on q and k), MLP (ReLU / GELU-tanh with biases / SwiGLU),
+optional projection biases, and the LM head (own matrix / tied embedding).
+``Decoder`` runs any combination on device buffers:
+
+* float32 weights: every product goes through ``dkv_gemm_f32`` (one in-order
+  reduction per output), so a row's logits do not depend on how many rows
+  share the pass -- the verify pass and one-token decoding agree bit for bit,
+  which is what makes greedy self-speculative decoding exactly lossless.
+* bfloat16 weights: the projections run as bf16 GEMMs on the matrix cores
+  (``torch.nn.functional.linear``); norms, RoPE, activations and residual adds
+  stay in the HIP kernels with float32 activations.
+
+Attention and the K/V writes go to the cache the forward is handed: the
+device-paged full cache (``PagedKVCache`` / ``FullKVCache``) or the drafter
+mirror (``CompressedKVCache``). ``forward(tokens, cache, start_pos)`` is the
+reference's single-sequence signature (numpy in, numpy (T, V) float32 out);
+``forward_batch`` is the batched device form the engine uses.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .compress import CompressedKVCache, FullKVCache
+from .paged import PagedKVCache, default_device
+
+
+def _t(x, device, dtype) -> Optional[torch.Tensor]:
+    if x is None:
+        return None
+    if torch.is_tensor(x):
+        return x.to(device=device, dtype=dtype).contiguous()
+    return torch.as_tensor(np.ascontiguousarray(np.asarray(x, np.float32))).to(device=device, dtype=dtype)
+
+
+class Layer:
+    """Device weights of one block. ``w*`` are stored [N, K] (layout 1) or
+    [K, N] (layout 0) as given; bf16 models always hold [N, K]."""
+
+    __slots__ = ("n1w", "n1b", "wqkv", "bqkv", "wo", "bo", "n2w", "n2b", "w1", "b1", "w2", "b2")
+
+
+class Decoder:
+    """Shared forward; subclasses fill the spec in their constructors.
+
+    Spec attributes: ``n_layers, d_model, n_heads, n_kv_heads, d_head,
+    vocab_size, eps, norm ('rms'|'layer'), mlp ('relu'|'gelu'|'swiglu'),
+    layout`` (0: weights [K, N] as ``x @ W``; 1: [N, K] as ``x @ W.T``),
+    ``emb, pos_table, rope_theta, head, head_layout, layers, nfw, nfb``.
+    """
+
+    norm = "rms"
+    mlp = "swiglu"
+    rope_theta: Optional[float] = None
+
+    # ------------------------------------------------------------ setup
+    def _setup_device(self, dtype, device) -> None:
+        self.device = torch.device(device) if device is not None else default_device()
+        self.wdtype = dtype
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("dtype must be torch.float32 or torch.bfloat16")
+        self.act_dtype = dtype           # dtype of GEMM inputs
+        self.kv_dtype = dtype            # dtype of the full cache
+        self._cs: Optional[torch.Tensor] = None
+        self._cs_len = 0
+
+    def _w(self, x, layout: int) -> torch.Tensor:
+        """Upload a weight matrix; bf16 models keep every matrix as [N, K]."""
+        t = _t(x, self.device, self.wdtype)
+        if self.wdtype == torch.bfloat16 and layout == 0:
+            t = t.t().contiguous()
+        return t
+
+    def _v(self, x) -> Optional[torch.Tensor]:
+        return _t(x, self.device, self.wdtype)
+
+    @property
+    def w_layout(self) -> int:
+        return 1 if self.wdtype == torch.bfloat16 else self.layout
+
+    def new_cache(self, batch: int = 1, max_tokens: int = 1 << 20) -> FullKVCache:
+        return FullKVCache(self.n_layers, self.n_kv_heads, self.d_head, dtype=self.kv_dtype, batch=batch,
+                           max_tokens=max_tokens, device=self.device)
+
+    # ------------------------------------------------------------ RoPE table
+    def _cos_sin(self, need: int):
+        """cos table then sin table, float32 [2, n, d/2], computed in float64 as
+        llama.py:164-172 does (the two halves of the reference's table are equal)."""
+        if self._cs is None or self._cs_len < need:
+            n = max(1024, 1 << (need - 1).bit_length())
+            D = self.d_head
+            inv = 1.0 / (self.rope_theta ** (np.arange(0, D, 2) / D))
+            ang = np.outer(np.arange(n), inv)
+            cs = np.stack([np.cos(ang), np.sin(ang)]).astype(np.float32)
+            self._cs = torch.as_tensor(cs).to(self.device)
+            self._cs_len = n
+        return self._cs, self._cs_len
+
+    # ------------------------------------------------------------ pieces
+    def _norm(self, h: torch.Tensor, w, b) -> torch.Tensor:
+        if self.norm == "rms":
+            return ops.rmsnorm(h, w, self.eps, self.act_dtype)
+        return ops.layernorm(h, w, b, self.eps, self.act_dtype)
+
+    def _proj(self, x: torch.Tensor, w: torch.Tensor, bias=None) -> torch.Tensor:
+        """x @ W (+ bias); float32 out for float32 models, bf16 out for bf16 models."""
+        if self.wdtype == torch.float32:
+            return ops.gemm_f32(x, w, self.layout, bias)
+        return F.linear(x, w, bias)
+
+    def _proj_add(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias=None) -> None:
+        """h += x @ W (+ bias)."""
+        if self.wdtype == torch.float32:
+            ops.gemm_f32(x, w, self.layout, bias, out=h, accumulate=True)
+        else:
+            ops.add_(h, F.linear(x, w), bias)
+
+    def _mlp(self, h: torch.Tensor, p: Layer) -> None:
+        x = self._norm(h, p.n2w, p.n2b)
+        if self.mlp == "swiglu":
+            a = ops.silu_mul(self._proj(x, p.w1), self.act_dtype)
+        elif self.mlp == "gelu":
+            a = ops.bias_gelu(self._proj(x, p.w1), p.b1, self.act_dtype)
+        else:
+            a = ops.relu(self._proj(x, p.w1), self.act_dtype)
+        self._proj_add(h, a, p.w2, p.b2)
+
+    def _head(self, h: torch.Tensor) -> torch.Tensor:
+        x = self._norm(h, self.nfw, self.nfb)
+        if self.wdtype == torch.float32:
+            return ops.gemm_f32(x, self.head, self.head_layout)
+        return F.linear(x, self.head).float()
+
+    # ------------------------------------------------------------ forward
+    def forward_batch(self, tokens: torch.Tensor, cache, start: Sequence[int],
+                      count: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """Run ``tokens`` [batch, T] (int32, on the device) at positions
+        start[s] .. start[s]+T-1 and return float32 logits [batch, T, vocab].
+
+        The first ``count[s]`` rows of sequence s (default all T) are appended to
+        ``cache``; the other rows are computed and their outputs are undefined
+        (the engine uses count 0 for sequences that are done). With the drafter
+        mirror T must be 1."""
+        b, T = tokens.shape
+        st = np.asarray(start, np.int64).reshape(b)
+        ct = np.full(b, T, np.int64) if count is None else np.asarray(count, np.int64).reshape(b)
+        if np.any(ct < 0) or np.any(ct > T):
+            raise ValueError("count must lie in [0, T]")
+        st = np.where(ct > 0, st, 0)          # finished sequences attend over a harmless prefix
+        pos = (st[:, None] + np.arange(T)[None, :]).astype(np.int32)
+        max_pos = int(pos.max()) + 1 if pos.size else 0
+        if self.pos_table is not None and max_pos > self.pos_table.shape[0]:
+            raise IndexError(f"position {max_pos - 1} beyond the position table ({self.pos_table.shape[0]})")
+        dev = self.device
+        positions = torch.as_tensor(pos.reshape(-1)).to(dev, non_blocking=True)
+        tok = tokens.reshape(-1).to(torch.int32).contiguous()
+        R = b * T
+        cs, cs_len = (None, 0)
+        if self.rope_theta is not None:
+            cs, cs_len = self._cos_sin(max_pos)
+
+        if isinstance(cache, CompressedKVCache):
+            attn = self._mirror_attention(cache, b, T, st, ct)
+        elif isinstance(cache, PagedKVCache):
+            attn = self._paged_attention(cache, b, T, st, ct, max_pos)
+        else:
+            raise TypeError(f"unsupported cache type {type(cache).__name__}: the GPU forward runs against "
+                            "draftkv.paged.PagedKVCache / compress.FullKVCache / compress.CompressedKVCache")
+
+        h = ops.embed(self.emb, tok, self.pos_table, positions if self.pos_table is not None else None)
+        Hq, Hkv, D = self.n_heads, self.n_kv_heads, self.d_head
+        for L, p in enumerate(self.layers):
+            x = self._norm(h, p.n1w, p.n1b)
+            q, k, v = ops.qkv_split(self._proj(x, p.wqkv), p.bqkv, Hq, Hkv, D, positions, cs, cs_len)
+            a = attn(L, q.view(b, T, Hq, D), k.view(b, T, Hkv, D), v.view(b, T, Hkv, D)).view(R, Hq * D)
+            if self.act_dtype != torch.float32:
+                a = a.to(self.act_dtype)
+            self._proj_add(h, a, p.wo, p.bo)
+            self._mlp(h, p)
+        logits = self._head(h).view(b, T, self.vocab_size)
+        attn.finish()
+        return logits
+
+    # ------------------------------------------------------------ caches
+    def _paged_attention(self, cache: PagedKVCache, b, T, st, ct, max_pos):
+        if isinstance(cache, FullKVCache) and not cache._ready:
+            cache._init(self.n_kv_heads, self.d_head)
+        if cache.batch != b:
+            raise ValueError(f"cache batch {cache.batch} != token batch {b}")
+        if cache.n_heads != self.n_kv_heads or cache.d_head != self.d_head:
+            raise ValueError("cache heads/width do not match the model")
+        if max_pos > cache.max_tokens:
+            raise ValueError(f"positions up to {max_pos} exceed the cache's max_tokens={cache.max_tokens}")
+        have = cache.n_tokens[:, 0]
+        for s in range(b):
+            if ct[s] > 0 and st[s] != have[s]:
+                raise ValueError(f"sequence {s}: rows must be appended at the cache end "
+                                 f"(start {st[s]}, cache holds {have[s]})")
+        cache.reserve(ct)
+        start_d = torch.as_tensor(st.astype(np.int32)).to(self.device, non_blocking=True)
+        count_d = None if np.all(ct == T) else torch.as_tensor(ct.astype(np.int32)).to(self.device, non_blocking=True)
+
+        def attn(L, q, k, v):
+            cache.append_layer(L, k, v, start_d, count_d)
+            return cache.attend(L, q, start_d, max_pos)
+
+        attn.finish = lambda: cache.commit(ct)
+        return attn
+
+    def _mirror_attention(self, cache: CompressedKVCache, b, T, st, ct):
+        if T != 1:
+            raise ValueError("the drafter mirror takes one row per sequence per forward")
+        if not cache._ready:
+            cache.batch = b
+            cache.seen = np.zeros(b, np.int64)
+            cache._alloc(self.n_kv_heads, self.d_head, max(cache._cap_hint or 0, 4096))
+        if cache.batch != b:
+            raise ValueError(f"mirror batch {cache.batch} != token batch {b}")
+        need = int((st + ct).max()) if b else 0
+        if need > cache.cap:                 # a segment never holds more rows than positions
+            cache._regrow(max(2 * cache.cap, need))
+        budgets = cache.begin_step(st, ct)
+        start_d = torch.as_tensor(st.astype(np.int32)).to(self.device, non_blocking=True)
+        count_d = None if np.all(ct == 1) else torch.as_tensor(ct.astype(np.int32)).to(self.device, non_blocking=True)
+
+        def attn(L, q, k, v):
+            cache.append_layer(L, k, v, start_d, budgets[L], count_d)
+            return cache.attend(L, q.view(b, self.n_heads, self.d_head))
+
+        attn.finish = lambda: None
+        return attn
+
+    # ------------------------------------------------------------ reference protocol
+    def forward(self, tokens, cache, start_pos: int) -> np.ndarray:
+        """Reference signature: ``tokens`` (T,) at positions [start_pos,
+        start_pos+T) of a batch-1 cache; returns numpy logits (T, vocab) float32."""
+        tok = np.asarray(tokens, np.int64).reshape(-1)
+        if tok.size and (tok.min() < 0 or tok.max() >= self.vocab_size):
+            raise IndexError("token id out of range")
+        t = torch.as_tensor(tok.astype(np.int32)).to(self.device)[None]
+        if isinstance(cache, PagedKVCache) and getattr(cache, "batch", 1) != 1:
+            raise ValueError("forward() is the batch-1 protocol; use forward_batch")
+        return self.forward_batch(t, cache, [start_pos]).cpu().numpy()[0]
+
+    def logits_to_probs(self, logits: np.ndarray, temperature: float = 1.0) -> np.ndarray:   # model.py:135-140
+        if temperature <= 0:
+            out = np.zeros_like(logits)
+            out[..., int(np.argmax(logits, -1))] = 1.0
+            return out
+        x = logits / temperature
+        x = x - x.max(-1, keepdims=True)
+        e = np.exp(x)
+        return e / e.sum(-1, keepdims=True)

@@ -1,0 +1,312 @@
+"""The draft/verify loop on the GPU.
+
+Reference: draftkv/engine.py:25-223. Same invariant -- the caches hold K/V for
+positions 0 .. len(tokens)-2 and the last token is pending -- the same round
+(draft gamma tokens against the compressed mirror, verify gamma+1 rows against
+the full cache, accept, roll back the full cache, resync the mirror) and the
+same results (``GenerationResult``, ``RoundLog``).
+
+What differs is where the work happens. A round runs a whole batch of
+sequences in lockstep: every forward, sample and accept decision is a device
+launch over the batch, and the host reads back one small block per round
+(accepted counts, next tokens, draft tokens, uniforms consumed) to do the
+bookkeeping the reference does in Python.
+
+Random numbers follow the reference's stream exactly: sequence s draws from
+``np.random.default_rng(seed + s)`` (sequence 0 is the reference's
+``self.rng``). A round pre-draws its uniforms on the host -- one per draft
+sample, then up to gamma accept tests plus one final sample -- and afterwards
+rewinds the generator and advances it by the number the device decisions
+consumed, so the stream stays where the reference's would be.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import ops
+from .compress import CompressedKVCache
+from .config import CompressionConfig
+from .controller import Controller, FixedPolicy
+
+
+def _layer_cfgs(cfg, n_layers: int) -> list:                        # engine.py:31-33
+    return list(cfg.cfgs) if hasattr(cfg, "cfgs") else [cfg] * n_layers
+
+
+@dataclass
+class RoundLog:                                                     # engine.py:44-50
+    cfg: CompressionConfig
+    gamma: int
+    accepted: int
+    emitted: int
+    ctx: int
+
+
+@dataclass
+class GenerationResult:                                             # engine.py:53-73
+    tokens: list
+    rounds: list = field(default_factory=list)
+    draft_steps: int = 0
+    verify_passes: int = 0
+    cache_rebuilds: int = 0
+    layers_rebuilt: int = 0
+
+    @property
+    def new_tokens(self) -> int:
+        return sum(r.emitted for r in self.rounds)
+
+    @property
+    def acceptance_rate(self) -> float:
+        drafted = sum(r.gamma for r in self.rounds)
+        return sum(r.accepted for r in self.rounds) / drafted if drafted else float("nan")
+
+    @property
+    def tokens_per_verify(self) -> float:
+        return self.new_tokens / self.verify_passes if self.verify_passes else float("nan")
+
+
+class DraftKVEngine:
+    """Self-speculative decoding where the drafter is the target model reading
+    a compressed copy of its own KV cache (engine.py:76-99). Greedy output is
+    identical to full-KV decoding; sampled output follows the speculative
+    rejection rule."""
+
+    def __init__(self, model, controller: Optional[Controller] = None, seed: int = 0,
+                 full_cache_factory=None) -> None:
+        self.model = model
+        self.controller = controller or FixedPolicy(CompressionConfig(4, 0.5), 4)
+        self.seed = seed
+        self.rng = np.random.default_rng(seed)
+        self._rngs = {0: self.rng}
+        # swappable authoritative cache (engine.py:96-98); called with no
+        # arguments and must hold as many sequences as the call has prompts
+        self.full_cache_factory = full_cache_factory
+        self.last_full = None       # the full cache of the last call (inspection, tests)
+        self.last_mirror = None
+
+    # ------------------------------------------------------------------ util
+    def _g(self, s: int) -> np.random.Generator:
+        g = self._rngs.get(s)
+        if g is None:
+            g = self._rngs[s] = np.random.default_rng(self.seed + s)
+        return g
+
+    def _new_full(self, batch: int, max_tokens: int):
+        if self.full_cache_factory is not None:
+            c = self.full_cache_factory()
+            if getattr(c, "batch", 1) != batch:
+                raise ValueError(f"full_cache_factory made a cache for {getattr(c, 'batch', 1)} sequences, "
+                                 f"need {batch}")
+            return c
+        return self.model.new_cache(batch=batch, max_tokens=max_tokens)
+
+    def _prefill(self, prompts, full) -> None:
+        lens = np.array([len(p) for p in prompts], np.int64)
+        T = int(lens.max()) - 1
+        if T <= 0:
+            return
+        tk = np.zeros((len(prompts), T), np.int32)
+        for s, p in enumerate(prompts):
+            tk[s, : len(p) - 1] = p[:-1]
+        self.model.forward_batch(torch.as_tensor(tk).to(self.model.device), full, [0] * len(prompts), lens - 1)
+
+    def _pending(self, toks) -> torch.Tensor:
+        return torch.as_tensor(np.array([t[-1] for t in toks], np.int32)).to(self.model.device)
+
+    @staticmethod
+    def _check_prompts(prompts, vocab: int):
+        out = []
+        for p in prompts:
+            p = [int(x) for x in p]
+            if not p:
+                raise ValueError("prompts must hold at least one token")
+            if min(p) < 0 or max(p) >= vocab:
+                raise IndexError("token id out of range")
+            out.append(p)
+        return out
+
+    # -------------------------------------------------------------- baseline
+    def generate_baseline(self, prompt, max_new_tokens: int, temperature: float = 0.0) -> list:
+        """Plain full-KV autoregressive decoding -- the reference output (engine.py:108-119)."""
+        return self.generate_baseline_batch([prompt], max_new_tokens, temperature)[0]
+
+    def generate_baseline_batch(self, prompts: Sequence, max_new_tokens: int, temperature: float = 0.0) -> list:
+        model = self.model
+        toks = self._check_prompts(prompts, model.vocab_size)
+        b = len(toks)
+        full = self._new_full(b, max(len(t) for t in toks) + max_new_tokens + 16)
+        self.last_full = full
+        self._prefill(toks, full)
+        dev = model.device
+        x = self._pending(toks)
+        start = np.array([len(t) - 1 for t in toks], np.int64)
+        out = torch.empty((b, max_new_tokens), dtype=torch.int32, device=dev)
+        u = np.stack([self._g(s).random(max_new_tokens) for s in range(b)], 1) if max_new_tokens else None
+        u_d = torch.as_tensor(np.ascontiguousarray(u)).to(dev) if max_new_tokens else None
+        for i in range(max_new_tokens):
+            logits = model.forward_batch(x[:, None], full, start + i)[:, 0]
+            x = ops.sample(logits, temperature, u_d[i])
+            out[:, i] = x
+        res = out.cpu().numpy()
+        return [toks[s] + [int(v) for v in res[s]] for s in range(b)]
+
+    # --------------------------------------------------------------- draftkv
+    def generate(self, prompt, max_new_tokens: int, temperature: float = 0.0,
+                 context_key: Optional[str] = None) -> GenerationResult:      # engine.py:122-223
+        return self.generate_batch([prompt], max_new_tokens, temperature, context_key)[0]
+
+    def generate_batch(self, prompts: Sequence, max_new_tokens: int, temperature: float = 0.0,
+                       context_key: Optional[str] = None) -> list:
+        """Decode every prompt with self-speculative rounds run in lockstep.
+
+        One controller decision (config, gamma) per round serves the batch;
+        gamma is capped by the largest remaining budget, and each sequence's
+        output is cut to ``max_new_tokens`` at the end (with one prompt this is
+        exactly the reference's cap ``min(gamma, budget - 1)``)."""
+        toks = self._check_prompts(prompts, self.model.vocab_size)
+        plen = np.array([len(t) for t in toks], np.int64)
+        # gamma <= budget - 1, so no round writes past position len(prompt) + max_new - 2
+        full = self._new_full(len(toks), int(plen.max()) + max_new_tokens + 16)
+        self._prefill(toks, full)
+        batch = DecodeBatch(self, toks, full, max_new_tokens, temperature, context_key)
+        while batch.step():
+            pass
+        return batch.results()
+
+
+class DecodeBatch:
+    """A batch in the middle of self-speculative decoding: token lists, the
+    full cache (holding positions 0 .. len-2 of every sequence), the drafter
+    mirror and the per-sequence random streams. ``step()`` runs one round
+    (engine.py:138-221) for every unfinished sequence."""
+
+    def __init__(self, engine: DraftKVEngine, toks: list, full, max_new_tokens: int, temperature: float = 0.0,
+                 context_key: Optional[str] = None) -> None:
+        self.engine, self.model = engine, engine.model
+        self.toks = toks
+        self.full = full
+        engine.last_full = full
+        self.plen = np.array([len(t) for t in toks], np.int64)
+        self.max_new = max_new_tokens
+        self.T = float(temperature)
+        self.key = context_key
+        self.b = len(toks)
+        self.res = [GenerationResult(tokens=toks[s]) for s in range(self.b)]
+        self.comp: Optional[CompressedKVCache] = None
+        self.comp_cfg = None
+        # the mirror never holds more rows per segment than the sequence has positions
+        need = int(self.plen.max()) + max_new_tokens + 16
+        self.cap_tokens = min(int(getattr(full, "max_tokens", need) or need), need)
+        self.last_emitted = 0             # tokens emitted by the last step, summed over the batch
+
+    def _sync(self, start) -> None:
+        self.comp.sync_from(self.full, start)
+
+    def results(self) -> list:
+        for s in range(self.b):
+            del self.toks[s][int(self.plen[s]) + self.max_new:]
+            self.res[s].tokens = self.toks[s]
+        return self.res
+
+    def step(self) -> bool:
+        eng, model, toks, full, res, b, T = self.engine, self.model, self.toks, self.full, self.res, self.b, self.T
+        dev, V = model.device, model.vocab_size
+        n = np.array([len(t) for t in toks], np.int64)          # caches cover 0 .. n-2
+        produced = n - self.plen
+        active = produced < self.max_new
+        self.last_emitted = 0
+        if not active.any():
+            return False
+        act = active.astype(np.int64)
+        budget = np.where(active, self.max_new - produced, 0)
+        ctx = int(n[active].max())
+        cfg, gamma = eng.controller.select(ctx, self.key)
+        gamma = min(int(gamma), max(int(budget.max()) - 1, 0))
+        flen = full.lengths()
+
+        if gamma <= 0:
+            logits = model.forward_batch(eng._pending(toks)[:, None], full, n - 1, act)[:, 0]
+            u = np.array([eng._g(s).random() if active[s] else 0.5 for s in range(b)])
+            tok = ops.sample(logits, T, torch.as_tensor(u).to(dev)).cpu().numpy()
+            for s in np.flatnonzero(active):
+                toks[s].append(int(tok[s]))
+                res[s].verify_passes += 1
+                res[s].rounds.append(RoundLog(cfg, 0, 0, 1, int(n[s])))
+            self.last_emitted = int(active.sum())
+            if self.comp is not None:
+                self._sync(np.where(active, n - 1, full.lengths()))
+            return True
+
+        # -- drafter's cache: build once, then rebuild only the layers that changed
+        if self.comp is None:
+            self.comp = CompressedKVCache(model.n_layers, cfg, batch=b, cap=self.cap_tokens, device=dev)
+            self.comp.sync_from(full, 0)
+            self.comp_cfg = cfg
+            for r in res:
+                r.cache_rebuilds += 1
+        elif self.comp_cfg != cfg:
+            old, new = _layer_cfgs(self.comp_cfg, model.n_layers), _layer_cfgs(cfg, model.n_layers)
+            changed = [L for L in range(model.n_layers) if old[L] != new[L]]
+            self.comp.rebuild_layers(full, changed, new)
+            self.comp_cfg = cfg
+            for r in res:
+                r.cache_rebuilds += 1
+                r.layers_rebuilt += len(changed)
+        comp = self.comp
+        eng.last_mirror = comp
+
+        # -- uniforms: gamma draft samples, then gamma+1 for verify
+        states = {}
+        u_draft = np.full((gamma, b), 0.5)
+        u_ver = np.full((b, gamma + 1), 0.5)
+        for s in np.flatnonzero(active):
+            g = eng._g(s)
+            u_draft[:, s] = g.random(gamma)
+            states[s] = g.bit_generator.state
+            u_ver[s] = g.random(gamma + 1)
+        u_draft_d = torch.as_tensor(u_draft).to(dev)
+        u_ver_d = torch.as_tensor(u_ver).to(dev)
+
+        # -- draft
+        x = eng._pending(toks)
+        pending = x
+        draft_tok = torch.empty((b, gamma), dtype=torch.int32, device=dev)
+        draft_logits = torch.empty((b, gamma, V), dtype=torch.float32, device=dev) if T > 0 else None
+        for i in range(gamma):
+            lg = model.forward_batch(x[:, None], comp, n - 1 + i, act)[:, 0]
+            if draft_logits is not None:
+                draft_logits[:, i].copy_(lg)
+            x = ops.sample(lg, T, u_draft_d[i])
+            draft_tok[:, i] = x
+
+        # -- verify
+        block = torch.cat([pending[:, None], draft_tok], 1).contiguous()
+        logits = model.forward_batch(block, full, n - 1, act * (gamma + 1))
+        acc, nxt, used = ops.accept(logits, draft_logits, draft_tok, T, u_ver_d)
+        host = torch.cat([torch.stack([acc, nxt, used], 1), draft_tok], 1).cpu().numpy()
+
+        # -- bookkeeping, rollback, resync
+        cut = flen.copy()
+        emitted_total = 0
+        for s in np.flatnonzero(active):
+            a, nx, k = int(host[s, 0]), int(host[s, 1]), int(host[s, 2])
+            emitted = [int(t) for t in host[s, 3: 3 + a]] + [nx]
+            toks[s].extend(emitted)
+            emitted_total += len(emitted)
+            g = eng._g(s)
+            g.bit_generator.state = states[s]
+            g.bit_generator.advance(k)
+            cut[s] = n[s] + a
+            eng.controller.update(cfg, gamma, a, int(n[s]), self.key)
+            res[s].rounds.append(RoundLog(cfg, gamma, a, len(emitted), int(n[s])))
+            res[s].draft_steps += gamma
+            res[s].verify_passes += 1
+        full.truncate(cut)
+        self._sync(np.where(active, n - 1, full.lengths()))
+        self.last_emitted = emitted_total
+        return True

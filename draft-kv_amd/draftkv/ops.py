@@ -225,3 +225,117 @@ def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: to
                            float(temperature), u.data_ptr(), res[0].data_ptr(), res[1].data_ptr(),
                            res[2].data_ptr(), ws.data_ptr(), ws.numel(), _stream()), "dkv_accept")
     return res[0], res[1], res[2]
+
+
+# ------------------------------------------------------------------ model forward ops
+def _odt(dtype) -> int:
+    return DKV_BF16 if dtype == torch.bfloat16 else DKV_F32
+
+
+def embed(table: torch.Tensor, tokens: torch.Tensor, pos_table: Optional[torch.Tensor] = None,
+          positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _need(tokens, "tokens", torch.int32)
+    rows, d = tokens.numel(), table.shape[1]
+    out = torch.empty((rows, d), dtype=torch.float32, device=table.device)
+    check(lib().dkv_embed(table.data_ptr(), _dt(table), tokens.data_ptr(), rows, d, _ptr(pos_table),
+                          _ptr(positions), out.data_ptr(), _stream()), "dkv_embed")
+    return out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out_dtype=torch.float32) -> torch.Tensor:
+    _need(x, "x", torch.float32, 2)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    check(lib().dkv_rmsnorm(x.data_ptr(), w.data_ptr(), _dt(w), x.shape[0], x.shape[1], float(eps), out.data_ptr(),
+                            _odt(out_dtype), _stream()), "dkv_rmsnorm")
+    return out
+
+
+def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, out_dtype=torch.float32) -> torch.Tensor:
+    _need(x, "x", torch.float32, 2)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    check(lib().dkv_layernorm(x.data_ptr(), w.data_ptr(), b.data_ptr(), _dt(w), x.shape[0], x.shape[1], float(eps),
+                              out.data_ptr(), _odt(out_dtype), _stream()), "dkv_layernorm")
+    return out
+
+
+def _bias(b: Optional[torch.Tensor]):
+    return (None, 0) if b is None else (b.data_ptr(), _dt(b))
+
+
+def qkv_split(qkv: torch.Tensor, bias: Optional[torch.Tensor], n_q_heads: int, n_kv_heads: int, d: int,
+              positions: Optional[torch.Tensor] = None, cos_sin: Optional[torch.Tensor] = None, max_pos: int = 0):
+    """Fused projection rows [q | k | v] (+ bias) -> float32 q [rows, Hq, d], k, v [rows, Hkv, d];
+    RoPE on q and k when ``cos_sin`` (cos table then sin table, [2, max_pos, d/2]) is given."""
+    _need(qkv, "qkv", ndim=2)
+    rows = qkv.shape[0]
+    if qkv.shape[1] != (n_q_heads + 2 * n_kv_heads) * d:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (Hq + 2 Hkv) * d")
+    dev = qkv.device
+    q = torch.empty((rows, n_q_heads, d), dtype=torch.float32, device=dev)
+    k = torch.empty((rows, n_kv_heads, d), dtype=torch.float32, device=dev)
+    v = torch.empty((rows, n_kv_heads, d), dtype=torch.float32, device=dev)
+    bp, bd = _bias(bias)
+    check(lib().dkv_qkv_split(qkv.data_ptr(), _dt(qkv), bp, bd, rows, n_q_heads, n_kv_heads, d, _ptr(positions),
+                              _ptr(cos_sin), max_pos, q.data_ptr(), k.data_ptr(), v.data_ptr(), _stream()),
+          "dkv_qkv_split")
+    return q, k, v
+
+
+def silu_mul(gate_up: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+    _need(gate_up, "gate_up", ndim=2)
+    rows, ff2 = gate_up.shape
+    out = torch.empty((rows, ff2 // 2), dtype=out_dtype, device=gate_up.device)
+    check(lib().dkv_silu_mul(gate_up.data_ptr(), _dt(gate_up), rows, ff2 // 2, out.data_ptr(), _odt(out_dtype),
+                             _stream()), "dkv_silu_mul")
+    return out
+
+
+def bias_gelu(x: torch.Tensor, bias: Optional[torch.Tensor], out_dtype=torch.float32) -> torch.Tensor:
+    _need(x, "x", ndim=2)
+    rows, n = x.shape
+    out = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+    bp, bd = _bias(bias)
+    check(lib().dkv_bias_gelu(x.data_ptr(), _dt(x), bp, bd, rows, n, out.data_ptr(), _odt(out_dtype), _stream()),
+          "dkv_bias_gelu")
+    return out
+
+
+def relu(x: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+    _need(x, "x", ndim=2)
+    rows, n = x.shape
+    out = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+    check(lib().dkv_relu(x.data_ptr(), _dt(x), rows, n, out.data_ptr(), _odt(out_dtype), _stream()), "dkv_relu")
+    return out
+
+
+def add_(h: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """h += x (+ bias); h float32 [rows, n], x float32 or bfloat16 of the same shape."""
+    _need(h, "h", torch.float32, 2)
+    _need(x, "x")
+    if x.numel() != h.numel():
+        raise ValueError("add_: shapes differ")
+    rows, n = h.shape
+    bp, bd = _bias(bias)
+    check(lib().dkv_add(h.data_ptr(), x.data_ptr(), _dt(x), bp, bd, rows, n, _stream()), "dkv_add")
+    return h
+
+
+def gemm_f32(x: torch.Tensor, w: torch.Tensor, w_layout: int, bias: Optional[torch.Tensor] = None,
+             out: Optional[torch.Tensor] = None, accumulate: bool = False) -> torch.Tensor:
+    """out (+)= x @ w (+ bias), w [K, N] (layout 0) or [N, K] (layout 1); float32, batch-invariant."""
+    _need(x, "x", torch.float32, 2)
+    _need(w, "w", torch.float32, 2)
+    M, K = x.shape
+    N = w.shape[1] if w_layout == 0 else w.shape[0]
+    if (w.shape[0] if w_layout == 0 else w.shape[1]) != K:
+        raise ValueError(f"gemm_f32: x {tuple(x.shape)} and w {tuple(w.shape)} (layout {w_layout}) disagree")
+    if out is None:
+        if accumulate:
+            raise ValueError("gemm_f32: accumulate needs an output")
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    elif out.shape != (M, N) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("gemm_f32: out must be contiguous float32 [M, N]")
+    bp, bd = _bias(bias)
+    check(lib().dkv_gemm_f32(x.data_ptr(), w.data_ptr(), w_layout, M, N, K, bp, bd, out.data_ptr(), int(accumulate),
+                             _stream()), "dkv_gemm_f32")
+    return out

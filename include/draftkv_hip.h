@@ -199,6 +199,47 @@ int dkv_accept(const float* target, const float* draft, const int32_t* draft_tok
                int32_t* accepted, int32_t* next_token, int32_t* n_uniforms, void* work,
                size_t work_bytes, dkv_stream_t stream);
 
+/* ------------------------------------------------------ model forward ops */
+/* The non-attention pieces of the model forwards (reference
+ * draftkv/model.py:100-133, draftkv/gpt2.py:182-213, draftkv/llama.py:175-225)
+ * on float32 activations [rows][d]. Every `*_dtype` is DKV_F32 or DKV_BF16:
+ * weight tables, inputs that come out of a bf16 GEMM, and outputs that feed
+ * one. A NULL bias means none. */
+
+/* out[r] = table[tokens[r]] (+ pos_table[positions[r]])  -- model.py:108, gpt2.py:186, llama.py:179 */
+int dkv_embed(const void* table, int32_t table_dtype, const int32_t* tokens, int32_t rows, int32_t d,
+              const void* pos_table, const int32_t* positions, float* out, dkv_stream_t stream);
+/* out = x / sqrt(mean(x^2) + eps) * w  -- model.py:18-19, llama.py:93-94 */
+int dkv_rmsnorm(const float* x, const void* w, int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out,
+                int32_t out_dtype, dkv_stream_t stream);
+/* out = (x - mean) / sqrt(var + eps) * w + b  -- gpt2.py:120-123 */
+int dkv_layernorm(const float* x, const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps,
+                  void* out, int32_t out_dtype, dkv_stream_t stream);
+/* Split fused projection rows [q heads | k heads | v heads] (+ bias) into f32 q [rows][Hq][d],
+ * k and v [rows][Hkv][d]; with cos_sin (cos table [max_pos][d/2] then sin table) apply
+ * rotate-half RoPE to q and k at positions[r]  -- model.py:118-120, gpt2.py:193-196,
+ * llama.py:164-172,186-198 */
+int dkv_qkv_split(const void* qkv, int32_t qkv_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
+                  int32_t n_q_heads, int32_t n_kv_heads, int32_t d, const int32_t* positions,
+                  const float* cos_sin, int32_t max_pos, float* q, float* k, float* v, dkv_stream_t stream);
+/* out = silu(gate) * up with gate_up = [rows][2*ff]  -- llama.py:102-103,222 */
+int dkv_silu_mul(const void* gate_up, int32_t gate_up_dtype, int32_t rows, int32_t ff, void* out, int32_t out_dtype,
+                 dkv_stream_t stream);
+/* out = gelu_tanh(x + bias)  -- gpt2.py:126-127,210 */
+int dkv_bias_gelu(const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows, int32_t n,
+                  void* out, int32_t out_dtype, dkv_stream_t stream);
+/* out = max(x, 0)  -- model.py:131 */
+int dkv_relu(const void* x, int32_t x_dtype, int32_t rows, int32_t n, void* out, int32_t out_dtype,
+             dkv_stream_t stream);
+/* h += x (+ bias): residual adds  -- model.py:128,131, gpt2.py:207,210, llama.py:219,222 */
+int dkv_add(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows, int32_t n,
+            dkv_stream_t stream);
+/* out (+)= x[M][K] . w (+ bias[N]), w[K][N] (w_layout 0) or w[N][K] (1), float32. Each output is
+ * one in-order k reduction, so a row's result is the same for any M (the verify pass and the
+ * one-token decode agree bit for bit)  -- the x @ W products of the model forwards */
+int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, int32_t N, int32_t K,
+                 const void* bias, int32_t bias_dtype, float* out, int32_t accumulate, dkv_stream_t stream);
+
 /* ---------------------------------------------------------------- misc */
 const char* dkv_last_error(void);
 int32_t dkv_version(void);

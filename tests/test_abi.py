@@ -14,7 +14,7 @@ HEADER = os.path.join(ROOT, "include", "draftkv_hip.h")
 def declared() -> set[str]:
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"\b(dkv_[a-z_]+)\s*\(", text))
+    return set(re.findall(r"\b(dkv_[a-z0-9_]+)\s*\(", text))
 
 
 def test_header_declares_the_hot_path():

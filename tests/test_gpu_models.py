@@ -1,0 +1,207 @@
+"""The GPU model forwards and the decode-round engine against the oracle.
+
+* logits of the three model families (tiny ReLU transformer, GPT-2, Llama with
+  GQA and biases) within 2e-3 relative / 1e-3 absolute of the numpy oracle;
+* batch invariance of the float32 forward: a verify block's rows equal the
+  one-token decode rows bit for bit (the property exact greedy losslessness
+  rests on);
+* greedy losslessness, the reference's own test (tests/test_lossless.py:28-35,
+  tests/test_paged.py:103-116): speculative output == full-KV decoding, for
+  every reference config and gamma, with contiguous and paged full caches;
+* token and accepted-run parity with the oracle engine on the same seed
+  (greedy and temperature sampling);
+* a batch of ragged prompts decodes to the same tokens as one at a time.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.models as om
+from oracle.caches import FullKVCache as OFull
+from oracle.config import Cfg
+from oracle.engine import Engine, fixed
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 2e-3, 1e-3
+
+GPT2_SMALL = dict(n_layer=2, n_head=4, n_embd=64, vocab_size=97, n_positions=512, n_inner=None,
+                  layer_norm_epsilon=1e-5)
+
+
+def _pair(name):
+    """(gpu model, oracle model) with identical weights."""
+    from draftkv import gpt2, llama, model
+    if name == "tiny":
+        return model.demo_model(), om.demo_model()
+    if name == "llama":
+        return llama.demo_llama(), om.demo_llama()
+    if name == "llama_bias":
+        return llama.demo_llama(attn_bias=True, n_layers=2), om.demo_llama(attn_bias=True, n_layers=2)
+    if name == "gpt2":
+        w = om.gpt2_random_weights(GPT2_SMALL, seed=0, std=0.2)
+        return gpt2.GPT2(w, GPT2_SMALL), om.GPT2(w, GPT2_SMALL)
+    raise KeyError(name)
+
+
+def _ocfg(c):
+    return Cfg(c.bits, c.keep_frac, c.sink, c.recent, c.group, "f16" if c.scale_fp16 else "f32")
+
+
+def _prompt(seed, n, vocab):
+    return [int(x) for x in np.random.default_rng(seed).integers(0, vocab, n)]
+
+
+MODELS = ["tiny", "llama", "llama_bias", "gpt2"]
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_forward_matches_oracle(dev, name):
+    g, o = _pair(name)
+    toks = np.array(_prompt(1, 41, g.vocab_size))
+    oc = OFull(o.n_layers)
+    want = o.forward(toks[:-1], oc, 0)
+    want1 = o.forward(toks[-1:], oc, 40)
+    gc = g.new_cache()
+    got = g.forward(toks[:-1], gc, 0)
+    got1 = g.forward(toks[-1:], gc, 40)
+    assert got.shape == want.shape and got.dtype == np.float32
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(got1, want1, rtol=RTOL, atol=ATOL)
+    assert gc.length == 41
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_verify_block_equals_decode_rows(dev, name):
+    """The float32 forward is batch-invariant: T rows in one pass == T one-row passes."""
+    g, _ = _pair(name)
+    toks = np.array(_prompt(2, 37, g.vocab_size))
+    a, b = g.new_cache(), g.new_cache()
+    g.forward(toks[:30], a, 0)
+    g.forward(toks[:30], b, 0)
+    block = g.forward(toks[30:], a, 30)
+    rows = np.stack([g.forward(toks[30 + i: 31 + i], b, 30 + i)[0] for i in range(7)])
+    assert np.array_equal(block.view(np.uint32), rows.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def tiny_setup():
+    from draftkv import DraftKVEngine
+    from draftkv.model import demo_model
+    m = demo_model()
+    prompt = _prompt(0, 192, m.vocab_size)
+    base = DraftKVEngine(m, seed=0).generate_baseline(prompt, 32, 0.0)
+    return m, prompt, base
+
+
+def _configs():
+    from draftkv import CompressionConfig as C
+    return [C(16, 1.0), C(8, 1.0), C(4, 1.0), C(4, 0.5), C(3, 0.5), C(2, 0.25)]
+
+
+@pytest.mark.parametrize("ci", range(6))
+@pytest.mark.parametrize("gamma", [1, 3, 6])
+def test_greedy_output_identical(dev, tiny_setup, ci, gamma):
+    from draftkv import DraftKVEngine, FixedPolicy
+    m, prompt, base = tiny_setup
+    cfg = _configs()[ci]
+    r = DraftKVEngine(m, FixedPolicy(cfg, gamma), seed=0).generate(prompt, 32, 0.0)
+    assert r.tokens == base, f"{cfg.label()} gamma={gamma} diverged from full-KV decoding"
+    assert r.new_tokens == 32 and r.verify_passes <= 32
+
+
+def test_baseline_matches_oracle_tokens(dev, tiny_setup):
+    m, prompt, base = tiny_setup
+    assert Engine(om.demo_model(), fixed(Cfg(), 1), seed=0).generate_baseline(prompt, 32, 0.0) == base
+
+
+@pytest.mark.parametrize("block_size", [4, 16])
+def test_lossless_with_paged_authoritative_cache(dev, tiny_setup, block_size):
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy, PagedKVCache
+    m, _, _ = tiny_setup
+    prompt = _prompt(3, 192, m.vocab_size)
+    base = DraftKVEngine(m, seed=0).generate_baseline(prompt, 32, 0.0)
+    eng = DraftKVEngine(m, FixedPolicy(CompressionConfig(4, 0.5), 5), seed=0,
+                        full_cache_factory=lambda: PagedKVCache(m.n_layers, m.n_heads, m.d_head,
+                                                                block_size=block_size, n_blocks=2048))
+    r = eng.generate(prompt, 32, 0.0)
+    assert r.tokens == base
+    eng.last_full.pool.check_invariants()
+
+
+@pytest.mark.parametrize("name", ["llama", "llama_bias", "gpt2"])
+def test_lossless_other_families(dev, name):
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    g, _ = _pair(name)
+    prompt = _prompt(4, 100, g.vocab_size)
+    base = DraftKVEngine(g, seed=0).generate_baseline(prompt, 24, 0.0)
+    for cfg, gamma in ((CompressionConfig(4, 0.5), 4), (CompressionConfig(2, 0.25, group=32, scale_fp16=True), 6)):
+        r = DraftKVEngine(g, FixedPolicy(cfg, gamma), seed=0).generate(prompt, 24, 0.0)
+        assert r.tokens == base, f"{name} {cfg.label()}"
+
+
+@pytest.mark.parametrize("ci,gamma", [(1, 4), (2, 3), (3, 5), (5, 4)])
+def test_rounds_match_oracle_engine(dev, tiny_setup, ci, gamma):
+    """Same tokens and the same accepted count in every round as the oracle engine."""
+    from draftkv import DraftKVEngine, FixedPolicy
+    m, prompt, _ = tiny_setup
+    cfg = _configs()[ci]
+    r = DraftKVEngine(m, FixedPolicy(cfg, gamma), seed=0).generate(prompt, 32, 0.0)
+    o = Engine(om.demo_model(), fixed(_ocfg(cfg), gamma), seed=0).generate(prompt, 32, 0.0)
+    assert r.tokens == o.tokens
+    assert [x.accepted for x in r.rounds] == [x.accepted for x in o.rounds]
+    assert r.cache_rebuilds == o.cache_rebuilds == 1
+
+
+@pytest.mark.parametrize("temperature", [0.7, 1.0])
+def test_sampling_matches_oracle_engine(dev, tiny_setup, temperature):
+    """Temperature sampling with the same seed: same draws, same tokens, same accepted runs."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    m, prompt, _ = tiny_setup
+    cfg = CompressionConfig(4, 1.0)
+    r = DraftKVEngine(m, FixedPolicy(cfg, 4), seed=7).generate(prompt, 32, temperature)
+    o = Engine(om.demo_model(), fixed(_ocfg(cfg), 4), seed=7).generate(prompt, 32, temperature)
+    assert r.tokens == o.tokens
+    assert [x.accepted for x in r.rounds] == [x.accepted for x in o.rounds]
+    base = Engine(om.demo_model(), fixed(_ocfg(cfg), 4), seed=7).generate_baseline(prompt, 16, temperature)
+    from draftkv import DraftKVEngine as E
+    assert E(m, seed=7).generate_baseline(prompt, 16, temperature) == base
+
+
+def test_batched_generate_equals_one_at_a_time(dev, tiny_setup):
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    m, _, _ = tiny_setup
+    prompts = [_prompt(10 + s, n, m.vocab_size) for s, n in enumerate((50, 64, 31))]
+    single = [DraftKVEngine(m, seed=0).generate_baseline(p, 20, 0.0) for p in prompts]
+    batch_base = DraftKVEngine(m, seed=0).generate_baseline_batch(prompts, 20, 0.0)
+    assert batch_base == single
+    res = DraftKVEngine(m, FixedPolicy(CompressionConfig(4, 0.5), 4), seed=0).generate_batch(prompts, 20, 0.0)
+    assert [r.tokens for r in res] == single
+
+
+def test_controller_driven_run_is_lossless(dev, tiny_setup):
+    from draftkv import CostModel, DraftKVEngine, ThompsonController, default_arms
+    m, prompt, base = tiny_setup
+    cm = CostModel(n_layers=m.n_layers, n_kv_heads=m.n_heads, d_head=m.d_head, weight_bytes=2.0e6,
+                   bandwidth=2.0e10, full_kv_bandwidth=6.4e8, hbm_kv_budget=2.0e5)
+    r = DraftKVEngine(m, ThompsonController(cm, default_arms(), seed=3), seed=0).generate(prompt, 32, 0.0)
+    assert r.tokens == base
+    assert r.verify_passes <= r.new_tokens
+
+
+def test_bf16_llama_runs_and_is_self_consistent(dev):
+    """bf16 weights + bf16 paged cache (the serving configuration): logits stay
+    close to the float32 model and speculative decoding runs end to end."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    from draftkv.llama import LlamaLike, demo_llama_weights
+    w, c = demo_llama_weights(attn_sharpness=1.0, attn_gain=1.0)
+    g16 = LlamaLike(w, c, dtype=torch.bfloat16)
+    g32 = LlamaLike(w, c)
+    toks = np.array(_prompt(5, 33, c["vocab_size"]))
+    a = g16.forward(toks, g16.new_cache(), 0)
+    b = g32.forward(toks, g32.new_cache(), 0)
+    assert np.abs(a - b).max() < 0.05 * max(1.0, np.abs(b).max())
+    r = DraftKVEngine(g16, FixedPolicy(CompressionConfig(4, 0.5, group=32, scale_fp16=True), 4),
+                      seed=0).generate(list(toks), 16, 0.0)
+    assert len(r.tokens) == 33 + 16 and r.new_tokens == 16
