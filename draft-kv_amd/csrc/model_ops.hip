@@ -21,7 +21,7 @@ __device__ __forceinline__ float bias_at(const void* bias, int64_t i, int dtype)
     return bias ? load_elem(bias, i, dtype) : 0.0f;
 }
 
-// Sum over the block (256 threads = 4 waves); every thread gets the total.
+// Sum over the block (up to 1024 threads = 16 waves); every thread gets the total.
 __device__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE;
@@ -33,136 +33,159 @@ __device__ float block_sum(float v, float* red) {
     return t;
 }
 
-// h[r] = table[tok[r]] (+ pos_table[pos[r]])
+// h[r] = table[tok[r]] (+ pos_table[pos[r]]); grid (column tiles, rows)
 __global__ void __launch_bounds__(256) embed_kernel(const void* __restrict__ table, int tdt,
                                                     const int32_t* __restrict__ tokens, int d,
                                                     const void* __restrict__ pos_table,
                                                     const int32_t* __restrict__ positions, float* __restrict__ out) {
-    const int r = blockIdx.x;
-    const int64_t t = tokens[r];
-    for (int i = threadIdx.x; i < d; i += blockDim.x) {
-        float v = load_elem(table, t * d + i, tdt);
-        if (pos_table) v += load_elem(pos_table, (int64_t)positions[r] * d + i, tdt);
-        out[(int64_t)r * d + i] = v;
-    }
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d) return;
+    float v = load_elem(table, (int64_t)tokens[r] * d + i, tdt);
+    if (pos_table) v += load_elem(pos_table, (int64_t)positions[r] * d + i, tdt);
+    out[(int64_t)r * d + i] = v;
 }
 
-// out = x / sqrt(mean(x*x) + eps) * w
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, const void* __restrict__ w, int wdt,
-                                                      int d, float eps, void* out, int odt) {
-    __shared__ float red[4];
+// One block per row, the row held in registers (NORM_EPT elements per
+// thread): optionally h += x (+ bias) first, written back to h, then
+//   RMSNorm:   out = h / sqrt(mean(h*h) + eps) * w
+//   LayerNorm: out = (h - mean) / sqrt(mean((h-mean)^2) + eps) * w + b
+constexpr int NORM_EPT = 8;
+template <bool LN>
+__global__ void __launch_bounds__(1024) norm_kernel(float* __restrict__ h, const void* __restrict__ x, int xdt,
+                                                    const void* __restrict__ xb, int xbdt, const void* __restrict__ w,
+                                                    const void* __restrict__ b, int wdt, int d, float eps, void* out,
+                                                    int odt) {
+    __shared__ float red[16];
     const int r = blockIdx.x;
-    const float* xr = x + (int64_t)r * d;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) ss += xr[i] * xr[i];
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / d + eps);
-    for (int i = threadIdx.x; i < d; i += blockDim.x)
-        store_elem(out, (int64_t)r * d + i, xr[i] * inv * load_elem(w, i, wdt), odt);
-}
-
-// out = (x - mean) / sqrt(var + eps) * w + b
-__global__ void __launch_bounds__(256) layernorm_kernel(const float* __restrict__ x, const void* __restrict__ w,
-                                                        const void* __restrict__ b, int wdt, int d, float eps,
-                                                        void* out, int odt) {
-    __shared__ float red[4];
-    const int r = blockIdx.x;
-    const float* xr = x + (int64_t)r * d;
+    float* hr = h + (int64_t)r * d;
+    float v[NORM_EPT];
     float s = 0.0f;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) s += xr[i];
-    const float mu = block_sum(s, red) / d;
-    float v = 0.0f;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) v += (xr[i] - mu) * (xr[i] - mu);
-    const float var = block_sum(v, red) / d;
-    const float inv = 1.0f / sqrtf(var + eps);
-    for (int i = threadIdx.x; i < d; i += blockDim.x)
-        store_elem(out, (int64_t)r * d + i, (xr[i] - mu) * inv * load_elem(w, i, wdt) + load_elem(b, i, wdt), odt);
+#pragma unroll
+    for (int j = 0; j < NORM_EPT; ++j) {
+        const int i = threadIdx.x + j * blockDim.x;
+        float t = 0.0f;
+        if (i < d) {
+            t = hr[i];
+            if (x) {
+                t += load_elem(x, (int64_t)r * d + i, xdt) + bias_at(xb, i, xbdt);
+                hr[i] = t;
+            }
+        }
+        v[j] = t;
+        s += LN ? t : t * t;
+    }
+    s = block_sum(s, red);
+    float mu = 0.0f, inv;
+    if (LN) {
+        mu = s / d;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NORM_EPT; ++j) {
+            const int i = threadIdx.x + j * blockDim.x;
+            if (i < d) q += (v[j] - mu) * (v[j] - mu);
+        }
+        inv = 1.0f / sqrtf(block_sum(q, red) / d + eps);
+    } else {
+        inv = 1.0f / sqrtf(s / d + eps);
+    }
+#pragma unroll
+    for (int j = 0; j < NORM_EPT; ++j) {
+        const int i = threadIdx.x + j * blockDim.x;
+        if (i < d) {
+            const float o = LN ? (v[j] - mu) * inv * load_elem(w, i, wdt) + load_elem(b, i, wdt)
+                               : v[j] * inv * load_elem(w, i, wdt);
+            store_elem(out, (int64_t)r * d + i, o, odt);
+        }
+    }
 }
 
 // Split a fused projection row [q heads | k heads | v heads] (+ bias) into
 // float32 q [r][hq][d], k [r][hkv][d], v [r][hkv][d], applying rotate-half
 // RoPE to q and k when a cos/sin table is given: out[j] = x[j]c[j] - x[j+h]s[j],
-// out[j+h] = x[j+h]c[j] + x[j]s[j] with h = d/2.
+// out[j+h] = x[j+h]c[j] + x[j]s[j] with h = d/2. Grid (item tiles, rows):
+// with RoPE an item is a q/k rotation pair or a v element, else one element.
 __global__ void __launch_bounds__(256) qkv_split_kernel(const void* __restrict__ qkv, int xdt,
                                                         const void* __restrict__ bias, int bdt, int hq, int hkv,
                                                         int d, const int32_t* __restrict__ positions,
                                                         const float* __restrict__ cs, int max_pos,
                                                         float* __restrict__ q, float* __restrict__ k,
                                                         float* __restrict__ v) {
-    const int r = blockIdx.x;
+    const int r = blockIdx.y;
     const int n = (hq + 2 * hkv) * d;
     const int64_t base = (int64_t)r * n;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (!cs) {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const float x = load_elem(qkv, base + i, xdt) + bias_at(bias, i, bdt);
-            const int head = i / d, c = i % d;
-            if (head < hq)
-                q[((int64_t)r * hq + head) * d + c] = x;
-            else if (head < hq + hkv)
-                k[((int64_t)r * hkv + head - hq) * d + c] = x;
-            else
-                v[((int64_t)r * hkv + head - hq - hkv) * d + c] = x;
-        }
+        if (i >= n) return;
+        const float x = load_elem(qkv, base + i, xdt) + bias_at(bias, i, bdt);
+        const int head = i / d, c = i % d;
+        if (head < hq)
+            q[((int64_t)r * hq + head) * d + c] = x;
+        else if (head < hq + hkv)
+            k[((int64_t)r * hkv + head - hq) * d + c] = x;
+        else
+            v[((int64_t)r * hkv + head - hq - hkv) * d + c] = x;
         return;
     }
     const int half = d / 2;
-    const int64_t p = positions[r];
-    const float* cr = cs + p * half;
-    const float* sr = cs + (int64_t)max_pos * half + p * half;
-    // q and k heads: one thread per rotation pair
-    for (int i = threadIdx.x; i < (hq + hkv) * half; i += blockDim.x) {
+    const int pairs = (hq + hkv) * half;
+    if (i < pairs) {
         const int head = i / half, j = i % half;
+        const int64_t p = positions[r];
+        const float cj = cs[p * half + j];
+        const float sj = cs[(int64_t)max_pos * half + p * half + j];
         const int c0 = head * d + j, c1 = c0 + half;
         const float a = load_elem(qkv, base + c0, xdt) + bias_at(bias, c0, bdt);
         const float b = load_elem(qkv, base + c1, xdt) + bias_at(bias, c1, bdt);
-        const float o0 = a * cr[j] - b * sr[j];
-        const float o1 = b * cr[j] + a * sr[j];
         float* dst = head < hq ? q + ((int64_t)r * hq + head) * d : k + ((int64_t)r * hkv + head - hq) * d;
-        dst[j] = o0;
-        dst[j + half] = o1;
-    }
-    for (int i = threadIdx.x; i < hkv * d; i += blockDim.x) {
-        const int c = (hq + hkv) * d + i;
-        v[(int64_t)r * hkv * d + i] = load_elem(qkv, base + c, xdt) + bias_at(bias, c, bdt);
+        dst[j] = a * cj - b * sj;
+        dst[j + half] = b * cj + a * sj;
+    } else if (i < pairs + hkv * d) {
+        const int e = i - pairs;
+        const int c = (hq + hkv) * d + e;
+        v[(int64_t)r * hkv * d + e] = load_elem(qkv, base + c, xdt) + bias_at(bias, c, bdt);
     }
 }
 
+// Elementwise kernels: grid (column tiles of 256, rows).
 // out = silu(gate) * up, gu = [rows][2*ff] (gate, then up)
 __global__ void __launch_bounds__(256) silu_mul_kernel(const void* __restrict__ gu, int gdt, int ff, void* out,
                                                        int odt) {
-    const int r = blockIdx.x;
-    for (int i = threadIdx.x; i < ff; i += blockDim.x) {
-        const float g = load_elem(gu, (int64_t)r * 2 * ff + i, gdt);
-        const float u = load_elem(gu, (int64_t)r * 2 * ff + ff + i, gdt);
-        store_elem(out, (int64_t)r * ff + i, g / (1.0f + __expf(-g)) * u, odt);
-    }
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= ff) return;
+    const float g = load_elem(gu, (int64_t)r * 2 * ff + i, gdt);
+    const float u = load_elem(gu, (int64_t)r * 2 * ff + ff + i, gdt);
+    store_elem(out, (int64_t)r * ff + i, g / (1.0f + __expf(-g)) * u, odt);
 }
 
 // out = gelu_tanh(x + bias)
 __global__ void __launch_bounds__(256) bias_gelu_kernel(const void* __restrict__ x, int xdt,
                                                         const void* __restrict__ bias, int bdt, int n, void* out,
                                                         int odt) {
-    const int r = blockIdx.x;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
-        const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-        store_elem(out, (int64_t)r * n + i, 0.5f * v * (1.0f + tanhf(u)), odt);
-    }
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
+    const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    store_elem(out, (int64_t)r * n + i, 0.5f * v * (1.0f + tanhf(u)), odt);
 }
 
 // out = max(x, 0)
 __global__ void __launch_bounds__(256) relu_kernel(const void* __restrict__ x, int xdt, int n, void* out, int odt) {
-    const int r = blockIdx.x;
-    for (int i = threadIdx.x; i < n; i += blockDim.x)
-        store_elem(out, (int64_t)r * n + i, fmaxf(load_elem(x, (int64_t)r * n + i, xdt), 0.0f), odt);
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    store_elem(out, (int64_t)r * n + i, fmaxf(load_elem(x, (int64_t)r * n + i, xdt), 0.0f), odt);
 }
 
 // h += x (+ bias)
 __global__ void __launch_bounds__(256) add_kernel(float* h, const void* __restrict__ x, int xdt,
                                                   const void* __restrict__ bias, int bdt, int n) {
-    const int r = blockIdx.x;
-    for (int i = threadIdx.x; i < n; i += blockDim.x)
-        h[(int64_t)r * n + i] += load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    h[(int64_t)r * n + i] += load_elem(x, (int64_t)r * n + i, xdt) + bias_at(bias, i, bdt);
 }
 
 // out[m][n] (+)= sum_k x[m][k] * w(k, n) (+ bias[n]), one thread per output,
@@ -204,33 +227,71 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const float* __restrict__
 
 using namespace dkv;
 
-#define DKV_ROWS_LAUNCH(kernel, rows, ...)                                                         \
-    do {                                                                                           \
-        if ((rows) <= 0) return DKV_OK;                                                            \
-        hipLaunchKernelGGL(kernel, dim3(rows), dim3(256), 0, as_stream(stream), __VA_ARGS__);      \
-        return check_launch(#kernel);                                                              \
+// grid (ceil(cols / 256), rows), 256 threads
+#define DKV_COLS_LAUNCH(kernel, rows, cols, ...)                                                              \
+    do {                                                                                                      \
+        if ((rows) <= 0 || (cols) <= 0) return DKV_OK;                                                        \
+        DKV_REQUIRE((rows) <= 65535, #kernel ": more than 65535 rows in one launch");                         \
+        hipLaunchKernelGGL(kernel, dim3(((cols) + 255) / 256, (rows)), dim3(256), 0, as_stream(stream),       \
+                           __VA_ARGS__);                                                                      \
+        return check_launch(#kernel);                                                                         \
     } while (0)
 
 static bool dtype_ok(int32_t dt) { return dt == DKV_F32 || dt == DKV_BF16; }
+
+static int norm_launch(bool ln, float* h, const void* x, int32_t x_dtype, const void* xb, int32_t xb_dtype,
+                       const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out,
+                       int32_t out_dtype, dkv_stream_t stream, const char* what) {
+    DKV_REQUIRE(h && w && out && d > 0 && dtype_ok(w_dtype) && dtype_ok(out_dtype), std::string(what) + ": bad arguments");
+    DKV_REQUIRE(!x || dtype_ok(x_dtype), std::string(what) + ": bad residual dtype");
+    DKV_REQUIRE(!xb || dtype_ok(xb_dtype), std::string(what) + ": bad bias dtype");
+    DKV_REQUIRE(!ln || b, std::string(what) + ": LayerNorm needs a bias");
+    DKV_REQUIRE(d <= NORM_EPT * 1024, std::string(what) + ": width above 8192");
+    if (rows <= 0) return DKV_OK;
+    const int threads = d > 2048 ? 1024 : d > 512 ? 256 : 64;
+    if (d > NORM_EPT * threads) return fail(DKV_EINVAL, std::string(what) + ": width too large");
+    if (ln)
+        hipLaunchKernelGGL(norm_kernel<true>, dim3(rows), dim3(threads), 0, as_stream(stream), h, x, x_dtype, xb,
+                           xb_dtype, w, b, w_dtype, d, eps, out, out_dtype);
+    else
+        hipLaunchKernelGGL(norm_kernel<false>, dim3(rows), dim3(threads), 0, as_stream(stream), h, x, x_dtype, xb,
+                           xb_dtype, w, b, w_dtype, d, eps, out, out_dtype);
+    return check_launch(what);
+}
 
 extern "C" int dkv_embed(const void* table, int32_t table_dtype, const int32_t* tokens, int32_t rows, int32_t d,
                          const void* pos_table, const int32_t* positions, float* out, dkv_stream_t stream) {
     DKV_REQUIRE(table && tokens && out && d > 0 && dtype_ok(table_dtype), "dkv_embed: bad arguments");
     DKV_REQUIRE(!pos_table || positions, "dkv_embed: positions needed with a position table");
-    DKV_ROWS_LAUNCH(embed_kernel, rows, table, table_dtype, tokens, d, pos_table, positions, out);
+    DKV_COLS_LAUNCH(embed_kernel, rows, d, table, table_dtype, tokens, d, pos_table, positions, out);
 }
 
 extern "C" int dkv_rmsnorm(const float* x, const void* w, int32_t w_dtype, int32_t rows, int32_t d, float eps,
                            void* out, int32_t out_dtype, dkv_stream_t stream) {
-    DKV_REQUIRE(x && w && out && d > 0 && dtype_ok(w_dtype) && dtype_ok(out_dtype), "dkv_rmsnorm: bad arguments");
-    DKV_ROWS_LAUNCH(rmsnorm_kernel, rows, x, w, w_dtype, d, eps, out, out_dtype);
+    return norm_launch(false, const_cast<float*>(x), nullptr, 0, nullptr, 0, w, nullptr, w_dtype, rows, d, eps, out,
+                       out_dtype, stream, "dkv_rmsnorm");
 }
 
 extern "C" int dkv_layernorm(const float* x, const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d,
                              float eps, void* out, int32_t out_dtype, dkv_stream_t stream) {
-    DKV_REQUIRE(x && w && b && out && d > 0 && dtype_ok(w_dtype) && dtype_ok(out_dtype),
-                "dkv_layernorm: bad arguments");
-    DKV_ROWS_LAUNCH(layernorm_kernel, rows, x, w, b, w_dtype, d, eps, out, out_dtype);
+    return norm_launch(true, const_cast<float*>(x), nullptr, 0, nullptr, 0, w, b, w_dtype, rows, d, eps, out,
+                       out_dtype, stream, "dkv_layernorm");
+}
+
+extern "C" int dkv_add_rmsnorm(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype,
+                               const void* w, int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out,
+                               int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(x, "dkv_add_rmsnorm: x is required");
+    return norm_launch(false, h, x, x_dtype, bias, bias_dtype, w, nullptr, w_dtype, rows, d, eps, out, out_dtype,
+                       stream, "dkv_add_rmsnorm");
+}
+
+extern "C" int dkv_add_layernorm(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype,
+                                 const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps,
+                                 void* out, int32_t out_dtype, dkv_stream_t stream) {
+    DKV_REQUIRE(x, "dkv_add_layernorm: x is required");
+    return norm_launch(true, h, x, x_dtype, bias, bias_dtype, w, b, w_dtype, rows, d, eps, out, out_dtype, stream,
+                       "dkv_add_layernorm");
 }
 
 extern "C" int dkv_qkv_split(const void* qkv, int32_t qkv_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
@@ -241,34 +302,35 @@ extern "C" int dkv_qkv_split(const void* qkv, int32_t qkv_dtype, const void* bia
                 "dkv_qkv_split: bad arguments");
     DKV_REQUIRE(!bias || dtype_ok(bias_dtype), "dkv_qkv_split: bad bias dtype");
     DKV_REQUIRE(!cos_sin || (positions && d % 2 == 0 && max_pos > 0), "dkv_qkv_split: RoPE needs positions, even d");
-    DKV_ROWS_LAUNCH(qkv_split_kernel, rows, qkv, qkv_dtype, bias, bias_dtype, n_q_heads, n_kv_heads, d, positions,
-                    cos_sin, max_pos, q, k, v);
+    const int items = cos_sin ? (n_q_heads + n_kv_heads) * (d / 2) + n_kv_heads * d : (n_q_heads + 2 * n_kv_heads) * d;
+    DKV_COLS_LAUNCH(qkv_split_kernel, rows, items, qkv, qkv_dtype, bias, bias_dtype, n_q_heads, n_kv_heads, d,
+                    positions, cos_sin, max_pos, q, k, v);
 }
 
 extern "C" int dkv_silu_mul(const void* gate_up, int32_t gate_up_dtype, int32_t rows, int32_t ff, void* out,
                             int32_t out_dtype, dkv_stream_t stream) {
     DKV_REQUIRE(gate_up && out && ff > 0 && dtype_ok(gate_up_dtype) && dtype_ok(out_dtype),
                 "dkv_silu_mul: bad arguments");
-    DKV_ROWS_LAUNCH(silu_mul_kernel, rows, gate_up, gate_up_dtype, ff, out, out_dtype);
+    DKV_COLS_LAUNCH(silu_mul_kernel, rows, ff, gate_up, gate_up_dtype, ff, out, out_dtype);
 }
 
 extern "C" int dkv_bias_gelu(const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
                              int32_t n, void* out, int32_t out_dtype, dkv_stream_t stream) {
     DKV_REQUIRE(x && out && n > 0 && dtype_ok(x_dtype) && dtype_ok(out_dtype) && (!bias || dtype_ok(bias_dtype)),
                 "dkv_bias_gelu: bad arguments");
-    DKV_ROWS_LAUNCH(bias_gelu_kernel, rows, x, x_dtype, bias, bias_dtype, n, out, out_dtype);
+    DKV_COLS_LAUNCH(bias_gelu_kernel, rows, n, x, x_dtype, bias, bias_dtype, n, out, out_dtype);
 }
 
 extern "C" int dkv_relu(const void* x, int32_t x_dtype, int32_t rows, int32_t n, void* out, int32_t out_dtype,
                         dkv_stream_t stream) {
     DKV_REQUIRE(x && out && n > 0 && dtype_ok(x_dtype) && dtype_ok(out_dtype), "dkv_relu: bad arguments");
-    DKV_ROWS_LAUNCH(relu_kernel, rows, x, x_dtype, n, out, out_dtype);
+    DKV_COLS_LAUNCH(relu_kernel, rows, n, x, x_dtype, n, out, out_dtype);
 }
 
 extern "C" int dkv_add(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
                        int32_t n, dkv_stream_t stream) {
     DKV_REQUIRE(h && x && n > 0 && dtype_ok(x_dtype) && (!bias || dtype_ok(bias_dtype)), "dkv_add: bad arguments");
-    DKV_ROWS_LAUNCH(add_kernel, rows, h, x, x_dtype, bias, bias_dtype, n);
+    DKV_COLS_LAUNCH(add_kernel, rows, n, h, x, x_dtype, bias, bias_dtype, n);
 }
 
 extern "C" int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, int32_t N, int32_t K,

@@ -58,6 +58,8 @@ _SIGS = {
     "dkv_embed": (C.c_int, [P, I32, P, I32, I32, P, P, P, P]),
     "dkv_rmsnorm": (C.c_int, [P, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_layernorm": (C.c_int, [P, P, P, I32, I32, I32, F32, P, I32, P]),
+    "dkv_add_rmsnorm": (C.c_int, [P, P, I32, P, I32, P, I32, I32, I32, F32, P, I32, P]),
+    "dkv_add_layernorm": (C.c_int, [P, P, I32, P, I32, P, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_qkv_split": (C.c_int, [P, I32, P, I32, I32, I32, I32, I32, P, P, I32, P, P, P, P]),
     "dkv_silu_mul": (C.c_int, [P, I32, I32, I32, P, I32, P]),
     "dkv_bias_gelu": (C.c_int, [P, I32, P, I32, I32, I32, P, I32, P]),

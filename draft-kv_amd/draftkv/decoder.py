@@ -118,25 +118,22 @@ class Decoder:
             return ops.gemm_f32(x, w, self.layout, bias)
         return F.linear(x, w, bias)
 
-    def _proj_add(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias=None) -> None:
-        """h += x @ W (+ bias)."""
+    def _residual(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias, nw, nb) -> torch.Tensor:
+        """h += x @ W (+ bias), then return the next norm of h (weights nw, nb).
+        float32: the GEMM accumulates into h; bf16: the add is fused into the norm."""
         if self.wdtype == torch.float32:
             ops.gemm_f32(x, w, self.layout, bias, out=h, accumulate=True)
-        else:
-            ops.add_(h, F.linear(x, w), bias)
+            return self._norm(h, nw, nb)
+        return ops.add_norm(h, F.linear(x, w), bias, nw, nb, self.eps, self.norm == "layer", self.act_dtype)
 
-    def _mlp(self, h: torch.Tensor, p: Layer) -> None:
-        x = self._norm(h, p.n2w, p.n2b)
+    def _mlp_inner(self, x: torch.Tensor, p: Layer) -> torch.Tensor:
         if self.mlp == "swiglu":
-            a = ops.silu_mul(self._proj(x, p.w1), self.act_dtype)
-        elif self.mlp == "gelu":
-            a = ops.bias_gelu(self._proj(x, p.w1), p.b1, self.act_dtype)
-        else:
-            a = ops.relu(self._proj(x, p.w1), self.act_dtype)
-        self._proj_add(h, a, p.w2, p.b2)
+            return ops.silu_mul(self._proj(x, p.w1), self.act_dtype)
+        if self.mlp == "gelu":
+            return ops.bias_gelu(self._proj(x, p.w1), p.b1, self.act_dtype)
+        return ops.relu(self._proj(x, p.w1), self.act_dtype)
 
-    def _head(self, h: torch.Tensor) -> torch.Tensor:
-        x = self._norm(h, self.nfw, self.nfb)
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
         if self.wdtype == torch.float32:
             return ops.gemm_f32(x, self.head, self.head_layout)
         return F.linear(x, self.head).float()
@@ -179,15 +176,18 @@ class Decoder:
 
         h = ops.embed(self.emb, tok, self.pos_table, positions if self.pos_table is not None else None)
         Hq, Hkv, D = self.n_heads, self.n_kv_heads, self.d_head
+        nL = len(self.layers)
+        x = self._norm(h, self.layers[0].n1w, self.layers[0].n1b)
         for L, p in enumerate(self.layers):
-            x = self._norm(h, p.n1w, p.n1b)
             q, k, v = ops.qkv_split(self._proj(x, p.wqkv), p.bqkv, Hq, Hkv, D, positions, cs, cs_len)
             a = attn(L, q.view(b, T, Hq, D), k.view(b, T, Hkv, D), v.view(b, T, Hkv, D)).view(R, Hq * D)
             if self.act_dtype != torch.float32:
                 a = a.to(self.act_dtype)
-            self._proj_add(h, a, p.wo, p.bo)
-            self._mlp(h, p)
-        logits = self._head(h).view(b, T, self.vocab_size)
+            x = self._residual(h, a, p.wo, p.bo, p.n2w, p.n2b)
+            nxt = self.layers[L + 1] if L + 1 < nL else None
+            nw, nb = (nxt.n1w, nxt.n1b) if nxt is not None else (self.nfw, self.nfb)
+            x = self._residual(h, self._mlp_inner(x, p), p.w2, p.b2, nw, nb)
+        logits = self._head(x).view(b, T, self.vocab_size)
         attn.finish()
         return logits
 

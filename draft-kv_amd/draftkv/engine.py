@@ -186,7 +186,7 @@ class DecodeBatch:
     (engine.py:138-221) for every unfinished sequence."""
 
     def __init__(self, engine: DraftKVEngine, toks: list, full, max_new_tokens: int, temperature: float = 0.0,
-                 context_key: Optional[str] = None) -> None:
+                 context_key: Optional[str] = None, reserve_cfgs: Sequence = ()) -> None:
         self.engine, self.model = engine, engine.model
         self.toks = toks
         self.full = full
@@ -203,6 +203,8 @@ class DecodeBatch:
         need = int(self.plen.max()) + max_new_tokens + 16
         self.cap_tokens = min(int(getattr(full, "max_tokens", need) or need), need)
         self.last_emitted = 0             # tokens emitted by the last step, summed over the batch
+        # arms the mirror may switch to: its pages are sized for the widest from the start
+        self.reserve_cfgs = list(reserve_cfgs) or list(getattr(engine.controller, "arms", ()))
 
     def _sync(self, start) -> None:
         self.comp.sync_from(self.full, start)
@@ -244,7 +246,9 @@ class DecodeBatch:
 
         # -- drafter's cache: build once, then rebuild only the layers that changed
         if self.comp is None:
-            self.comp = CompressedKVCache(model.n_layers, cfg, batch=b, cap=self.cap_tokens, device=dev)
+            self.comp = CompressedKVCache(model.n_layers, cfg, batch=b, cap=self.cap_tokens, device=dev,
+                                          reserve_cfgs=[c for a in self.reserve_cfgs
+                                                        for c in _layer_cfgs(a, model.n_layers)])
             self.comp.sync_from(full, 0)
             self.comp_cfg = cfg
             for r in res:

@@ -258,6 +258,26 @@ def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, out
     return out
 
 
+def add_norm(h: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor], w: torch.Tensor,
+             b: Optional[torch.Tensor], eps: float, layer_norm: bool, out_dtype=torch.float32) -> torch.Tensor:
+    """h += x (+ bias) in place, then return RMSNorm(h) (or LayerNorm when ``layer_norm``)."""
+    _need(h, "h", torch.float32, 2)
+    _need(x, "x")
+    if x.numel() != h.numel():
+        raise ValueError("add_norm: shapes differ")
+    rows, d = h.shape
+    out = torch.empty((rows, d), dtype=out_dtype, device=h.device)
+    bp, bd = _bias(bias)
+    if layer_norm:
+        check(lib().dkv_add_layernorm(h.data_ptr(), x.data_ptr(), _dt(x), bp, bd, w.data_ptr(), b.data_ptr(), _dt(w),
+                                      rows, d, float(eps), out.data_ptr(), _odt(out_dtype), _stream()),
+              "dkv_add_layernorm")
+    else:
+        check(lib().dkv_add_rmsnorm(h.data_ptr(), x.data_ptr(), _dt(x), bp, bd, w.data_ptr(), _dt(w), rows, d,
+                                    float(eps), out.data_ptr(), _odt(out_dtype), _stream()), "dkv_add_rmsnorm")
+    return out
+
+
 def _bias(b: Optional[torch.Tensor]):
     return (None, 0) if b is None else (b.data_ptr(), _dt(b))
 

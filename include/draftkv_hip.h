@@ -215,6 +215,15 @@ int dkv_rmsnorm(const float* x, const void* w, int32_t w_dtype, int32_t rows, in
 /* out = (x - mean) / sqrt(var + eps) * w + b  -- gpt2.py:120-123 */
 int dkv_layernorm(const float* x, const void* w, const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps,
                   void* out, int32_t out_dtype, dkv_stream_t stream);
+/* h += x (+ bias), written back to h, then out = RMSNorm(h) / LayerNorm(h): the residual add
+ * of one block fused with the norm that opens the next  -- model.py:128-130, gpt2.py:207-209,
+ * llama.py:219-221 (and the final norm, model.py:133, gpt2.py:212, llama.py:224) */
+int dkv_add_rmsnorm(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, const void* w,
+                    int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out, int32_t out_dtype,
+                    dkv_stream_t stream);
+int dkv_add_layernorm(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, const void* w,
+                      const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out,
+                      int32_t out_dtype, dkv_stream_t stream);
 /* Split fused projection rows [q heads | k heads | v heads] (+ bias) into f32 q [rows][Hq][d],
  * k and v [rows][Hkv][d]; with cos_sin (cos table [max_pos][d/2] then sin table) apply
  * rotate-half RoPE to q and k at positions[r]  -- model.py:118-120, gpt2.py:193-196,

@@ -1,0 +1,134 @@
+"""The model-forward kernels (include/draftkv_hip.h "model forward ops") against
+plain PyTorch float32 references of the same ops, with float32 and bf16 inputs
+and row counts that exercise the 2-D grids (1, 7, 32 and 300 rows)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from draftkv import ops
+    return ops
+
+
+ROWS = [1, 7, 32, 300]
+
+
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("d", [64, 576, 768, 4096])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_add_rmsnorm_and_layernorm(dev, rows, d, xdt):
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(rows * 7 + d)
+    h0 = torch.randn((rows, d), generator=g, device=dev)
+    x = torch.randn((rows, d), generator=g, device=dev).to(xdt)
+    bias = torch.randn((d,), generator=g, device=dev).to(xdt)
+    w = (1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(xdt)
+    b = (0.1 * torch.randn((d,), generator=g, device=dev)).to(xdt)
+    for ln in (False, True):
+        h = h0.clone()
+        out = ops.add_norm(h, x, bias, w, b if ln else None, 1e-5, ln, torch.float32)
+        ref_h = h0 + x.float() + bias.float()
+        if ln:
+            mu = ref_h.mean(-1, keepdim=True)
+            var = ((ref_h - mu) ** 2).mean(-1, keepdim=True)
+            ref = (ref_h - mu) / torch.sqrt(var + 1e-5) * w.float() + b.float()
+        else:
+            ref = ref_h / torch.sqrt((ref_h * ref_h).mean(-1, keepdim=True) + 1e-5) * w.float()
+        torch.testing.assert_close(h, ref_h, rtol=1e-6, atol=1e-6)
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+        o16 = ops.add_norm(h0.clone(), x, bias, w, b if ln else None, 1e-5, ln, torch.bfloat16)
+        assert o16.dtype == torch.bfloat16
+        torch.testing.assert_close(o16.float(), ref.bfloat16().float(), rtol=0, atol=0.02 * ref.abs().max().item())
+    plain = ops.rmsnorm(h0, w, 1e-6)
+    torch.testing.assert_close(plain, h0 / torch.sqrt((h0 * h0).mean(-1, keepdim=True) + 1e-6) * w.float(),
+                               rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("hq,hkv,d", [(4, 4, 16), (32, 8, 128), (9, 3, 64)])
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_qkv_split_rope(dev, rows, hq, hkv, d, rope, xdt):
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(rows + hq + d)
+    n = (hq + 2 * hkv) * d
+    qkv = torch.randn((rows, n), generator=g, device=dev).to(xdt)
+    bias = torch.randn((n,), generator=g, device=dev).to(xdt)
+    pos = torch.randint(0, 5000, (rows,), generator=g, device=dev, dtype=torch.int32)
+    max_pos = 8192
+    inv = 1.0 / (500000.0 ** (np.arange(0, d, 2) / d))
+    ang = np.outer(np.arange(max_pos), inv)
+    cs = torch.as_tensor(np.stack([np.cos(ang), np.sin(ang)]).astype(np.float32)).to(dev)
+    q, k, v = ops.qkv_split(qkv, bias, hq, hkv, d, pos if rope else None, cs if rope else None, max_pos)
+    x = qkv.float() + bias.float()
+    rq = x[:, : hq * d].view(rows, hq, d)
+    rk = x[:, hq * d: (hq + hkv) * d].view(rows, hkv, d)
+    rv = x[:, (hq + hkv) * d:].view(rows, hkv, d)
+    if rope:
+        c = cs[0][pos.long()].repeat(1, 2)[:, None, :]
+        s = cs[1][pos.long()].repeat(1, 2)[:, None, :]
+
+        def rot(t):
+            return torch.cat([-t[..., d // 2:], t[..., : d // 2]], -1)
+
+        rq, rk = rq * c + rot(rq) * s, rk * c + rot(rk) * s
+    torch.testing.assert_close(q, rq, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(k, rk, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(v, rv, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_activations(dev, rows, xdt):
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(rows)
+    ff = 1536
+    gu = (2 * torch.randn((rows, 2 * ff), generator=g, device=dev)).to(xdt)
+    ref = torch.nn.functional.silu(gu[:, :ff].float()) * gu[:, ff:].float()
+    torch.testing.assert_close(ops.silu_mul(gu), ref, rtol=1e-5, atol=1e-5)
+    x = (2 * torch.randn((rows, 3072), generator=g, device=dev)).to(xdt)
+    bias = torch.randn((3072,), generator=g, device=dev)
+    xb = x.float() + bias
+    ref = 0.5 * xb * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (xb + 0.044715 * xb ** 3)))
+    torch.testing.assert_close(ops.bias_gelu(x, bias), ref, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ops.relu(x), torch.relu(x.float()), rtol=0, atol=0)
+    h = torch.randn((rows, 3072), generator=g, device=dev)
+    ref = h + x.float() + bias
+    torch.testing.assert_close(ops.add_(h, x, bias), ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 97, 64), (9, 200, 130), (300, 64, 768)])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g, device=dev)
+    w = torch.randn((K, N) if layout == 0 else (N, K), generator=g, device=dev)
+    bias = torch.randn((N,), generator=g, device=dev)
+    ref = x.double() @ (w.double() if layout == 0 else w.double().t()) + bias.double()
+    out = ops.gemm_f32(x, w, layout, bias)
+    torch.testing.assert_close(out.double(), ref, rtol=1e-4, atol=1e-4)
+    acc = torch.randn((M, N), generator=g, device=dev)
+    got = ops.gemm_f32(x, w, layout, bias, out=acc.clone(), accumulate=True)
+    torch.testing.assert_close(got.double(), ref + acc.double(), rtol=1e-4, atol=1e-4)
+    # one row alone == the same row inside the batch, bit for bit
+    r = M // 2
+    one = ops.gemm_f32(x[r:r + 1].contiguous(), w, layout, bias)
+    assert torch.equal(one[0], out[r])
+
+
+def test_embed_with_positions(dev):
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(3)
+    table = torch.randn((50, 96), generator=g, device=dev).bfloat16()
+    pos_t = torch.randn((40, 96), generator=g, device=dev).bfloat16()
+    tok = torch.randint(0, 50, (33,), generator=g, device=dev, dtype=torch.int32)
+    pos = torch.randint(0, 40, (33,), generator=g, device=dev, dtype=torch.int32)
+    out = ops.embed(table, tok, pos_t, pos)
+    torch.testing.assert_close(out, table.float()[tok.long()] + pos_t.float()[pos.long()], rtol=0, atol=0)
