@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--period", type=int, default=64)
     ap.add_argument("--baseline-steps", type=int, default=8)
-    ap.add_argument("--workload", choices=["e2e", "kernels"], default="e2e")
+    ap.add_argument("--workload", choices=["e2e", "kernels", "copy"], default="e2e")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--gamma", type=int, default=16)
@@ -100,6 +100,17 @@ def shuffled_full_cache(L, H, D, batch, ctx, extra, dtype, seed=0):
     fill_kv(full.store, H, bs, D)
     full.commit([ctx - 1] * batch)
     return full
+
+
+def measured_traffic(key: str):
+    """HBM bytes per call of a kernel, from the FETCH_SIZE / WRITE_SIZE counter
+    runs summarised in profiles/ (scaled by a copy kernel of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "roofline_traffic.json")
+    try:
+        with open(path) as f:
+            return float(json.load(f)[key]["traffic_bytes_per_call"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def drafter_bytes(rows_per_seq, n_kv_heads, d, bits, group, q_heads):
@@ -369,6 +380,9 @@ def run_e2e(args):
     main_arm = arms[1]
     mb, mus, mn = arm_calls.get(main_arm, [float("nan"), float("nan"), 0])
     achieved = mb / (mus * 1e-6) / 1e9 if mn else float("nan")
+    traffic = None
+    if (b, ctx, main_arm.bits, main_arm.group, main_arm.keep_frac) == (32, 32768, 4, 32, 0.25):
+        traffic = measured_traffic("drafter_attention_int4_g32_keep0.25_b32_ctx32k")
     v_us = t_ver.mean_us()
     v_bytes = verify_bytes(full.lengths().astype(np.float64) + gmax / 2, Hkv, D, gmax + 1, Hq)
     # plain full-KV decoding on the same cache (one token per sequence per step)
@@ -418,7 +432,9 @@ def run_e2e(args):
                    "full_kv_decode_tok_s": base_tps, "speedup_vs_full_kv_decode": value / base_tps,
                    "requantize_ms": [round(t, 3) for t in t_req.times_ms()]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": "profiles/attention_hbm_traffic_b32_ctx32k.md (FETCH_SIZE x 2.0 + "
+                                       "WRITE_SIZE, copy-kernel calibrated)" if traffic else None,
                      "kernel": f"drafter attention, {main_arm.label()} g{main_arm.group} (dkv_drafter_attention: "
                                "split-K pass + combine + mass)",
                      "bytes_per_call": mb / max(mn, 1), "us_per_call": mus / max(mn, 1), "calls": mn},
@@ -464,25 +480,34 @@ def run_kernels(args):
     g.manual_seed(2)
     qd = torch.randn((b, Hq, D), generator=g, device=dev)
     qv = torch.randn((b, gamma + 1, Hq, D), generator=g, device=dev)
+    q1 = torch.randn((b, 1, Hq, D), generator=g, device=dev)
     start = torch.full((b,), ctx - 1 - gamma, dtype=torch.int32, device=dev)
+    start1 = torch.full((b,), ctx - 1, dtype=torch.int32, device=dev)
     max_len = ctx
-    for _ in range(args.warmup):
+
+    def one_pass():
         for layer in range(L):
             comp.attend(layer, qd)
+        for layer in range(L):
             full.attend(layer, qv, start, max_len)
-    torch.cuda.synchronize()
+        for layer in range(L):
+            tdec.obj.attend_decode(layer, q1, start1, max_len)
+
+    full.attend_decode = full.attend
     td, tv = EventTimer(comp, "attend"), EventTimer(full, "attend")
-    td.on = tv.on = True
+    tdec = EventTimer(full, "attend_decode")
+    for _ in range(args.warmup):
+        one_pass()
+    torch.cuda.synchronize()
+    td.on = tv.on = tdec.on = True
     for _ in range(args.steps):
-        for layer in range(L):
-            comp.attend(layer, qd)
-        for layer in range(L):
-            full.attend(layer, qv, start, max_len)
+        one_pass()
     torch.cuda.synchronize()
     rows = comp.rows().astype(np.float64).mean(axis=1)
     d_bytes = drafter_bytes(rows, Hkv, D, args.bits, args.group, Hq)
     v_bytes = verify_bytes(np.full(b, ctx - 1.0 - gamma / 2), Hkv, D, gamma + 1, Hq)
-    d_us, v_us = td.mean_us(), tv.mean_us()
+    dec_bytes = verify_bytes(np.full(b, ctx - 1.0), Hkv, D, 1, Hq)
+    d_us, v_us, dec_us = td.mean_us(), tv.mean_us(), tdec.mean_us()
     achieved = d_bytes / (d_us * 1e-6) / 1e9
     return {
         "metric": "drafter / verify attention kernels, Llama-3-8B attention shape b=32 ctx32k",
@@ -495,9 +520,32 @@ def run_kernels(args):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "bytes_per_call": d_bytes,
                      "us_per_call": d_us},
         "kernels": {"verify_attention": {"us_per_call": v_us, "bytes_per_call": v_bytes,
-                                         "GB/s": v_bytes / (v_us * 1e-6) / 1e9}},
+                                         "GB/s": v_bytes / (v_us * 1e-6) / 1e9, "T": gamma + 1},
+                    "decode_attention": {"us_per_call": dec_us, "bytes_per_call": dec_bytes,
+                                         "GB/s": dec_bytes / (dec_us * 1e-6) / 1e9, "T": 1}},
         "cpu_baseline": None,
     }
+
+
+def run_copy(args):
+    """A plain device-to-device copy of 1 GiB, repeated: the reference dispatch
+    for scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes."""
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / max(args.steps, 1)
+    return {"metric": "device copy 1 GiB (counter calibration)", "value": 2 * n / dt / 1e9, "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": dt * 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": "copy 1 GiB device to device", "bytes_read": n, "bytes_written": n}}
 
 
 def main():
@@ -510,7 +558,7 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    out = run_e2e(args) if args.workload == "e2e" else run_kernels(args)
+    out = {"e2e": run_e2e, "kernels": run_kernels, "copy": run_copy}[args.workload](args)
     print(json.dumps(out), flush=True)
 
 

@@ -269,6 +269,16 @@ __device__ __forceinline__ void load_page(PageRegs<D, CB, MF>& r, const uint8_t*
     load_words(r.vm, reinterpret_cast<const uint32_t*>(pg + f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB));
 }
 
+// Column offsets of group g within a 16-lane row (see the kernel): the
+// subgroup of lane XORs generated by 15, 7 and 3, in butterfly order.
+__constant__ int kColXor[8] = {0, 15, 7, 8, 3, 12, 4, 11};
+
+// value of lane (l ^ mask) of the same 16-lane row, through a DPP move
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 template <int D, int CB, int MF>
 __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
                                                               const float* __restrict__ q, int Hq, float scale,
@@ -289,8 +299,21 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     const int r_end = min(r_begin + rps, n);
     const PageFmt f = page_fmt(cfg, D);
     const int col = lane % 16, jj = lane / 16;
-    const bool cvalid = col < ncol;
-    const int gcol = cvalid ? col / G : 0, hcol = cvalid ? col % G : 0;
+    // column col = hcol ^ kColXor[gcol]: the NG columns of a head form an
+    // orbit of the lane involutions row_mirror (^15), row_half_mirror (^7) and
+    // quad reverse (^3), so their sum is a butterfly of DPP adds that leaves
+    // the bitwise-same total in every column of the head
+    int gcol = 0, hcol = 0;
+    bool cvalid = false;
+    for (int g = 0; g < NG; ++g) {
+        const int hh = col ^ kColXor[g];
+        if (hh < G) {
+            gcol = g;
+            hcol = hh;
+            cvalid = true;
+        }
+    }
+    (void)ncol;
     const int hq = h * G + hcol;
     const int gmeta = min(gcol, NG - 1);
 
@@ -339,14 +362,15 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
                 sv[4 * a + r] = cvalid ? fmaf(mt.scale, sa[r], mt.lo * qsum) : 0.0f;
             }
         }
-        // sum the group columns of each head: lanes (g * G + hcol) of this 16-lane row
+        // sum the group columns of each head (pairwise butterfly over the orbit)
         float sh[8];
 #pragma unroll
-        for (int x = 0; x < 8; ++x) sh[x] = 0.0f;
-        for (int g = 0; g < NG; ++g) {
-            const int src = (lane & ~15) | (g * G + hcol);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) sh[x] += __shfl(sv[x], src);
+        for (int x = 0; x < 8; ++x) {
+            float v = sv[x];
+            if (NG >= 2) v += dpp_f32<0x140>(v);   // row_mirror: col ^ 15
+            if (NG >= 4) v += dpp_f32<0x141>(v);   // row_half_mirror: col ^ 7
+            if (NG >= 8) v += dpp_f32<0x1B>(v);    // quad_perm [3,2,1,0]: col ^ 3
+            sh[x] = v;
         }
         // mask, scale, optional spill, online softmax per column
         float pv[8];

@@ -489,6 +489,186 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_kernel(RebuildArgs a) {
     }
 }
 
+// Rebuild, one block per (page, head, sequence x changed layer), head_dim <= 128:
+//   1. the page's kept rows of K and V (bf16/f32, from the paged full cache)
+//      are staged in LDS as float32 with coalesced loads;
+//   2. every lane quantizes 8 channels of one row (group min/max over the
+//      group's lanes, zero padding of a short last group included), writes K
+//      code words and the (scale, lo) pairs, and leaves V codes in LDS;
+//   3. V code words (8 rows per word for 4-bit codes, 4 for bytes) are
+//      assembled from LDS and stored whole.
+constexpr int RB_MAXD = 128;
+struct RebuildSmem {
+    float x[2][PAGE][RB_MAXD];
+    uint8_t vcode[PAGE][RB_MAXD];
+};
+
+__global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a) {
+    const int page = blockIdx.x, h = blockIdx.y;
+    const int s = blockIdx.z % a.m.batch, L = a.layers[blockIdx.z / a.m.batch];
+    const dkv_drafter_t& m = a.m;
+    const dkv_paged_t& f = a.full;
+    const dkv_qcfg_t cfg = a.cfgs[L];
+    const int D = m.head_dim;
+    const int n = a.len[s];
+    const int B = a.budget[L * m.batch + s];
+    int kept, sink;
+    if (n <= B || cfg.recent == 0) {
+        kept = n;
+        sink = n;
+    } else {
+        kept = B;
+        sink = min(cfg.sink, n);
+    }
+    kept = min(kept, m.cap);
+    if (page == 0 && h == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
+    const int r0 = page * PAGE;
+    if (r0 >= kept) return;
+    const int rows = min(PAGE, kept - r0);
+    __shared__ RebuildSmem sm;
+    const PageFmt pf = page_fmt(cfg, D);
+    uint8_t* pg = page_ptr(m, s, L, h, page);
+    auto pos_of = [&](int r) { return r < sink ? r : n - (kept - sink) + (r - sink); };
+
+    // ---- 1. stage K (rows contiguous in the block) and V (rows contiguous per channel)
+    const int64_t bel = paged_block_elems(f);
+    const int64_t vb = (int64_t)f.n_kv_heads * f.block_size * D;
+    for (int u = threadIdx.x; u < PAGE * (D / 8); u += BLK) {
+        const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (i < rows) {
+            const int p = pos_of(r0 + i);
+            const int32_t blk = paged_block(f, s, L, p);
+            const int64_t o = (int64_t)blk * bel + ((int64_t)h * f.block_size + p % f.block_size) * D + c8;
+            if (f.dtype == DKV_BF16) {
+                const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.pool) + o);
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = bf16_to_f32(ww[e] & 0xffffu);
+                    v[2 * e + 1] = bf16_to_f32(ww[e] >> 16);
+                }
+            } else {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(f.pool) + o);
+                const float4 x0 = src[0], x1 = src[1];
+                v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+                v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.x[0][i][c8 + e] = v[e];
+    }
+    for (int u = threadIdx.x; u < PAGE * D; u += BLK) {
+        const int d = u / PAGE, i = u % PAGE;
+        float v = 0.0f;
+        if (i < rows) {
+            const int p = pos_of(r0 + i);
+            const int32_t blk = paged_block(f, s, L, p);
+            const int64_t o = (int64_t)blk * bel + vb + ((int64_t)h * D + d) * f.block_size + p % f.block_size;
+            v = load_elem(f.pool, o, f.dtype);
+        }
+        sm.x[1][i][d] = v;
+    }
+    __syncthreads();
+
+    // ---- 2. quantize: lane = (tensor, row, octet); a row owns U2 lanes (power of two)
+    const int gl = pf.cb == 32 ? 1 : pf.group / 8;         // lanes per group
+    const int U = pf.cb == 32 ? D / 8 : pf.NG * gl;          // octets that belong to a group
+    int U2 = 1;
+    while (U2 < U) U2 <<= 1;
+    for (int u = threadIdx.x; u < 2 * PAGE * U2; u += BLK) {
+        const int t = u / (PAGE * U2), rem = u % (PAGE * U2);
+        const int i = rem / U2, oct = rem % U2, d0 = 8 * oct;
+        const bool live = i < rows;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (d0 + e < D) ? sm.x[t][i][d0 + e] : 0.0f;
+        if (pf.cb == 32) {
+            if (live && d0 < D) {
+                float* dst = reinterpret_cast<float*>(pg + (t ? pf.vc : pf.kc)) + (int64_t)i * D + d0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dst[e] = v[e];
+            }
+            continue;
+        }
+        float mn = INFINITY, mx = -INFINITY;
+        if (oct < U) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                mn = fminf(mn, v[e]);
+                mx = fmaxf(mx, v[e]);
+            }
+        }
+        for (int o = 1; o < gl; o <<= 1) {
+            mn = fminf(mn, __shfl_xor(mn, o));
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+        }
+        const GroupMeta gm = group_meta(mn, mx, cfg.bits, pf.meta_f16);
+        int code[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) code[e] = quant_code(v[e], gm, cfg.bits);
+        if (oct >= U || d0 >= D) continue;
+        const bool first = d0 % pf.group == 0;
+        if (t == 0) {
+            if (!live) continue;
+            uint32_t* sec = reinterpret_cast<uint32_t*>(pg + pf.kc);
+            if (pf.cb == 4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w |= static_cast<uint32_t>(code[e]) << code_shift(4, e);
+                sec[((int64_t)i * D + d0) / 8] = w;
+            } else {
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w0 |= static_cast<uint32_t>(code[e]) << code_shift(8, e);
+                    w1 |= static_cast<uint32_t>(code[4 + e]) << code_shift(8, e);
+                }
+                sec[((int64_t)i * D + d0) / 4] = w0;
+                sec[((int64_t)i * D + d0) / 4 + 1] = w1;
+            }
+            if (first) write_meta(pg + k_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (d0 + e < D) sm.vcode[i][d0 + e] = static_cast<uint8_t>(code[e]);
+            if (live && first) write_meta(pg + v_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
+        }
+    }
+    if (h == 0) {
+        int32_t* pos = m.pos + row_index(m, s, L);
+        double* score = m.score + row_index(m, s, L);
+        for (int i = threadIdx.x; i < rows; i += BLK) {
+            pos[r0 + i] = pos_of(r0 + i);
+            score[r0 + i] = 0.0;
+        }
+    }
+    if (pf.cb == 32) return;
+    __syncthreads();
+
+    // ---- 3. V code words: word ((a*4 + j)*NDT + t) holds channel d = 16t + a of
+    // the rows (j, e) = {4j..4j+3, 16+4j..16+4j+3}; bytes: two words per (a, j, t)
+    uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
+    const int per = pf.cb == 4 ? 8 : 4;                     // rows per word
+    const int n_words = 16 * 4 * pf.NDT * (8 / per);
+    for (int u = threadIdx.x; u < n_words; u += BLK) {
+        const int half = pf.cb == 4 ? 0 : u % 2;
+        const int base = pf.cb == 4 ? u : u / 2;
+        const int t = base % pf.NDT, aj = base / pf.NDT;
+        const int j = aj % 4, acol = aj / 4;
+        const int d = 16 * t + acol;
+        if (d >= D) continue;
+        uint32_t w = 0;
+        for (int q = 0; q < per; ++q) {
+            const int e = half * 4 + q;
+            const int i = e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4);
+            const uint32_t code = sm.vcode[i][d];
+            w |= code << (pf.cb == 4 ? code_shift(4, e) : code_shift(8, q));
+        }
+        vsec[pf.cb == 4 ? base : base * 2 + half] = w;
+    }
+}
+
 // ------------------------------------------------------------ gather
 struct GatherOut {
     uint8_t* codes;
@@ -657,8 +837,15 @@ extern "C" int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_
     }
     a.len = len;
     a.budget = budget;
-    hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(mirror->cap / PAGE, mirror->batch, n_changed), dim3(BLK), 0,
-                       as_stream(stream), a);
+    if (mirror->head_dim <= RB_MAXD && mirror->head_dim % 8 == 0) {
+        DKV_REQUIRE((int64_t)mirror->batch * n_changed <= 65535, "dkv_drafter_rebuild: batch x layers too large");
+        hipLaunchKernelGGL(drafter_rebuild_page_kernel, dim3(mirror->cap / PAGE, mirror->n_kv_heads,
+                                                              mirror->batch * n_changed),
+                           dim3(BLK), 0, as_stream(stream), a);
+    } else {
+        hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(mirror->cap / PAGE, mirror->batch, n_changed), dim3(BLK), 0,
+                           as_stream(stream), a);
+    }
     return check_launch("dkv_drafter_rebuild");
 }
 

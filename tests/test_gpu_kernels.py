@@ -124,13 +124,16 @@ def test_paged_attention_matches_oracle(dev, dtype, Hq, Hkv, D, chunk):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_verify_is_batch_invariant_with_decode(dev, dtype):
+@pytest.mark.parametrize("Hq,Hkv,D,g,n", [(8, 2, 64, 8, 700), (32, 8, 128, 16, 2600), (9, 3, 64, 4, 1030),
+                                          (4, 4, 128, 1, 64)])
+def test_verify_is_batch_invariant_with_decode(dev, dtype, Hq, Hkv, D, g, n):
     """A verify pass over gamma+1 queries gives each row the bit pattern the
-    one-token decode step at that position gives (the losslessness contract)."""
+    one-token decode step at that position gives (the losslessness contract),
+    also when the rows span several query-tile groups and key super-chunks."""
     draftkv, _ = _dk()
-    rng = np.random.default_rng(7)
-    b, Hq, Hkv, D, n, g = 2, 8, 2, 64, 700, 8
-    pc = draftkv.PagedKVCache(1, Hkv, D, 16, 128, dtype="bf16" if dtype == "bf16" else np.float32, batch=b,
+    rng = np.random.default_rng(7 + g)
+    b = 2
+    pc = draftkv.PagedKVCache(1, Hkv, D, 16, 256, dtype="bf16" if dtype == "bf16" else np.float32, batch=b,
                               chunk_keys=256)
     k = rng.standard_normal((b, n + g, Hkv, D)).astype(np.float32)
     v = rng.standard_normal((b, n + g, Hkv, D)).astype(np.float32)
