@@ -32,9 +32,12 @@ namespace dkv {
 constexpr int DQB = 16;     // max query heads per KV head (generic path)
 constexpr int DMAXD = 128;  // LDS tiles stay under 64 KB
 
-__host__ __device__ inline int rows_per_split(const dkv_drafter_t& m) {
-    // enough splits to fill the chip at small batch, few partials at large batch
-    return (m.batch * m.n_kv_heads >= 128) ? 512 : 128;
+__host__ __device__ inline int rows_per_split(const dkv_drafter_t& m, int G) {
+    // enough splits to fill the chip at small batch, few partials at large
+    // batch; at most 2048 (row, query head) logits per split (8 KB of LDS
+    // staging per wave in the MFMA kernel)
+    const int base = (m.batch * m.n_kv_heads >= 128) ? 512 : 128;
+    return std::max(PAGE, std::min(base, (2048 / std::max(G, 1)) / PAGE * PAGE));
 }
 
 // ---------------------------------------------------------------- generic path
@@ -321,13 +324,17 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     f16x8_t qhi[NSTEP], qlo[NSTEP];
     float qsum = 0.0f;
     {
+        // loads are unconditional (hq is a valid head for every lane); the
+        // column's group mask is a select, so no branch per element
         const float* qr = q + ((int64_t)s * Hq + hq) * D + DL * jj;
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = DL * jj + 8 * st + e;
-                const float v = (cvalid && d / group == gcol) ? qr[8 * st + e] : 0.0f;
+                float raw = qr[8 * st + e];
+                asm volatile("" : "+v"(raw));   // load unconditionally (no branch per element)
+                const float v = (cvalid && d / group == gcol) ? raw : 0.0f;
                 const _Float16 hi = (_Float16)v;
                 const _Float16 lo = (_Float16)(v - (float)hi);
                 qhi[st][e] = hi;
@@ -343,6 +350,17 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     float m_run = -INFINITY, l_run = 0.0f, bsum = 0.0f, zsum = 0.0f;
 
     const uint32_t magic = magic_f16x2();
+    const uint32_t use2 = NG >= 2 ? 0xFFFFFFFFu : 0u, use4 = NG >= 4 ? 0xFFFFFFFFu : 0u,
+                   use8 = NG >= 8 ? 0xFFFFFFFFu : 0u;
+    // Logit spill through a buffer resource over this sequence's logits: lanes
+    // with nothing to store get an offset past the end, which the hardware
+    // drops, so the store needs no branch (a branch would split the loop body
+    // and let the compiler sink the next page's loads to their use).
+    // Logits for note_attention are staged in this wave's LDS region
+    // [head][row - r_begin] (lanes with nothing to keep write a dummy slot),
+    // so the loop issues no memory stores; they go out after the split.
+    extern __shared__ float dyn_smem[];
+    float* slog = dyn_smem + wave * (G * rps + WAVE);
     // one page of work on registers already loaded
     auto step = [&](const PageRegs<D, CB, MF>& cur, const int p0) {
         // ---- QK over the page's two 16-row tiles, folded per (row, group)
@@ -356,20 +374,24 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qhi[st], sa, 0, 0, 0);
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qlo[st], sa, 0, 0, 0);
             }
+            // columns outside every (group, head) pair have q = 0 and stay
+            // finite; rows past the live count are masked below
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const GroupMeta mt = pair_of<MF>(cur.km[a], r);
-                sv[4 * a + r] = cvalid ? fmaf(mt.scale, sa[r], mt.lo * qsum) : 0.0f;
+                sv[4 * a + r] = fmaf(mt.scale, sa[r], mt.lo * qsum);
             }
         }
-        // sum the group columns of each head (pairwise butterfly over the orbit)
+        // sum the group columns of each head (pairwise butterfly over the
+        // orbit); a step the group count does not use adds +0 (masked bits,
+        // no branch)
         float sh[8];
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
             float v = sv[x];
-            if (NG >= 2) v += dpp_f32<0x140>(v);   // row_mirror: col ^ 15
-            if (NG >= 4) v += dpp_f32<0x141>(v);   // row_half_mirror: col ^ 7
-            if (NG >= 8) v += dpp_f32<0x1B>(v);    // quad_perm [3,2,1,0]: col ^ 3
+            v += __uint_as_float(__float_as_uint(dpp_f32<0x140>(v)) & use2);   // row_mirror: col ^ 15
+            v += __uint_as_float(__float_as_uint(dpp_f32<0x141>(v)) & use4);   // row_half_mirror: col ^ 7
+            v += __uint_as_float(__float_as_uint(dpp_f32<0x1B>(v)) & use8);    // quad [3,2,1,0]: col ^ 3
             sh[x] = v;
         }
         // mask, scale, optional spill, online softmax per column
@@ -378,9 +400,9 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
             const int row = p0 + 16 * (x / 4) + 4 * jj + (x % 4);
-            const bool ok = cvalid && row < r_end;
+            const bool ok = row < r_end;
             const float v = ok ? sh[x] * scale : -INFINITY;
-            if (logits && ok && gcol == 0) logits[((int64_t)s * Hq + hq) * m.cap + row] = v;
+            slog[(ok && cvalid && gcol == 0) ? hcol * rps + (row - r_begin) : G * rps + lane] = v;
             pv[x] = v;
             mx = fmaxf(mx, v);
         }
@@ -400,10 +422,12 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
             for (int t = 0; t < NDT; ++t) acc[t] *= alpha;
             m_run = m_new;
         }
+        // m_run is finite from the first page on (every split starts with a
+        // live row), so masked rows give exp(-inf) = 0 with no test
         float sum = 0.0f;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-            pv[x] = (pv[x] == -INFINITY) ? 0.0f : __expf(pv[x] - m_run);
+            pv[x] = __expf(pv[x] - m_run);
             sum += pv[x];
         }
         sum += __shfl_xor(sum, 16);
@@ -416,11 +440,16 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
         for (int e = 0; e < 8; ++e) {
             const GroupMeta mt = pair_of<MF>(cur.vm, e);
             const int row = p0 + (e < 4 ? 4 * jj + e : 16 + 4 * jj + e - 4);
-            const bool ok = cvalid && row < r_end;
-            const _Float16 b = ok ? (_Float16)(pv[e] * mt.scale) : (_Float16)0.0f;
+            // rows past the live count may hold stale meta: zero it (p is 0 there)
+            const bool ok = row < r_end;
+            const float sc = ok ? mt.scale : 0.0f, lo = ok ? mt.lo : 0.0f;
+            _Float16 b = (_Float16)(pv[e] * sc);
+            // pin the rounded f16: the correction -1024 * sum(b) cancels the
+            // MFMA's 1024 offset only if it adds exactly the operand's bits
+            asm volatile("" : "+v"(b));
             bop[e] = b;
             bs += (float)b;
-            zs += ok ? pv[e] * mt.lo : 0.0f;
+            zs += pv[e] * lo;
         }
         bsum += bs;
         zsum += zs;
@@ -430,12 +459,11 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t], 0, 0, 0);
         }
     };
-    // pages k and k+1 are in flight while page k is computed: three register
-    // buffers rotate through an unrolled-by-3 loop
     const int np = (r_end - r_begin + PAGE - 1) / PAGE;
     const int pg0 = r_begin / PAGE;
     auto fetch = [&](PageRegs<D, CB, MF>& b, int k) {
-        if (k < np) load_page(b, page_ptr(m, s, layer, h, pg0 + k), f, col, jj, gmeta);
+        // past the last page, reload the last one (no branch around the loads)
+        load_page(b, page_ptr(m, s, layer, h, pg0 + min(k, np - 1)), f, col, jj, gmeta);
     };
     // page k+1 is in flight while page k is computed (two buffers, unrolled by 2)
     PageRegs<D, CB, MF> b0, b1;
@@ -446,6 +474,15 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
         if (k + 1 >= np) break;
         fetch(b0, k + 2);
         step(b1, r_begin + (k + 1) * PAGE);
+    }
+    // staged logits of the split's rows, one coalesced pass per query head
+    if (logits) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int nr = r_end - r_begin;
+        for (int i = lane; i < G * nr; i += WAVE) {
+            const int g = i / nr, r = i % nr;
+            logits[((int64_t)s * Hq + h * G + g) * m.cap + r_begin + r] = slog[g * rps + r];
+        }
     }
     // totals of the per-column corrections over the 4 lane groups
     bsum += __shfl_xor(bsum, 16);
@@ -496,20 +533,34 @@ __global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int
     }
 }
 
-// score[row] += sum over query heads of exp(logit - max) / sum
+// score[row] += sum over query heads of exp(logit - max) / sum. A thread
+// takes 4 consecutive rows (16-byte loads of each head's logits); the heads'
+// (max, sum) sit in LDS.
+constexpr int MASS_ROWS = 4;
 __global__ void __launch_bounds__(256) draft_mass_kernel(dkv_drafter_t m, int layer, int Hq,
                                                          const float* __restrict__ logits,
                                                          const float* __restrict__ stats) {
+    extern __shared__ float st[];   // [Hq][2]
     const int s = blockIdx.y;
+    for (int i = threadIdx.x; i < 2 * Hq; i += blockDim.x) st[i] = stats[(int64_t)s * Hq * 2 + i];
+    __syncthreads();
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    float mass = 0.0f;
+    const int r0 = (blockIdx.x * blockDim.x + threadIdx.x) * MASS_ROWS;
+    if (r0 >= n) return;
+    float mass[MASS_ROWS] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* lg = logits + (int64_t)s * Hq * m.cap + r0;
     for (int hq = 0; hq < Hq; ++hq) {
-        const float mm = stats[((int64_t)s * Hq + hq) * 2], l = stats[((int64_t)s * Hq + hq) * 2 + 1];
-        mass += __expf(logits[((int64_t)s * Hq + hq) * m.cap + r] - mm) / l;
+        const float mm = st[2 * hq], l = st[2 * hq + 1];
+        const float4 x = *reinterpret_cast<const float4*>(lg + (int64_t)hq * m.cap);
+        mass[0] += __expf(x.x - mm) / l;
+        mass[1] += __expf(x.y - mm) / l;
+        mass[2] += __expf(x.z - mm) / l;
+        mass[3] += __expf(x.w - mm) / l;
     }
-    m.score[row_index(m, s, layer) + r] += static_cast<double>(mass);
+    double* sc = m.score + row_index(m, s, layer) + r0;
+#pragma unroll
+    for (int j = 0; j < MASS_ROWS; ++j)
+        if (r0 + j < n) sc[j] += static_cast<double>(mass[j]);
 }
 
 static size_t smem_bytes(int D) {
@@ -526,19 +577,30 @@ static bool fast_path(const dkv_drafter_t& m, const dkv_qcfg_t& c, int Hq) {
 
 using namespace dkv;
 
-static int n_splits_of(const dkv_drafter_t* m) {
-    const int rps = rows_per_split(*m);
+static int n_splits_of(const dkv_drafter_t* m, int n_q_heads) {
+    const int rps = rows_per_split(*m, n_q_heads / std::max(m->n_kv_heads, 1));
     return (m->cap + rps - 1) / rps;
+}
+
+// workspace sections, each starting on a 256-byte boundary: partials
+// [b][Hq][splits][D+2], stats [b][Hq][2], logits [b][Hq][cap] (with mass)
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+struct DraftWork {
+    size_t stats_off, logits_off, bytes;
+};
+static DraftWork draft_work(const dkv_drafter_t& m, int n_q_heads, int want_mass) {
+    const size_t b = m.batch, D = m.head_dim;
+    DraftWork w;
+    w.stats_off = align256(sizeof(float) * b * n_q_heads * n_splits_of(&m, n_q_heads) * (D + 2));
+    w.logits_off = align256(w.stats_off + sizeof(float) * b * n_q_heads * 2);
+    w.bytes = want_mass ? w.logits_off + sizeof(float) * b * n_q_heads * (size_t)m.cap : w.logits_off;
+    return w;
 }
 
 extern "C" size_t dkv_drafter_attention_workspace(const dkv_drafter_t* mirror, int32_t n_q_heads,
                                                   int32_t want_mass) {
     if (!mirror || n_q_heads <= 0) return 0;
-    const size_t b = mirror->batch, D = mirror->head_dim;
-    size_t bytes = sizeof(float) * b * n_q_heads * n_splits_of(mirror) * (D + 2);   // partials
-    bytes += sizeof(float) * b * n_q_heads * 2;                                      // stats
-    if (want_mass) bytes += sizeof(float) * b * n_q_heads * (size_t)mirror->cap;     // logits
-    return bytes;
+    return draft_work(*mirror, n_q_heads, want_mass).bytes;
 }
 
 extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t cfg, const float* q,
@@ -557,17 +619,20 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     const size_t need = dkv_drafter_attention_workspace(mirror, n_q_heads, want_mass);
     if (!work || work_bytes < need)
         return fail(DKV_EWORKSPACE, "dkv_drafter_attention: workspace too small (need " + std::to_string(need) + ")");
-    const int ns = n_splits_of(mirror), rps = rows_per_split(m);
+    const int G = n_q_heads / m.n_kv_heads;
+    const int ns = n_splits_of(mirror, n_q_heads), rps = rows_per_split(m, G);
+    const DraftWork wl = draft_work(m, n_q_heads, want_mass);
     float* part = static_cast<float*>(work);
-    float* stats = part + (size_t)m.batch * n_q_heads * ns * (m.head_dim + 2);
-    float* logits = want_mass ? stats + (size_t)m.batch * n_q_heads * 2 : nullptr;
+    float* stats = reinterpret_cast<float*>(static_cast<char*>(work) + wl.stats_off);
+    float* logits = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.logits_off) : nullptr;
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
     if (fast_path(m, cfg, n_q_heads)) {
         const dim3 grid((ns + 3) / 4, m.n_kv_heads, m.batch);
         const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
-#define DKV_LAUNCH(DD, CC, MM)                                                                                    \
-    hipLaunchKernelGGL((draft_attn_mfma_kernel<DD, CC, MM>), grid, dim3(256), 0, st, m, layer, cfg, q, n_q_heads, \
+        const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + WAVE);
+#define DKV_LAUNCH(DD, CC, MM)                                                                                      \
+    hipLaunchKernelGGL((draft_attn_mfma_kernel<DD, CC, MM>), grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, \
                        scale, rps, ns, part, logits)
         switch (key) {
             case 0: DKV_LAUNCH(64, 4, 0); break;
@@ -590,8 +655,9 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
                        rps, ns, out, stats);
     if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
     if (want_mass) {
-        hipLaunchKernelGGL(draft_mass_kernel, dim3((m.cap + 255) / 256, m.batch), dim3(256), 0, st, m, layer,
-                           n_q_heads, logits, stats);
+        const int per_block = 256 * MASS_ROWS;
+        hipLaunchKernelGGL(draft_mass_kernel, dim3((m.cap + per_block - 1) / per_block, m.batch), dim3(256),
+                           sizeof(float) * 2 * n_q_heads, st, m, layer, n_q_heads, logits, stats);
         rc = check_launch("dkv_drafter_attention(mass)");
     }
     return rc;
