@@ -290,7 +290,10 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     constexpr int NSTEP = D / 32;     // k-steps of the QK product
     constexpr int NDT = D / 16;       // d-tiles of the PV product
     constexpr int DL = D / 4;         // channels per lane group in QK
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    // the wave index through readfirstlane: the compiler then knows it (and
+    // the split, row range and page addresses) to be wave-uniform, keeps them
+    // in scalar registers and runs the page loop as a scalar loop
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
     const int split = blockIdx.x * 4 + wave;
     if (split >= n_splits) return;
     const int h = blockIdx.y, s = blockIdx.z;
@@ -324,17 +327,22 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
     f16x8_t qhi[NSTEP], qlo[NSTEP];
     float qsum = 0.0f;
     {
-        // loads are unconditional (hq is a valid head for every lane); the
-        // column's group mask is a select, so no branch per element
-        const float* qr = q + ((int64_t)s * Hq + hq) * D + DL * jj;
+        // the lane's DL channels as DL/4 vector loads, all in flight at once
+        // (hq is a valid head for every lane); the column's group mask is a
+        // bit mask, so the loads stay unconditional
+        const float4* qr = reinterpret_cast<const float4*>(q + ((int64_t)s * Hq + hq) * D + DL * jj);
+        float4 qv[DL / 4];
+#pragma unroll
+        for (int x = 0; x < DL / 4; ++x) qv[x] = qr[x];
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = DL * jj + 8 * st + e;
-                float raw = qr[8 * st + e];
-                asm volatile("" : "+v"(raw));   // load unconditionally (no branch per element)
-                const float v = (cvalid && d / group == gcol) ? raw : 0.0f;
+                const float4 w4 = qv[(8 * st + e) / 4];
+                const float raw = (e % 4 == 0) ? w4.x : (e % 4 == 1) ? w4.y : (e % 4 == 2) ? w4.z : w4.w;
+                const uint32_t keep = (cvalid && d / group == gcol) ? 0xFFFFFFFFu : 0u;
+                const float v = __uint_as_float(__float_as_uint(raw) & keep);
                 const _Float16 hi = (_Float16)v;
                 const _Float16 lo = (_Float16)(v - (float)hi);
                 qhi[st][e] = hi;
@@ -466,13 +474,18 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
         load_page(b, page_ptr(m, s, layer, h, pg0 + min(k, np - 1)), f, col, jj, gmeta);
     };
     // page k+1 is in flight while page k is computed (two buffers, unrolled by 2)
+    // The scheduling barriers keep each fetch ahead of the page's products:
+    // left alone, the scheduler sinks the loads into the QK MFMAs, so the
+    // next page's latency hides behind half a page instead of a whole one.
     PageRegs<D, CB, MF> b0, b1;
     fetch(b0, 0);
     for (int k = 0; k < np; k += 2) {
         fetch(b1, k + 1);
+        __builtin_amdgcn_sched_barrier(0);
         step(b0, r_begin + k * PAGE);
         if (k + 1 >= np) break;
         fetch(b0, k + 2);
+        __builtin_amdgcn_sched_barrier(0);
         step(b1, r_begin + (k + 1) * PAGE);
     }
     // staged logits of the split's rows, one coalesced pass per query head
@@ -627,7 +640,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     float* logits = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.logits_off) : nullptr;
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
-    if (fast_path(m, cfg, n_q_heads)) {
+    // the fast path reads q rows with 16-byte vector loads
+    if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
         const dim3 grid((ns + 3) / 4, m.n_kv_heads, m.batch);
         const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
         const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + WAVE);

@@ -189,8 +189,9 @@ __global__ void __launch_bounds__(256) paged_attn_kernel(dkv_paged_t c, int laye
 }
 
 // ---------------------------------------------------------------- MFMA path
-// bf16 cache with 16-token blocks. One wave owns 16 query rows (a "q-tile")
-// and walks its block's key chunk 32 keys (two blocks) at a time:
+// bf16 cache with 16-token blocks, D = 64 or 128. A workgroup owns one
+// (sequence, KV head, key chunk) and W q-tiles of 16 query rows, one wave per
+// q-tile, and walks the chunk 32 keys (two blocks) per step:
 //   S^T[16 keys][16 rows] = K[16 keys][D] . Q^T     (v_mfma_f32_16x16x32_bf16)
 //   O^T[16 d][16 rows]   += V^T[16 d][32 keys] . P^T
 // Q and P are split into bf16 hi + lo parts (two MFMAs each), which keeps the
@@ -198,50 +199,114 @@ __global__ void __launch_bounds__(256) paged_attn_kernel(dkv_paged_t c, int laye
 // accumulator a lane holds keys 4*(l/16)+r of one query row l%16; the PV
 // B operand wants 8 keys of one row per lane, so the k-slots of the PV
 // product are ordered {4j..4j+3, 16+4j..16+4j+3} (j = l/16) and the
-// probabilities never leave their lane. V is stored transposed per block, so
-// the matching V^T A operand is two 8-byte loads per lane.
-// Within the QK product lane group j owns d in [j*D/4, (j+1)*D/4): a lane
-// reads D/4 contiguous K elements of its key and the same slice of q.
-// Every per-row operation depends only on absolute key positions, so a
-// row's partial is identical for any T (batch invariance).
+// probabilities never leave their lane. Within the QK product lane group j
+// owns d in [j*D/4, (j+1)*D/4).
+//
+// Staging. The K and V of a step go to LDS through direct-to-LDS loads
+// (global_load_lds_dwordx4), VERIFY_STAGES steps deep, so HBM latency hides
+// behind the products of earlier steps without holding registers, and the
+// workgroup reads each byte of its chunk from HBM once whatever the number
+// of q-tiles. K lands in the order of the QK A operand (slot (tile, k-step)
+// = 1 KB, 16 B per lane), so an operand read is one conflict-free
+// ds_read_b128; V keeps the block's V^T layout [d][16 keys]. The loads are
+// issued from inline asm and waited for by hand (s_waitcnt vmcnt + s_barrier):
+// the compiler's own tracking of LDS DMA would make every LDS read wait for
+// all loads in flight, prefetches included.
+//
+// Every per-row operation depends only on absolute key positions (keys past a
+// row's position add exact zeros, with the rescale factor exactly 1), and
+// floating-point contraction is off, so a row's partial is bit-identical for
+// any T and any W (batch invariance between verify and decode).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ __bf16 to_bf16(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16_rne(f)); }
-__device__ __forceinline__ float from_bf16(__bf16 h) { return bf16_to_f32(__builtin_bit_cast(uint16_t, h)); }
+// round to nearest even in hardware (v_cvt_pk_bf16_f32); the split operands
+// are finite, where this equals the integer rounding of f32_to_bf16_rne
+__device__ __forceinline__ __bf16 to_bf16(float f) { return (__bf16)f; }
+__device__ __forceinline__ float from_bf16(__bf16 h) { return (float)h; }
 
 template <int D>
-__global__ void __launch_bounds__(256) paged_attn_mfma_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
-                                                              int T, int Hq, const int32_t* __restrict__ start,
-                                                              int CH, int n_chunks, int n_qtiles, float scale,
-                                                              float* __restrict__ part) {
-    constexpr int NSTEP = D / 32;      // k-steps of the QK product
+struct VerifyStage {
+    static constexpr int NSTEP = D / 32;               // k-steps of the QK product
+    static constexpr int K_BYTES = 2 * NSTEP * 1024;   // two 16-key tiles, operand order
+    static constexpr int V_BLOCK = D * 16 * 2;         // one block's V^T of one head
+    static constexpr int NVI = V_BLOCK / 1024;         // 1 KB loads per V block
+    static constexpr int NI = 2 * NSTEP + 2 * NVI;     // 1 KB loads per step
+    static constexpr int BYTES = K_BYTES + 2 * V_BLOCK;
+};
+constexpr int VERIFY_STAGES = 3;
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from g to LDS byte address lds + 16 * lane (m0 = base)
+__device__ __forceinline__ void dma_b128(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// at most N of this wave's loads still in flight, its LDS reads done, then
+// the workgroup barrier
+template <int N>
+__device__ __forceinline__ void wait_loads_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// keys at or past the cache end read as zero (their probability is 0, and
+// 0 * garbage could be NaN): mask of the 4 bf16 keys starting nv before it
+__device__ __forceinline__ uint64_t key_mask4(int nv) {
+    return nv >= 4 ? ~0ull : nv <= 0 ? 0ull : (1ull << (16 * nv)) - 1ull;
+}
+
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
+                                                                 int T, int Hq, const int32_t* __restrict__ start,
+                                                                 int CH, int n_qgroups, int n_chunks, int n_qtiles,
+                                                                 float scale, float* __restrict__ part) {
+#pragma clang fp contract(off)
+    using St = VerifyStage<D>;
+    constexpr int S = VERIFY_STAGES;
+    constexpr int NSTEP = St::NSTEP;
     constexpr int NDT = D / 16;        // d-tiles of the PV product
     constexpr int DL = D / 4;          // d elements per lane group in QK
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int qb = blockIdx.x % ((n_qtiles + 3) / 4), chunk = blockIdx.x / ((n_qtiles + 3) / 4);
-    const int qtile = qb * 4 + wave;
-    if (qtile >= n_qtiles) return;
+    constexpr int LPW = St::NI / W;    // loads per wave per step
+    static_assert(St::NI % W == 0, "a step's loads split evenly over the waves");
+    // wave index through readfirstlane: the q-tile and everything derived
+    // from it are then wave-uniform (scalar registers and branches)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int qg = blockIdx.x % n_qgroups, chunk = blockIdx.x / n_qgroups;
     const int h = blockIdx.y, s = blockIdx.z;
     const int G = Hq / c.n_kv_heads;
     const int s0 = start[s];
     const int len = s0 + T;
     const int k_begin = chunk * CH;
-    if (k_begin >= len) return;
-    const int col = lane % 16, jj = lane / 16;
-    const int r0 = qtile * 16;
     const int n_rows = T * G;
-    const int last_row = min(r0 + 15, n_rows - 1);
+    // the group's last row bounds the keys any of its rows may see
+    const int last_row = min((qg + 1) * W * 16, n_rows) - 1;
     const int max_qpos = s0 + last_row / G;
-    if (k_begin > max_qpos) return;
+    if (k_begin >= len || k_begin > max_qpos) return;   // uniform over the workgroup
     const int k_end = min(min(k_begin + CH, len), max_qpos + 1);
-
-    // this lane's query row
-    const int r = r0 + col;
-    const bool rvalid = r < n_rows;
+    const int nsteps = (k_end - k_begin + 31) / 32;
+    const int qtile = qg * W + wave;
+    const bool active = qtile < n_qtiles;               // wave-uniform
+    const int col = lane % 16, jj = lane / 16;
+    const int r = qtile * 16 + col;
+    const bool rvalid = active && r < n_rows;
     const int t = rvalid ? r / G : 0;
     const int hq = h * G + (rvalid ? r % G : 0);
     const int qpos = s0 + t;
+
+    extern __shared__ __align__(16) char lds[];
+    // block ids of the keys [k_begin, min(k_begin + 32 * nsteps, len))
+    int32_t* sblk = reinterpret_cast<int32_t*>(lds + S * St::BYTES);
+    {
+        const int32_t* btab = c.block_table + ((int64_t)s * c.n_layers + layer) * c.max_blocks + k_begin / 16;
+        const int nblk = (min(k_begin + 32 * nsteps, len) - k_begin + 15) / 16;
+        for (int i = threadIdx.x; i < nblk; i += 64 * W) sblk[i] = btab[i];
+    }
 
     bf16x8_t qhi[NSTEP], qlo[NSTEP];
     {
@@ -256,38 +321,57 @@ __global__ void __launch_bounds__(256) paged_attn_mfma_kernel(dkv_paged_t c, int
                 qlo[st][e] = to_bf16(v - from_bf16(hi));
             }
     }
+    __syncthreads();   // block ids visible (no staging load is in flight yet)
+
+    const uint16_t* pool = static_cast<const uint16_t*>(c.pool);
+    const int64_t bel = paged_block_elems(c);
+    const int64_t vbase = (int64_t)c.n_kv_heads * 16 * D;
+    // this wave's share of the loads of step j, into stage j % S
+    auto issue = [&](int j) {
+        const int kb = k_begin + 32 * j;
+        const int32_t b0 = sblk[2 * j];
+        const int32_t b1 = (kb + 16 < len) ? sblk[2 * j + 1] : b0;
+        const uint32_t base = lds_offset(lds + (j % S) * St::BYTES);
+#pragma unroll
+        for (int x = 0; x < LPW; ++x) {
+            const int i = wave * LPW + x;   // load index within the step (uniform)
+            const uint16_t* g;
+            if (i < 2 * NSTEP) {            // K tile a, k-step st: 16 B of row col
+                const int a = i / NSTEP, st = i % NSTEP;
+                g = pool + (int64_t)(a ? b1 : b0) * bel + ((int64_t)h * 16 + col) * D + DL * jj + 8 * st;
+            } else {                        // V^T of block a, 1 KB piece pc, linear
+                const int v = i - 2 * NSTEP, a = v / St::NVI, pc = v % St::NVI;
+                g = pool + (int64_t)(a ? b1 : b0) * bel + vbase + (int64_t)h * D * 16 + (pc * 64 + lane) * 8;
+            }
+            dma_b128(g, base + i * 1024);
+        }
+    };
+
     f32x4_t acc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const uint16_t* pool = static_cast<const uint16_t*>(c.pool);
-    const int64_t bel = paged_block_elems(c);
-    const int64_t vbase = (int64_t)c.n_kv_heads * 16 * D;
-    const int32_t* btab = c.block_table + ((int64_t)s * c.n_layers + layer) * c.max_blocks;
-
-    for (int kb = k_begin; kb < k_end; kb += 32) {
-        const int32_t blk0 = btab[kb / 16];
-        const bool has1 = kb + 16 < len;
-        const int32_t blk1 = has1 ? btab[kb / 16 + 1] : blk0;
+    for (int j = 0; j < S - 1; ++j)
+        if (j < nsteps) issue(j);
+    for (int i = 0; i < nsteps; ++i) {
+        // this wave's loads of step i are done once at most those of the
+        // S-2 later steps remain; the barrier makes every wave's loads of
+        // step i visible and frees stage (i-1) % S for step i+S-1
+        if (i + S - 2 < nsteps) wait_loads_barrier<(S - 2) * LPW>();
+        else wait_loads_barrier<0>();
+        if (i + S - 1 < nsteps) issue(i + S - 1);
+        if (!active) continue;
+        const int kb = k_begin + 32 * i;
+        const char* stage = lds + (i % S) * St::BYTES;
         // ---- S^T for the two 16-key tiles
         f32x4_t sacc[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-            const int key = kb + 16 * a + col;
-            const int32_t blk = a ? blk1 : blk0;
-            const uint16_t* kr = pool + (int64_t)blk * bel + ((int64_t)h * 16 + col) * D + DL * jj;
-            const bool kvalid = key < len;
             f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < NSTEP; ++st) {
-                bf16x8_t kv;
-                if (kvalid) {
-                    const uint4 w = *reinterpret_cast<const uint4*>(kr + 8 * st);
-                    kv = __builtin_bit_cast(bf16x8_t, w);
-                } else {
-                    kv = bf16x8_t{};
-                }
+                const bf16x8_t kv = *reinterpret_cast<const bf16x8_t*>(stage + (a * NSTEP + st) * 1024 + lane * 16);
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qhi[st], sa, 0, 0, 0);
                 sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qlo[st], sa, 0, 0, 0);
             }
@@ -310,49 +394,42 @@ __global__ void __launch_bounds__(256) paged_attn_mfma_kernel(dkv_paged_t c, int
         const float m_new = fmaxf(m_run, mx);
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            p[i] = (p[i] == -INFINITY) ? 0.0f : __expf(p[i] - m_new);
-            sum += p[i];
+        for (int k = 0; k < 8; ++k) {
+            p[k] = (p[k] == -INFINITY) ? 0.0f : __expf(p[k] - m_new);
+            sum += p[k];
         }
         sum += __shfl_xor(sum, 16);
         sum += __shfl_xor(sum, 32);
-        const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
+        // alpha is exactly 1 when the row's max did not move (exp(0) = 1, and
+        // a row with no live key yet has o = 0 and l = 0 either way), so the
+        // accumulators need rescaling only when some row of the wave moved
+        const float alpha = (m_new == m_run) ? 1.0f : (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
         l_run = l_run * alpha + sum;
         m_run = m_new;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+        }
         bf16x8_t phi, plo;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const __bf16 hi = to_bf16(p[i]);
-            phi[i] = hi;
-            plo[i] = to_bf16(p[i] - from_bf16(hi));
+        for (int k = 0; k < 8; ++k) {
+            const __bf16 hi = to_bf16(p[k]);
+            phi[k] = hi;
+            plo[k] = to_bf16(p[k] - from_bf16(hi));
         }
         // ---- O^T += V^T . P^T over the 32 keys
-        const uint16_t* v0 = pool + (int64_t)blk0 * bel + vbase + (int64_t)h * D * 16 + 4 * jj;
-        const uint16_t* v1 = pool + (int64_t)blk1 * bel + vbase + (int64_t)h * D * 16 + 4 * jj;
-        // 4 consecutive keys of V^T row d; keys at or past the cache end read as
-        // zero (their probability is 0, and 0 * garbage could be NaN)
-        auto ld4 = [&](const uint16_t* p, int first_key) -> uint2 {
-            const int nv = len - first_key;
-            if (nv <= 0) return uint2{0u, 0u};
-            uint2 w = *reinterpret_cast<const uint2*>(p);
-            if (nv < 4) {
-                const unsigned long long m = (1ull << (16 * nv)) - 1ull;
-                w.x &= static_cast<unsigned>(m);
-                w.y &= static_cast<unsigned>(m >> 32);
-            }
-            return w;
-        };
+        const char* vs = stage + St::K_BYTES;
+        const uint64_t m0 = key_mask4(len - (kb + 4 * jj)), m1 = key_mask4(len - (kb + 16 + 4 * jj));
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             const int d = 16 * dt + col;
-            const uint2 lo2 = ld4(v0 + (int64_t)d * 16, kb + 4 * jj);
-            const uint2 hi2 = ld4(v1 + (int64_t)d * 16, kb + 16 + 4 * jj);
-            const uint4 w = {lo2.x, lo2.y, hi2.x, hi2.y};
+            const uint2 lo2 = *reinterpret_cast<const uint2*>(vs + (d * 16 + 4 * jj) * 2);
+            const uint2 hi2 = *reinterpret_cast<const uint2*>(vs + St::V_BLOCK + (d * 16 + 4 * jj) * 2);
+            const uint4 w = {lo2.x & (uint32_t)m0, lo2.y & (uint32_t)(m0 >> 32), hi2.x & (uint32_t)m1,
+                             hi2.y & (uint32_t)(m1 >> 32)};
             const bf16x8_t vv = __builtin_bit_cast(bf16x8_t, w);
-            f32x4_t o = acc[dt] * alpha;
-            o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, phi, o, 0, 0, 0);
-            o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, plo, o, 0, 0, 0);
-            acc[dt] = o;
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, phi, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, plo, acc[dt], 0, 0, 0);
         }
     }
     if (!rvalid) return;
@@ -447,14 +524,35 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
     // pass and a one-token decode step take the same arithmetic path
     const bool mfma = c.dtype == DKV_BF16 && c.block_size == 16 && (c.head_dim == 64 || c.head_dim == 128);
     if (mfma) {
-        const int qblocks = (n_qtiles + 3) / 4;
-        const dim3 grid(n_chunks * qblocks, c.n_kv_heads, c.batch), blk(64 * std::min(4, n_qtiles));
-        if (c.head_dim == 128)
-            hipLaunchKernelGGL(dkv::paged_attn_mfma_kernel<128>, grid, blk, 0, st, c, layer, q, T, n_q_heads, start,
-                               chunk_keys, n_chunks, n_qtiles, scale, static_cast<float*>(work));
-        else
-            hipLaunchKernelGGL(dkv::paged_attn_mfma_kernel<64>, grid, blk, 0, st, c, layer, q, T, n_q_heads, start,
-                               chunk_keys, n_chunks, n_qtiles, scale, static_cast<float*>(work));
+        // one wave per q-tile, up to 8 per workgroup (a power of two, so a
+        // step's loads split evenly); staged steps plus the chunk's block ids
+        const int W = n_qtiles <= 1 ? 1 : n_qtiles <= 2 ? 2 : n_qtiles <= 4 ? 4 : 8;
+        const int n_qgroups = (n_qtiles + W - 1) / W;
+        DKV_REQUIRE((int64_t)n_chunks * n_qgroups < (1LL << 31), "dkv_paged_attention: grid too large");
+        const size_t stage = c.head_dim == 128 ? dkv::VerifyStage<128>::BYTES : dkv::VerifyStage<64>::BYTES;
+        const size_t lds = dkv::VERIFY_STAGES * stage + (((size_t)chunk_keys / 16 * 4 + 15) & ~size_t(15));
+        DKV_REQUIRE(lds <= 64 * 1024, "dkv_paged_attention: chunk_keys too large for the bf16 kernel (max 16384)");
+        const dim3 grid(n_chunks * n_qgroups, c.n_kv_heads, c.batch), blk(64 * W);
+        float* part = static_cast<float*>(work);
+#define DKV_VERIFY(DD, WW)                                                                                          \
+    hipLaunchKernelGGL((dkv::paged_attn_mfma_kernel<DD, WW>), grid, blk, lds, st, c, layer, q, T, n_q_heads, start, \
+                       chunk_keys, n_qgroups, n_chunks, n_qtiles, scale, part)
+        if (c.head_dim == 128) {
+            switch (W) {
+                case 1: DKV_VERIFY(128, 1); break;
+                case 2: DKV_VERIFY(128, 2); break;
+                case 4: DKV_VERIFY(128, 4); break;
+                default: DKV_VERIFY(128, 8); break;
+            }
+        } else {
+            switch (W) {
+                case 1: DKV_VERIFY(64, 1); break;
+                case 2: DKV_VERIFY(64, 2); break;
+                case 4: DKV_VERIFY(64, 4); break;
+                default: DKV_VERIFY(64, 8); break;
+            }
+        }
+#undef DKV_VERIFY
     } else {
         hipLaunchKernelGGL(dkv::paged_attn_kernel, dim3(n_chunks * n_qtiles, c.n_kv_heads, c.batch), dim3(256),
                            dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, chunk_keys, n_chunks,
