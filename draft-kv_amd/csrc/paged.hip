@@ -234,7 +234,7 @@ struct VerifyStage {
     static constexpr int NI = 2 * NSTEP + 2 * NVI;     // 1 KB loads per step
     static constexpr int BYTES = K_BYTES + 2 * V_BLOCK;
 };
-constexpr int VERIFY_STAGES = 3;
+constexpr int VERIFY_STAGES = 2;
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -531,12 +531,19 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
         DKV_REQUIRE((int64_t)n_chunks * n_qgroups < (1LL << 31), "dkv_paged_attention: grid too large");
         const size_t stage = c.head_dim == 128 ? dkv::VerifyStage<128>::BYTES : dkv::VerifyStage<64>::BYTES;
         const size_t lds = dkv::VERIFY_STAGES * stage + (((size_t)chunk_keys / 16 * 4 + 15) & ~size_t(15));
-        DKV_REQUIRE(lds <= 64 * 1024, "dkv_paged_attention: chunk_keys too large for the bf16 kernel (max 16384)");
+        // gfx950 gives a workgroup up to 160 KB of LDS
+        DKV_REQUIRE(lds <= 160 * 1024, "dkv_paged_attention: chunk_keys too large for the bf16 kernel");
         const dim3 grid(n_chunks * n_qgroups, c.n_kv_heads, c.batch), blk(64 * W);
         float* part = static_cast<float*>(work);
-#define DKV_VERIFY(DD, WW)                                                                                          \
-    hipLaunchKernelGGL((dkv::paged_attn_mfma_kernel<DD, WW>), grid, blk, lds, st, c, layer, q, T, n_q_heads, start, \
-                       chunk_keys, n_qgroups, n_chunks, n_qtiles, scale, part)
+#define DKV_VERIFY(DD, WW)                                                                                         \
+    do {                                                                                                           \
+        auto kfn = dkv::paged_attn_mfma_kernel<DD, WW>;                                                            \
+        if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),                             \
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+            return dkv::fail(DKV_ELAUNCH, "dkv_paged_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
+        hipLaunchKernelGGL(kfn, grid, blk, lds, st, c, layer, q, T, n_q_heads, start, chunk_keys, n_qgroups,       \
+                           n_chunks, n_qtiles, scale, part);                                                       \
+    } while (0)
         if (c.head_dim == 128) {
             switch (W) {
                 case 1: DKV_VERIFY(128, 1); break;

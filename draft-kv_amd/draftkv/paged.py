@@ -92,7 +92,7 @@ class PagedKVCache:
 
     def __init__(self, n_layers: int, n_heads: int, d_head: int, block_size: int = 16,
                  n_blocks: int = 512, dtype=np.float32, *, batch: int = 1,
-                 max_tokens: Optional[int] = None, device=None, chunk_keys: int = 512) -> None:
+                 max_tokens: Optional[int] = None, device=None, chunk_keys: int = 2048) -> None:
         self.n_layers, self.n_heads, self.d_head = n_layers, n_heads, d_head
         self.block_size, self.n_blocks, self.batch = block_size, n_blocks, batch
         self.dtype = _torch_dtype(dtype)
