@@ -3,7 +3,8 @@
     python draft-kv_amd/build.py [-j N]
 
 Every source is compiled with hipcc for gfx950 only, with packed-fp32 code
-generation disabled (-Xclang -target-feature -Xclang -packed-fp32-ops), then
+generation disabled (-Xclang -target-feature -Xclang -packed-fp32-ops) and
+MFMA accumulators kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form), then
 linked into one shared library exporting the C ABI of include/draftkv_hip.h.
 """
 
@@ -22,8 +23,11 @@ LIB = os.path.join(OUT_DIR, "libdraftkv_hip.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs (gfx950 allows it), so
+# a VALU rescale of an accumulator needs no AGPR <-> VGPR copies
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wno-unused-result"]
 
 

@@ -12,19 +12,24 @@
 //
 // Fast path (4/8-bit codes, D = 64 or 128, groups a multiple of 16,
 // G * groups <= 16): v_mfma_f32_16x16x32_f16 on the raw codes.
+//   Codes enter the MFMA as f16 subnormals: the bits (word & 0x000F000F)
+//   read as an f16 pair are exactly (code * 2^-24, code' * 2^-24), and the
+//   MFMA keeps subnormal inputs, so one AND (plus a shift) turns two codes
+//   into an exact operand. The 2^24 is folded into the softmax scale (QK) and
+//   into the output (PV).
 //   QK: S'[16 rows][16 cols] = code . Qg^T, where column j = (group g, head
 //       h) holds q_h restricted to group g (zero elsewhere), split into f16
-//       hi + lo parts. The magic-number conversion (code | 0x6400) gives the
-//       exact f16 value 1024 + code in one and/or per two codes; a packed f16
-//       subtract removes the 1024 exactly. Folding scale and zero in fp32 per
-//       (row, group) and summing the group columns of a head gives its logit:
+//       hi + lo parts. Folding scale and zero in fp32 per (row, group) and
+//       summing the group columns of a head gives its logit:
 //         s_h = sum_g scale_g * S'[g,h] + lo_g * sum_{d in g} q_h[d]
-//   PV: O'[16 d][16 cols] = (1024 + code_V)^T . B with B[row][(g,h)] =
+//   PV: O'[16 d][16 cols] = code_V^T . B with B[row][(g,h)] =
 //       f16(p_h[row] * scaleV_g[row]); then
-//         o_h[d] = O'[d][(g(d),h)] - 1024 * sum_rows B + sum_rows p_h * loV_g
+//         o_h[d] = O'[d][(g(d),h)] + sum_rows p_h * loV_g
 // The accumulator lanes of the QK product already hold the 8 rows of one
 // column that the PV B operand needs, so probabilities never move between
 // lanes; the V page layout (mirror_layout.h) is the PV A operand.
+#include <type_traits>
+
 #include "mirror_layout.h"
 
 namespace dkv {
@@ -169,55 +174,26 @@ __global__ void __launch_bounds__(256) draft_attn_kernel(dkv_drafter_t m, int la
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+constexpr float kTwo24 = 16777216.0f;            // 2^24
+constexpr float kTwoM24 = 1.0f / 16777216.0f;    // 2^-24
 
-// 8 codes of one word (cb 4) or two words (cb 8) -> f16 (1024 + code) x 8
+// 8 codes of one word (cb 4) or two words (cb 8) -> 8 f16 subnormals
+// code * 2^-24 (the interleaved word order of mirror_layout.h puts two codes
+// in the low bits of the two halves)
 template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w, uint32_t magic);
-
-// the same codes as exact f16 integers (one packed f16 subtract per pair):
-// the QK fold multiplies by the group scale, so an uncancelled 1024 offset
-// would cost precision when scales are large
-template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16_exact(const uint32_t* w, uint32_t magic) {
-    f16x8_t x = codes_to_f16<CB>(w, magic);
-    const f16x2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f16x2_t p = {x[2 * i], x[2 * i + 1]};
-        p = p - off;
-        x[2 * i] = p[0];
-        x[2 * i + 1] = p[1];
-    }
-    return x;
-}
-
-// (x & mask) | 0x64006400. Written as a bitfield insert of x into an opaque
-// copy of the constant, so it becomes one v_bfi_b32 instead of an and + or
-// (the constant would otherwise fold and the pattern be lost).
-__device__ __forceinline__ uint32_t magic_f16x2() {
-    uint32_t y;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(y));
-    return y;
-}
-__device__ __forceinline__ uint32_t and_or_magic(uint32_t x, uint32_t mask, uint32_t magic) {
-    return (x & mask) | (magic & ~mask);
-}
-
-template <int CB>
-__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w, uint32_t magic) {
+__device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w) {
     uint4 r;
     if (CB == 4) {
         const uint32_t x = w[0];
-        r.x = and_or_magic(x, 0x000F000Fu, magic);
-        r.y = and_or_magic(x >> 4, 0x000F000Fu, magic);
-        r.z = and_or_magic(x >> 8, 0x000F000Fu, magic);
-        r.w = and_or_magic(x >> 12, 0x000F000Fu, magic);
+        r.x = x & 0x000F000Fu;
+        r.y = (x >> 4) & 0x000F000Fu;
+        r.z = (x >> 8) & 0x000F000Fu;
+        r.w = (x >> 12) & 0x000F000Fu;
     } else {
-        r.x = and_or_magic(w[0], 0x00FF00FFu, magic);
-        r.y = and_or_magic(w[0] >> 8, 0x00FF00FFu, magic);
-        r.z = and_or_magic(w[1], 0x00FF00FFu, magic);
-        r.w = and_or_magic(w[1] >> 8, 0x00FF00FFu, magic);
+        r.x = w[0] & 0x00FF00FFu;
+        r.y = (w[0] >> 8) & 0x00FF00FFu;
+        r.z = w[1] & 0x00FF00FFu;
+        r.w = (w[1] >> 8) & 0x00FF00FFu;
     }
     return __builtin_bit_cast(f16x8_t, r);
 }
@@ -236,7 +212,7 @@ struct PageRegs {
 };
 
 template <int N>
-__device__ __forceinline__ void load_words(uint32_t (&dst)[N], const uint32_t* src) {
+__device__ __forceinline__ void load_words(uint32_t (&dst)[N], const uint8_t* src) {
     if constexpr (N % 4 == 0) {
 #pragma unroll
         for (int x = 0; x < N / 4; ++x) {
@@ -248,92 +224,128 @@ __device__ __forceinline__ void load_words(uint32_t (&dst)[N], const uint32_t* s
         }
     } else {
 #pragma unroll
-        for (int x = 0; x < N; ++x) dst[x] = src[x];
+        for (int x = 0; x < N; ++x) dst[x] = reinterpret_cast<const uint32_t*>(src)[x];
     }
 }
 
-template <int MF>
-__device__ __forceinline__ GroupMeta pair_of(const uint32_t* w, int k) {
-    if (MF) return {half_bits_to_f32(w[k] & 0xffffu), half_bits_to_f32(w[k] >> 16)};
-    return {__uint_as_float(w[2 * k]), __uint_as_float(w[2 * k + 1])};
-}
+// byte offsets of a lane's operands inside a page (the same for every page)
+struct LaneOffsets {
+    uint32_t k[2], km[2], v, vm;
+};
 
 template <int D, int CB, int MF>
-__device__ __forceinline__ void load_page(PageRegs<D, CB, MF>& r, const uint8_t* pg, const PageFmt& f, int col, int jj,
-                                          int gmeta) {
-    using R = PageRegs<D, CB, MF>;
+__device__ __forceinline__ void load_page(PageRegs<D, CB, MF>& r, const uint8_t* pg, const LaneOffsets& o) {
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
-        load_words(r.k[a], reinterpret_cast<const uint32_t*>(pg + f.kc + (int64_t)(16 * a + col) * (D * CB / 8)) +
-                               R::WPL * jj);
-        load_words(r.km[a], reinterpret_cast<const uint32_t*>(pg + k_meta_off(f, 16 * a + 4 * jj, gmeta)));
+        load_words(r.k[a], pg + o.k[a]);
+        load_words(r.km[a], pg + o.km[a]);
     }
-    load_words(r.v, reinterpret_cast<const uint32_t*>(pg + f.vc) + (col * 4 + jj) * R::NV);
-    load_words(r.vm, reinterpret_cast<const uint32_t*>(pg + f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB));
+    load_words(r.v, pg + o.v);
+    load_words(r.vm, pg + o.vm);
+}
+
+// (scale, lo) pair k of a lane's meta words
+template <int MF>
+__device__ __forceinline__ float meta_scale(const uint32_t* w, int k) {
+    if (MF) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] & 0xffffu));
+    return __uint_as_float(w[2 * k]);
+}
+template <int MF>
+__device__ __forceinline__ float meta_lo(const uint32_t* w, int k) {
+    if (MF) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] >> 16));
+    return __uint_as_float(w[2 * k + 1]);
 }
 
 // Column offsets of group g within a 16-lane row (see the kernel): the
 // subgroup of lane XORs generated by 15, 7 and 3, in butterfly order.
 __constant__ int kColXor[8] = {0, 15, 7, 8, 3, 12, 4, 11};
 
-// value of lane (l ^ mask) of the same 16-lane row, through a DPP move
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+template <bool B>
+using bool_c = std::integral_constant<bool, B>;
+
+// v[x] = v[lane (l ^ m) of the 16-lane row] + v[x] for the 8 values, one
+// fused v_add_f32_dpp each (the compiler keeps DPP moves and adds apart). The
+// s_nop covers the two wait states a DPP read needs after a VALU write; the
+// later adds read registers written at least two instructions earlier.
+#define DKV_DPP_ADD8(CTRL, v)                                                                        \
+    asm volatile("s_nop 1\n\t"                                                                        \
+                 "v_add_f32_dpp %0, %0, %0 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %1, %1, %1 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %2, %2, %2 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %3, %3, %3 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %4, %4, %4 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %5, %5, %5 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %6, %6, %6 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                  \
+                 "v_add_f32_dpp %7, %7, %7 " CTRL " row_mask:0xf bank_mask:0xf"                        \
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), \
+                   "+v"(v[7]))
+
+// Max / sum over the 4 lane groups of a column (lanes l, l^16, l^32, l^48)
+// with the VALU lane swaps of gfx950 instead of LDS permutes: after the swap
+// of 32-lane halves and then of 16-lane rows, every lane holds the bitwise
+// same result.
+__device__ __forceinline__ float lanegroup_max(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float lanegroup_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// One wave's split: its (group, head) column, the Q operands, and the online
+// softmax state over the split's pages. Both MFMA kernels drive it; they
+// differ only in how a page reaches registers and where the logits go.
 template <int D, int CB, int MF>
-__global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
-                                                              const float* __restrict__ q, int Hq, float scale,
-                                                              int rps, int n_splits, float* __restrict__ part,
-                                                              float* __restrict__ logits) {
-    constexpr int NSTEP = D / 32;     // k-steps of the QK product
-    constexpr int NDT = D / 16;       // d-tiles of the PV product
-    constexpr int DL = D / 4;         // channels per lane group in QK
-    // the wave index through readfirstlane: the compiler then knows it (and
-    // the split, row range and page addresses) to be wave-uniform, keeps them
-    // in scalar registers and runs the page loop as a scalar loop
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
-    const int split = blockIdx.x * 4 + wave;
-    if (split >= n_splits) return;
-    const int h = blockIdx.y, s = blockIdx.z;
-    const int G = Hq / m.n_kv_heads;
-    const int group = cfg.group, NG = D / group, ncol = G * NG;
-    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int r_begin = split * rps;
-    if (r_begin >= n) return;
-    const int r_end = min(r_begin + rps, n);
-    const PageFmt f = page_fmt(cfg, D);
-    const int col = lane % 16, jj = lane / 16;
-    // column col = hcol ^ kColXor[gcol]: the NG columns of a head form an
-    // orbit of the lane involutions row_mirror (^15), row_half_mirror (^7) and
-    // quad reverse (^3), so their sum is a butterfly of DPP adds that leaves
-    // the bitwise-same total in every column of the head
-    int gcol = 0, hcol = 0;
-    bool cvalid = false;
-    for (int g = 0; g < NG; ++g) {
-        const int hh = col ^ kColXor[g];
-        if (hh < G) {
-            gcol = g;
-            hcol = hh;
-            cvalid = true;
-        }
-    }
-    (void)ncol;
-    const int hq = h * G + hcol;
-    const int gmeta = min(gcol, NG - 1);
+struct SplitCore {
+    static constexpr int NSTEP = D / 32;   // k-steps of the QK product
+    static constexpr int NDT = D / 16;     // d-tiles of the PV product
+    static constexpr int DL = D / 4;       // channels per lane group in QK
+    using Regs = PageRegs<D, CB, MF>;
 
-    // Q^T columns (group, head) in f16 hi + lo, and the column's q sum
+    int col, jj, group, NG, gcol, hcol, gmeta;
+    bool cvalid;
     f16x8_t qhi[NSTEP], qlo[NSTEP];
-    float qsum = 0.0f;
-    {
-        // the lane's DL channels as DL/4 vector loads, all in flight at once
-        // (hq is a valid head for every lane); the column's group mask is a
-        // bit mask, so the loads stay unconditional
+    float qsum_s, scale_s;
+    f32x4_t acc[NDT];
+    float m_run, l_run, zsum;
+
+    __device__ __forceinline__ void init(const float* __restrict__ q, int s, int h, int Hq, int G, int grp, int lane,
+                                         float scale) {
+        col = lane % 16;
+        jj = lane / 16;
+        group = grp;
+        NG = D / grp;
+        // column col = hcol ^ kColXor[gcol]: the NG columns of a head form an
+        // orbit of the lane involutions row_mirror (^15), row_half_mirror (^7)
+        // and quad reverse (^3), so their sum is a butterfly of DPP adds that
+        // leaves the bitwise-same total in every column of the head
+        gcol = 0;
+        hcol = 0;
+        cvalid = false;
+        for (int g = 0; g < NG; ++g) {
+            const int hh = col ^ kColXor[g];
+            if (hh < G) {
+                gcol = g;
+                hcol = hh;
+                cvalid = true;
+            }
+        }
+        gmeta = min(gcol, NG - 1);
+        // Q^T columns (group, head) in f16 hi + lo, and the column's q sum: the
+        // lane's DL channels as DL/4 vector loads, all in flight at once (hq is a
+        // valid head for every lane); the group mask is a bit mask, so the loads
+        // stay unconditional
+        const int hq = h * G + hcol;
         const float4* qr = reinterpret_cast<const float4*>(q + ((int64_t)s * Hq + hq) * D + DL * jj);
         float4 qv[DL / 4];
 #pragma unroll
         for (int x = 0; x < DL / 4; ++x) qv[x] = qr[x];
+        float qsum = 0.0f;
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st)
 #pragma unroll
@@ -351,80 +363,70 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
             }
         qsum += __shfl_xor(qsum, 16);
         qsum += __shfl_xor(qsum, 32);
+        // the QK product runs on code * 2^-24: fold the 2^24 into the zero
+        // term and the softmax scale (powers of two, exact)
+        qsum_s = qsum * kTwoM24;
+        scale_s = scale * kTwo24;
     }
-    f32x4_t acc[NDT];
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f, bsum = 0.0f, zsum = 0.0f;
 
-    const uint32_t magic = magic_f16x2();
-    const uint32_t use2 = NG >= 2 ? 0xFFFFFFFFu : 0u, use4 = NG >= 4 ? 0xFFFFFFFFu : 0u,
-                   use8 = NG >= 8 ? 0xFFFFFFFFu : 0u;
-    // Logit spill through a buffer resource over this sequence's logits: lanes
-    // with nothing to store get an offset past the end, which the hardware
-    // drops, so the store needs no branch (a branch would split the loop body
-    // and let the compiler sink the next page's loads to their use).
-    // Logits for note_attention are staged in this wave's LDS region
-    // [head][row - r_begin] (lanes with nothing to keep write a dummy slot),
-    // so the loop issues no memory stores; they go out after the split.
-    extern __shared__ float dyn_smem[];
-    float* slog = dyn_smem + wave * (G * rps + WAVE);
-    // one page of work on registers already loaded
-    auto step = [&](const PageRegs<D, CB, MF>& cur, const int p0) {
+    // fresh softmax state for the next split
+    __device__ __forceinline__ void reset() {
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        m_run = -INFINITY;
+        l_run = 0.0f;
+        zsum = 0.0f;
+    }
+
+    // One page on operands already in registers. TAIL pages hold rows at or
+    // past r_end (masked to exact zeros, their stale meta zeroed). sink(pv, p0)
+    // receives the page's scaled logits (rows 4jj+x, 16+4jj+x-4 of column col).
+    template <bool TAIL, class Sink>
+    __device__ __forceinline__ void page(const Regs& cur, int p0, int r_end, Sink&& sink) {
         // ---- QK over the page's two 16-row tiles, folded per (row, group)
+        // (the two tiles' MFMA chains interleaved, so each hides the other's latency)
         float sv[8];
+        f32x4_t sa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-            f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int st = 0; st < NSTEP; ++st) {
-                const f16x8_t kv = codes_to_f16_exact<CB>(cur.k[a] + st * (CB / 4), magic);
-                sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qhi[st], sa, 0, 0, 0);
-                sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qlo[st], sa, 0, 0, 0);
-            }
-            // columns outside every (group, head) pair have q = 0 and stay
-            // finite; rows past the live count are masked below
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const GroupMeta mt = pair_of<MF>(cur.km[a], r);
-                sv[4 * a + r] = fmaf(mt.scale, sa[r], mt.lo * qsum);
-            }
+        for (int st = 0; st < NSTEP; ++st) {
+            const f16x8_t kv0 = codes_to_f16<CB>(cur.k[0] + st * (CB / 4));
+            const f16x8_t kv1 = codes_to_f16<CB>(cur.k[1] + st * (CB / 4));
+            sa[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv0, qhi[st], sa[0], 0, 0, 0);
+            sa[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv1, qhi[st], sa[1], 0, 0, 0);
+            sa[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv0, qlo[st], sa[0], 0, 0, 0);
+            sa[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv1, qlo[st], sa[1], 0, 0, 0);
         }
-        // sum the group columns of each head (pairwise butterfly over the
-        // orbit); a step the group count does not use adds +0 (masked bits,
-        // no branch)
-        float sh[8];
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            float v = sv[x];
-            v += __uint_as_float(__float_as_uint(dpp_f32<0x140>(v)) & use2);   // row_mirror: col ^ 15
-            v += __uint_as_float(__float_as_uint(dpp_f32<0x141>(v)) & use4);   // row_half_mirror: col ^ 7
-            v += __uint_as_float(__float_as_uint(dpp_f32<0x1B>(v)) & use8);    // quad [3,2,1,0]: col ^ 3
-            sh[x] = v;
-        }
-        // mask, scale, optional spill, online softmax per column
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sv[4 * a + r] = fmaf(meta_scale<MF>(cur.km[a], r), sa[a][r],
+                                     fmaf(meta_lo<MF>(cur.km[a], r), qsum_s, 0.0f));
+        // sum the group columns of each head: a pairwise butterfly over the
+        // orbit, as many steps as the group count needs (uniform branches)
+        if (NG >= 2) DKV_DPP_ADD8("row_mirror", sv);            // col ^ 15
+        if (NG >= 4) DKV_DPP_ADD8("row_half_mirror", sv);       // col ^ 7
+        if (NG >= 8) DKV_DPP_ADD8("quad_perm:[3,2,1,0]", sv);   // col ^ 3
+        // scale, mask the tail, hand over, online softmax per column
         float pv[8];
         float mx = -INFINITY;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-            const int row = p0 + 16 * (x / 4) + 4 * jj + (x % 4);
-            const bool ok = row < r_end;
-            const float v = ok ? sh[x] * scale : -INFINITY;
-            slog[(ok && cvalid && gcol == 0) ? hcol * rps + (row - r_begin) : G * rps + lane] = v;
+            float v = sv[x] * scale_s;
+            if (TAIL) v = (p0 + 16 * (x / 4) + 4 * jj + (x % 4) < r_end) ? v : -INFINITY;
             pv[x] = v;
             mx = fmaxf(mx, v);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        sink(pv, p0);
+        mx = lanegroup_max(mx);
         // Lazy rescale: the reference max only moves when a column's max grows
-        // by more than 6 (so p <= e^6); o, l and the corrections share the
+        // by more than 6 (so p <= e^6); o, l and the zero term share the
         // reference, and the combine merges partials on any reference.
         const bool grow = mx > m_run + 6.0f;
         if (__any(grow)) {
             const float m_new = grow ? mx : m_run;
             const float alpha = (m_run == -INFINITY) ? 0.0f : __expf(m_run - m_new);
             l_run *= alpha;
-            bsum *= alpha;
             zsum *= alpha;
 #pragma unroll
             for (int t = 0; t < NDT; ++t) acc[t] *= alpha;
@@ -432,64 +434,150 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
         }
         // m_run is finite from the first page on (every split starts with a
         // live row), so masked rows give exp(-inf) = 0 with no test
-        float sum = 0.0f;
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            pv[x] = __expf(pv[x] - m_run);
-            sum += pv[x];
-        }
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        l_run += sum;
+        for (int x = 0; x < 8; ++x) pv[x] = __expf(pv[x] - m_run);
+        float sum = pv[0];
+#pragma unroll
+        for (int x = 1; x < 8; ++x) sum += pv[x];
+        l_run += lanegroup_sum(sum);
         // ---- PV: B[row (jj, e)][col] = f16(p * scaleV), rows e<4: 4jj+e, e>=4: 16+4jj+e-4
         f16x8_t bop;
-        float bs = 0.0f, zs = 0.0f;
+        float zs = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const GroupMeta mt = pair_of<MF>(cur.vm, e);
-            const int row = p0 + (e < 4 ? 4 * jj + e : 16 + 4 * jj + e - 4);
-            // rows past the live count may hold stale meta: zero it (p is 0 there)
-            const bool ok = row < r_end;
-            const float sc = ok ? mt.scale : 0.0f, lo = ok ? mt.lo : 0.0f;
-            _Float16 b = (_Float16)(pv[e] * sc);
-            // pin the rounded f16: the correction -1024 * sum(b) cancels the
-            // MFMA's 1024 offset only if it adds exactly the operand's bits
-            asm volatile("" : "+v"(b));
-            bop[e] = b;
-            bs += (float)b;
-            zs += pv[e] * lo;
+            float sc = meta_scale<MF>(cur.vm, e), lo = meta_lo<MF>(cur.vm, e);
+            if (TAIL) {
+                // rows past the live count may hold stale meta: zero it (p is 0 there)
+                const bool ok = p0 + (e < 4 ? 4 * jj + e : 16 + 4 * jj + e - 4) < r_end;
+                sc = ok ? sc : 0.0f;
+                lo = ok ? lo : 0.0f;
+            }
+            // one rounding of the exact product (v_fma_mix to f16); p, sc >= 0
+            bop[e] = (_Float16)fmaf(pv[e], sc, 0.0f);
+            zs = fmaf(pv[e], lo, zs);
         }
-        bsum += bs;
         zsum += zs;
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-            const f16x8_t av = codes_to_f16<CB>(cur.v + t * (CB / 4), magic);
+            const f16x8_t av = codes_to_f16<CB>(cur.v + t * (CB / 4));
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t], 0, 0, 0);
         }
+    }
+
+    // the split's partial: o = 2^24 * O' + zero term per d of the column's
+    // group, then (m, l)
+    __device__ __forceinline__ void finish(float* __restrict__ part, int s, int h, int Hq, int G, int n_splits,
+                                           int split) {
+        // total of the zero-point term over the 4 lane groups
+        zsum += __shfl_xor(zsum, 16);
+        zsum += __shfl_xor(zsum, 32);
+        if (!cvalid) return;
+        float* pp = part + (((int64_t)s * Hq + h * G + hcol) * n_splits + split) * (D + 2);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+            if ((16 * t) / group != gcol) continue;   // this column's group covers tile t
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pp[16 * t + 4 * jj + r] = acc[t][r] * kTwo24 + zsum;
+        }
+        if (gcol == 0 && jj == 0) {
+            pp[D] = m_run;
+            pp[D + 1] = l_run;
+        }
+    }
+};
+
+// byte offsets of a lane's operands inside a page (the same for every page)
+template <int D, int CB, int MF>
+__device__ __forceinline__ LaneOffsets lane_offsets(const PageFmt& f, int col, int jj, int gmeta) {
+    using Regs = PageRegs<D, CB, MF>;
+    LaneOffsets off;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        off.k[a] = (uint32_t)(f.kc + (16 * a + col) * (D * CB / 8) + Regs::WPL * 4 * jj);
+        off.km[a] = (uint32_t)k_meta_off(f, 16 * a + 4 * jj, gmeta);
+    }
+    off.v = (uint32_t)(f.vc + (col * 4 + jj) * Regs::NV * 4);
+    off.vm = (uint32_t)(f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB);
+    return off;
+}
+
+// ---- register-staged kernel (8-bit codes): pages loaded straight into
+// registers one page ahead; logits staged in LDS and written after the split
+template <int D, int CB, int MF>
+__global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
+                                                                 const float* __restrict__ q, int Hq, float scale,
+                                                                 int rps, int n_splits, float* __restrict__ part,
+                                                                 float* __restrict__ logits) {
+    using Core = SplitCore<D, CB, MF>;
+    using Regs = typename Core::Regs;
+    // the wave index through readfirstlane: the compiler then knows it (and
+    // the split, row range and page addresses) to be wave-uniform, keeps them
+    // in scalar registers and runs the page loop as a scalar loop
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int G = Hq / m.n_kv_heads;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    // the grid covers the splits of a few resident rounds; each wave walks
+    // splits blockIdx.x*4 + wave, + 4*gridDim.x, ... while they hold rows
+    if ((int)(blockIdx.x * 4 + wave) * rps >= n) return;
+    const PageFmt f = page_fmt(cfg, D);
+    Core c;
+    c.init(q, s, h, Hq, G, cfg.group, lane, scale);
+    const LaneOffsets off = lane_offsets<D, CB, MF>(f, c.col, c.jj, c.gmeta);
+    extern __shared__ float dyn_smem[];
+    float* slog = dyn_smem + wave * (G * rps + 8 * WAVE);
+    const bool writer = c.cvalid && c.gcol == 0;
+    const int slog_base = writer ? c.hcol * rps + 4 * c.jj : G * rps + 8 * lane;
+    const int slog_step = writer ? 1 : 0, slog_second = writer ? 16 : 4;
+    for (int split = blockIdx.x * 4 + wave; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
+    const int r_begin = split * rps;
+    const int r_end = min(r_begin + rps, n);
+    c.reset();
+
+    // Logits for note_attention are staged in this wave's LDS region
+    // [head][row - r_begin]; lanes that hold a head's logits (group column
+    // 0) write two 16-byte runs of rows per page, the others write a dummy
+    // slot of their own, so the loop issues no global stores and no branch.
+    auto stage = [&](const float (&pv)[8], int p0) {
+        float* dst = slog + slog_base + slog_step * (p0 - r_begin);
+        *reinterpret_cast<float4*>(dst) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        *reinterpret_cast<float4*>(dst + slog_second) = make_float4(pv[4], pv[5], pv[6], pv[7]);
     };
+
     const int np = (r_end - r_begin + PAGE - 1) / PAGE;
+    const int nfull = (r_end - r_begin) / PAGE;   // pages whose 32 rows are all live
     const int pg0 = r_begin / PAGE;
-    auto fetch = [&](PageRegs<D, CB, MF>& b, int k) {
+    auto fetch = [&](Regs& b, int k) {
         // past the last page, reload the last one (no branch around the loads)
-        load_page(b, page_ptr(m, s, layer, h, pg0 + min(k, np - 1)), f, col, jj, gmeta);
+        load_page(b, page_ptr(m, s, layer, h, pg0 + min(k, np - 1)), off);
     };
-    // page k+1 is in flight while page k is computed (two buffers, unrolled by 2)
-    // The scheduling barriers keep each fetch ahead of the page's products:
-    // left alone, the scheduler sinks the loads into the QK MFMAs, so the
-    // next page's latency hides behind half a page instead of a whole one.
-    PageRegs<D, CB, MF> b0, b1;
-    fetch(b0, 0);
-    for (int k = 0; k < np; k += 2) {
-        fetch(b1, k + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        step(b0, r_begin + k * PAGE);
-        if (k + 1 >= np) break;
-        fetch(b0, k + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        step(b1, r_begin + (k + 1) * PAGE);
+    // Full pages: page k+1 is in flight while page k is computed (two
+    // buffers, unrolled by 2). The scheduling barriers keep each fetch ahead
+    // of the page's products: left alone, the scheduler sinks the loads into
+    // the QK MFMAs, so the next page's latency hides behind half a page
+    // instead of a whole one.
+    Regs b0, b1;
+    if (nfull > 0) {
+        fetch(b0, 0);
+        for (int k = 0; k < nfull; k += 2) {
+            fetch(b1, k + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            c.template page<false>(b0, r_begin + k * PAGE, r_end, stage);
+            if (k + 1 >= nfull) break;
+            fetch(b0, k + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            c.template page<false>(b1, r_begin + (k + 1) * PAGE, r_end, stage);
+        }
+    }
+    // the split's last page when it is partly live (the mirror's tail):
+    // outside the loop, so the masking code adds no registers to it
+    if (nfull < np) {
+        fetch(b0, nfull);
+        c.template page<true>(b0, r_begin + nfull * PAGE, r_end, stage);
     }
     // staged logits of the split's rows, one coalesced pass per query head
     if (logits) {
+        // the wave reads back only its own LDS region, in program order
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int nr = r_end - r_begin;
         for (int i = lane; i < G * nr; i += WAVE) {
@@ -497,22 +585,175 @@ __global__ void __launch_bounds__(256) draft_attn_mfma_kernel(dkv_drafter_t m, i
             logits[((int64_t)s * Hq + h * G + g) * m.cap + r_begin + r] = slog[g * rps + r];
         }
     }
-    // totals of the per-column corrections over the 4 lane groups
-    bsum += __shfl_xor(bsum, 16);
-    bsum += __shfl_xor(bsum, 32);
-    zsum += __shfl_xor(zsum, 16);
-    zsum += __shfl_xor(zsum, 32);
-    if (!cvalid) return;
-    float* pp = part + (((int64_t)s * Hq + hq) * n_splits + split) * (D + 2);
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-        if ((16 * t) / group != gcol) continue;   // this column's group covers tile t
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pp[16 * t + 4 * jj + r] = acc[t][r] - 1024.0f * bsum + zsum;
+    c.finish(part, s, h, Hq, G, n_splits, split);
     }
-    if (gcol == 0 && jj == 0) {
-        pp[D] = m_run;
-        pp[D + 1] = l_run;
+}
+
+// ---- LDS-staged kernel (4-bit codes). Each wave streams its pages through a
+// ring of S page slots in LDS with direct-to-LDS loads (global_load_lds), S-1
+// pages ahead of the products, without holding them in registers. A slot is
+// LPP 1 KB loads, each 16 B per lane:
+//   2: K codes, linear (row r at r * D/2 bytes)
+//   D/64: V codes, gathered into lane order (load x: lane l's words 4x..4x+3)
+//   the rest: K meta then V meta, linear
+// The logits go straight from registers to the workspace (two 16-byte stores
+// per writer lane per page). The loads are issued from inline asm and waited
+// for by count (s_waitcnt vmcnt): the compiler's own tracking of LDS DMA would
+// wait for every load in flight before any LDS read. Stores count in vmcnt
+// too, so the count covers both.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from base + voff to LDS byte address lds + 16 * lane
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (the count is an immediate)
+__device__ __forceinline__ void vm_wait(int n) {
+    switch (n) {
+#define DKV_VMW(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        DKV_VMW(0) DKV_VMW(1) DKV_VMW(2) DKV_VMW(3) DKV_VMW(4) DKV_VMW(5) DKV_VMW(6) DKV_VMW(7)
+        DKV_VMW(8) DKV_VMW(9) DKV_VMW(10) DKV_VMW(11) DKV_VMW(12) DKV_VMW(13) DKV_VMW(14) DKV_VMW(15)
+        DKV_VMW(16) DKV_VMW(17) DKV_VMW(18) DKV_VMW(19) DKV_VMW(20) DKV_VMW(21) DKV_VMW(22) DKV_VMW(23)
+        DKV_VMW(24) DKV_VMW(25) DKV_VMW(26) DKV_VMW(27) DKV_VMW(28) DKV_VMW(29) DKV_VMW(30) DKV_VMW(31)
+#undef DKV_VMW
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;   // never more in flight
+    }
+}
+
+// 1 KB loads per page slot: 2 for K codes, D/64 for V codes, the rest for
+// the K and V meta (f16 pairs of up to 4 groups fit one load, 8 groups or f32
+// pairs need 2, f32 pairs of 8 groups 4)
+__host__ __device__ inline int dma_lpp(const PageFmt& f, int D) {
+    return 2 + D / 64 + (int)((2 * (f.vc - f.km) + 1023) / 1024);
+}
+// ring depth: 4 slots of 5 KB (80 KB per 4-wave block, 2 blocks per CU), 3 of larger
+__host__ __device__ constexpr int dma_stages(int lpp) { return lpp <= 5 ? 4 : 3; }
+
+template <int D, int MF, bool STORE, int LPP>
+__global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
+                                                                const float* __restrict__ q, int Hq, float scale,
+                                                                int rps, int n_splits, float* __restrict__ part,
+                                                                float* __restrict__ logits) {
+    constexpr int CB = 4;
+    using Core = SplitCore<D, CB, MF>;
+    using Regs = typename Core::Regs;
+    constexpr int NVL = D / 64;                 // V code loads per slot
+    constexpr int SPP = STORE ? 2 : 0;          // logit stores per page
+    constexpr int S = dma_stages(LPP);          // ring slots
+    constexpr int SLOT = LPP * 1024;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int G = Hq / m.n_kv_heads;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    // the grid covers the splits of a few resident rounds; each wave walks
+    // splits blockIdx.x*4 + wave, + 4*gridDim.x, ... while they hold rows
+    if ((int)(blockIdx.x * 4 + wave) * rps >= n) return;
+    const PageFmt f = page_fmt(cfg, D);
+    const uint32_t kmb = (uint32_t)(f.vc - f.km);   // K meta bytes (= V meta bytes)
+    Core c;
+    c.init(q, s, h, Hq, G, cfg.group, lane, scale);
+
+    // source offset of each 1 KB load (the same for every page)
+    uint32_t src[LPP];
+#pragma unroll
+    for (int i = 0; i < LPP; ++i) {
+        uint32_t o;
+        if (i < 2) {
+            o = (uint32_t)f.kc + i * 1024 + lane * 16;
+        } else if (i < 2 + NVL) {
+            o = (uint32_t)f.vc + (c.col * 4 + c.jj) * Regs::NV * 4 + (i - 2) * 16;
+        } else {
+            const uint32_t mo = (i - 2 - NVL) * 1024 + lane * 16;
+            o = mo < kmb ? (uint32_t)f.km + mo : (mo < 2 * kmb ? (uint32_t)f.vm + (mo - kmb) : (uint32_t)f.km);
+        }
+        src[i] = o;
+    }
+    // LDS offsets of the lane's operands inside a slot
+    constexpr uint32_t mbase = (2 + NVL) * 1024;
+    const uint32_t o_k = (c.col * 4 + c.jj) * 16;   // + a * 1024
+    const uint32_t o_v = 2 * 1024 + lane * 16;      // + x * 1024
+    const uint32_t o_km = mbase + (c.gmeta * PAGE + 4 * c.jj) * f.metaB;   // + 16 a * metaB
+    const uint32_t o_vm = mbase + kmb + (c.gmeta * PAGE + 8 * c.jj) * f.metaB;
+
+    extern __shared__ __align__(16) char dma_smem[];
+    char* ring = dma_smem + (size_t)wave * S * SLOT;
+    const bool writer = c.cvalid && c.gcol == 0;
+    for (int split = blockIdx.x * 4 + wave; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
+    const int r_begin = split * rps;
+    const int r_end = min(r_begin + rps, n);
+    c.reset();
+    const int np = (r_end - r_begin + PAGE - 1) / PAGE;
+    const int nfull = (r_end - r_begin) / PAGE;
+    const int pg0 = r_begin / PAGE;
+    // page j goes to slot j % S; the slot offsets advance by addition
+    int slot_in = 0, slot_out = 0;   // byte offsets of the next slot to fill / to read
+    auto issue = [&](int j) {
+        const uint8_t* pg = page_ptr(m, s, layer, h, pg0 + j);
+        const uint32_t dst = lds_addr(ring + slot_in);
+#pragma unroll
+        for (int i = 0; i < LPP; ++i) dma16(pg, src[i], dst + i * 1024);
+        slot_in = slot_in + SLOT == S * SLOT ? 0 : slot_in + SLOT;
+    };
+    auto operands = [&](Regs& r) {
+        const char* sl = ring + slot_out;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            load_words(r.k[a], reinterpret_cast<const uint8_t*>(sl + a * 1024 + o_k));
+            load_words(r.km[a], reinterpret_cast<const uint8_t*>(sl + o_km + 16 * a * f.metaB));
+        }
+#pragma unroll
+        for (int x = 0; x < NVL; ++x) {
+            const uint4 w = *reinterpret_cast<const uint4*>(sl + x * 1024 + o_v);
+            r.v[4 * x] = w.x;
+            r.v[4 * x + 1] = w.y;
+            r.v[4 * x + 2] = w.z;
+            r.v[4 * x + 3] = w.w;
+        }
+        load_words(r.vm, reinterpret_cast<const uint8_t*>(sl + o_vm));
+        slot_out = slot_out + SLOT == S * SLOT ? 0 : slot_out + SLOT;
+    };
+    // logits of a page straight to the workspace: lanes of group column 0
+    // hold rows 4jj..4jj+3 and 16+4jj..16+4jj+3 of head hcol
+    float* lrow = STORE ? logits + ((int64_t)s * Hq + h * G + c.hcol) * m.cap + 4 * c.jj : nullptr;
+    auto store = [&](const float (&pv)[8], int p0) {
+        if (STORE && writer) {
+            *reinterpret_cast<float4*>(lrow + p0) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            *reinterpret_cast<float4*>(lrow + p0 + 16) = make_float4(pv[4], pv[5], pv[6], pv[7]);
+        }
+    };
+    // In flight after page k's loads: the loads of the pages issued after it
+    // (at most S-2 ahead) and the stores of the pages computed since it was
+    // issued (at most S-1). The steady state is one immediate.
+    constexpr int N_STEADY = LPP * (S - 2) + SPP * (S - 1);
+    auto wait_page = [&](int k) {
+        const int ahead = min(S - 2, np - 1 - k), since = min(k, S - 1);
+        if (ahead == S - 2 && since == S - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_STEADY) : "memory");
+        else vm_wait(LPP * ahead + SPP * since);
+    };
+
+    for (int j = 0; j < S - 1; ++j)
+        if (j < np) issue(j);
+    Regs cur;
+    for (int k = 0; k < nfull; ++k) {
+        wait_page(k);
+        if (k + S - 1 < np) issue(k + S - 1);
+        operands(cur);
+        c.template page<false>(cur, r_begin + k * PAGE, r_end, store);
+    }
+    if (nfull < np) {
+        wait_page(nfull);
+        operands(cur);
+        c.template page<true>(cur, r_begin + nfull * PAGE, r_end, store);
+    }
+    c.finish(part, s, h, Hq, G, n_splits, split);
     }
 }
 
@@ -642,23 +883,62 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     hipStream_t st = as_stream(stream);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
-        const dim3 grid((ns + 3) / 4, m.n_kv_heads, m.batch);
-        const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
-        const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + WAVE);
+        // blocks of 4 splits, enough for about two resident rounds (8 waves per
+        // CU for the LDS-staged kernel, 12 for the register-staged one); each
+        // wave walks its further splits, so any row count up to cap is covered
+        const bool dma = cfg.bits <= 4 && m.head_dim == 128;
+        const int per_seg = std::max(1, (2 * 256 * (dma ? 8 : 12) / 4) / std::max(1, m.n_kv_heads * m.batch));
+        const dim3 grid(std::min((ns + 3) / 4, per_seg), m.n_kv_heads, m.batch);
+        if (dma) {
+            // 4-bit codes: pages streamed through an LDS ring, S-1 ahead; the
+            // kernel is instantiated per loads-per-page count, which fixes its
+            // slot size and ring depth (and so the LDS it is given)
+            const int LPP = dma_lpp(page_fmt(cfg, 128), 128);
+#define DKV_DMA(MM, ST, LP)                                                                                       \
+    do {                                                                                                          \
+        auto kfn = draft_attn_dma_kernel<128, MM, ST, LP>;                                                        \
+        const size_t lds = (size_t)4 * dma_stages(LP) * LP * 1024;                                                \
+        if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),                            \
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+            return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
+        hipLaunchKernelGGL(kfn, grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, scale, rps, ns, part,      \
+                           logits);                                                                               \
+    } while (0)
+#define DKV_DMA2(MM, LP)              \
+    do {                              \
+        if (logits) DKV_DMA(MM, true, LP); \
+        else DKV_DMA(MM, false, LP);  \
+    } while (0)
+            // (meta bytes per section: 32 rows x groups x 4 (f16 pair) or 8 (f32 pair))
+            const int key = (cfg.meta_f16 ? 100 : 0) + LPP;
+            switch (key) {
+                case 105: DKV_DMA2(1, 5); break;   // f16, up to 4 groups
+                case 106: DKV_DMA2(1, 6); break;   // f16, 8 groups
+                case 5: DKV_DMA2(0, 5); break;     // f32, up to 2 groups
+                case 6: DKV_DMA2(0, 6); break;     // f32, 4 groups
+                case 8: DKV_DMA2(0, 8); break;     // f32, 8 groups
+                default:
+                    return fail(DKV_EINVAL, "dkv_drafter_attention: no 4-bit kernel for " + std::to_string(LPP) +
+                                                " loads per page");
+            }
+#undef DKV_DMA2
+#undef DKV_DMA
+        } else {
+            const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
+            const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + 8 * WAVE);
 #define DKV_LAUNCH(DD, CC, MM)                                                                                      \
     hipLaunchKernelGGL((draft_attn_mfma_kernel<DD, CC, MM>), grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, \
                        scale, rps, ns, part, logits)
-        switch (key) {
-            case 0: DKV_LAUNCH(64, 4, 0); break;
-            case 1: DKV_LAUNCH(64, 4, 1); break;
-            case 2: DKV_LAUNCH(64, 8, 0); break;
-            case 3: DKV_LAUNCH(64, 8, 1); break;
-            case 4: DKV_LAUNCH(128, 4, 0); break;
-            case 5: DKV_LAUNCH(128, 4, 1); break;
-            case 6: DKV_LAUNCH(128, 8, 0); break;
-            default: DKV_LAUNCH(128, 8, 1); break;
-        }
+            switch (key) {
+                case 0: DKV_LAUNCH(64, 4, 0); break;
+                case 1: DKV_LAUNCH(64, 4, 1); break;
+                case 2: DKV_LAUNCH(64, 8, 0); break;
+                case 3: DKV_LAUNCH(64, 8, 1); break;
+                case 6: DKV_LAUNCH(128, 8, 0); break;
+                default: DKV_LAUNCH(128, 8, 1); break;
+            }
 #undef DKV_LAUNCH
+        }
     } else {
         hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
                            m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
