@@ -758,7 +758,9 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
 }
 
 // ---------------------------------------------------------------- combine + mass
-// merge splits per (seq, query head); also records the final (max, sum)
+// Merge splits per (seq, query head) and record the final (max, sum). The
+// global max comes first, so the weighted sums over the splits are
+// independent terms and their loads can all be in flight (8 at a time).
 __global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int layer, const float* __restrict__ part,
                                                             int Hq, int rps, int n_splits, float* __restrict__ out,
                                                             float* __restrict__ stats) {
@@ -767,17 +769,18 @@ __global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
     const int ns = min((n + rps - 1) / rps, n_splits);
     const float* p = part + ((int64_t)s * Hq + hq) * n_splits * (D + 2);
+    float mm = -INFINITY;
+#pragma unroll 8
+    for (int c = 0; c < ns; ++c) mm = fmaxf(mm, p[(int64_t)c * (D + 2) + D]);
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float mm = -INFINITY, l = 0.0f, o = 0.0f;
+        float l = 0.0f, o = 0.0f;
+#pragma unroll 8
         for (int c = 0; c < ns; ++c) {
             const float* pc = p + (int64_t)c * (D + 2);
-            const float mc = pc[D], lc = pc[D + 1];
-            const float mn = fmaxf(mm, mc);
-            const float a = (mm == -INFINITY) ? 0.0f : __expf(mm - mn);
-            const float b = (mc == -INFINITY) ? 0.0f : __expf(mc - mn);
-            l = l * a + lc * b;
-            o = o * a + pc[d] * b;
-            mm = mn;
+            const float mc = pc[D];
+            const float w = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
+            l = fmaf(pc[D + 1], w, l);
+            o = fmaf(pc[d], w, o);
         }
         out[((int64_t)s * Hq + hq) * D + d] = (l > 0.0f) ? o / l : 0.0f;
         if (d == 0 && stats) {
@@ -788,28 +791,41 @@ __global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int
 }
 
 // score[row] += sum over query heads of exp(logit - max) / sum. A thread
-// takes 4 consecutive rows (16-byte loads of each head's logits); the heads'
-// (max, sum) sit in LDS.
+// takes 4 consecutive rows (16-byte loads of each head's logits), 8 heads'
+// loads in flight at a time; the heads' (max, 1/sum) sit in LDS.
 constexpr int MASS_ROWS = 4;
+constexpr int MASS_HEADS = 8;
 __global__ void __launch_bounds__(256) draft_mass_kernel(dkv_drafter_t m, int layer, int Hq,
                                                          const float* __restrict__ logits,
                                                          const float* __restrict__ stats) {
-    extern __shared__ float st[];   // [Hq][2]
+    extern __shared__ float st[];   // [Hq][2]: max, 1 / sum
     const int s = blockIdx.y;
-    for (int i = threadIdx.x; i < 2 * Hq; i += blockDim.x) st[i] = stats[(int64_t)s * Hq * 2 + i];
+    for (int i = threadIdx.x; i < Hq; i += blockDim.x) {
+        const float l = stats[((int64_t)s * Hq + i) * 2 + 1];
+        st[2 * i] = stats[((int64_t)s * Hq + i) * 2];
+        st[2 * i + 1] = l > 0.0f ? 1.0f / l : 0.0f;
+    }
     __syncthreads();
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
     const int r0 = (blockIdx.x * blockDim.x + threadIdx.x) * MASS_ROWS;
     if (r0 >= n) return;
     float mass[MASS_ROWS] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float* lg = logits + (int64_t)s * Hq * m.cap + r0;
-    for (int hq = 0; hq < Hq; ++hq) {
-        const float mm = st[2 * hq], l = st[2 * hq + 1];
-        const float4 x = *reinterpret_cast<const float4*>(lg + (int64_t)hq * m.cap);
-        mass[0] += __expf(x.x - mm) / l;
-        mass[1] += __expf(x.y - mm) / l;
-        mass[2] += __expf(x.z - mm) / l;
-        mass[3] += __expf(x.w - mm) / l;
+    for (int h0 = 0; h0 < Hq; h0 += MASS_HEADS) {
+        float4 x[MASS_HEADS];
+#pragma unroll
+        for (int j = 0; j < MASS_HEADS; ++j)
+            x[j] = (h0 + j < Hq) ? *reinterpret_cast<const float4*>(lg + (int64_t)(h0 + j) * m.cap)
+                                 : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+#pragma unroll
+        for (int j = 0; j < MASS_HEADS; ++j) {
+            const int hq = min(h0 + j, Hq - 1);
+            const float mm = st[2 * hq], il = (h0 + j < Hq) ? st[2 * hq + 1] : 0.0f;
+            mass[0] = fmaf(__expf(x[j].x - mm), il, mass[0]);
+            mass[1] = fmaf(__expf(x[j].y - mm), il, mass[1]);
+            mass[2] = fmaf(__expf(x[j].z - mm), il, mass[2]);
+            mass[3] = fmaf(__expf(x[j].w - mm), il, mass[3]);
+        }
     }
     double* sc = m.score + row_index(m, s, layer) + r0;
 #pragma unroll
