@@ -498,13 +498,17 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_kernel(RebuildArgs a) {
 //   3. V code words (8 rows per word for 4-bit codes, 4 for bytes) are
 //      assembled from LDS and stored whole.
 constexpr int RB_MAXD = 128;
+// rows padded by 4 floats: the V staging stores walk rows at a fixed channel,
+// and a 512-byte row stride would put all 32 rows in one LDS bank (the pad
+// keeps rows 16-byte aligned for the vector reads of the quantize step)
+constexpr int RB_ROW = RB_MAXD + 4;
 struct RebuildSmem {
-    float x[2][PAGE][RB_MAXD];
+    float x[2][PAGE][RB_ROW];
     uint8_t vcode[PAGE][RB_MAXD];
 };
 
 __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a) {
-    const int page = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.y;
     const int s = blockIdx.z % a.m.batch, L = a.layers[blockIdx.z / a.m.batch];
     const dkv_drafter_t& m = a.m;
     const dkv_paged_t& f = a.full;
@@ -521,53 +525,87 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
         sink = min(cfg.sink, n);
     }
     kept = min(kept, m.cap);
-    if (page == 0 && h == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
-    const int r0 = page * PAGE;
-    if (r0 >= kept) return;
-    const int rows = min(PAGE, kept - r0);
+    if (blockIdx.x == 0 && h == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
     __shared__ RebuildSmem sm;
+    __shared__ int32_t sblk[PAGE], soff[PAGE];   // source block and slot of each row of the page
     const PageFmt pf = page_fmt(cfg, D);
-    uint8_t* pg = page_ptr(m, s, L, h, page);
     auto pos_of = [&](int r) { return r < sink ? r : n - (kept - sink) + (r - sink); };
-
-    // ---- 1. stage K (rows contiguous in the block) and V (rows contiguous per channel)
     const int64_t bel = paged_block_elems(f);
     const int64_t vb = (int64_t)f.n_kv_heads * f.block_size * D;
-    for (int u = threadIdx.x; u < PAGE * (D / 8); u += BLK) {
-        const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
-        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // the grid covers a few pages per segment; a block walks its segment's
+    // pages while they hold rows
+    for (int page = blockIdx.x; page * PAGE < kept; page += gridDim.x) {
+    const int r0 = page * PAGE;
+    const int rows = min(PAGE, kept - r0);
+    uint8_t* pg = page_ptr(m, s, L, h, page);
+    __syncthreads();   // the previous page is out of LDS
+    if (threadIdx.x < PAGE) {
+        const int i = threadIdx.x;
+        int32_t blk = 0, off = 0;
         if (i < rows) {
             const int p = pos_of(r0 + i);
-            const int32_t blk = paged_block(f, s, L, p);
-            const int64_t o = (int64_t)blk * bel + ((int64_t)h * f.block_size + p % f.block_size) * D + c8;
-            if (f.dtype == DKV_BF16) {
-                const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.pool) + o);
-                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            blk = paged_block(f, s, L, p);
+            off = p % f.block_size;
+        }
+        sblk[i] = blk;
+        soff[i] = off;
+    }
+    __syncthreads();
+
+    // ---- 1. stage K (rows contiguous in the block) and V (rows contiguous per
+    // channel); every load of a thread is issued before the LDS stores
+    {
+        constexpr int KU = PAGE * (RB_MAXD / 8) / BLK;   // K octets per thread
+        float kv[KU][8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[2 * e] = bf16_to_f32(ww[e] & 0xffffu);
-                    v[2 * e + 1] = bf16_to_f32(ww[e] >> 16);
+        for (int x = 0; x < KU; ++x) {
+            const int u = threadIdx.x + x * BLK;
+            const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kv[x][e] = 0.0f;
+            if (u < PAGE * (D / 8) && i < rows) {
+                const int64_t o = (int64_t)sblk[i] * bel + ((int64_t)h * f.block_size + soff[i]) * D + c8;
+                if (f.dtype == DKV_BF16) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.pool) + o);
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kv[x][2 * e] = bf16_to_f32(ww[e] & 0xffffu);
+                        kv[x][2 * e + 1] = bf16_to_f32(ww[e] >> 16);
+                    }
+                } else {
+                    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(f.pool) + o);
+                    const float4 x0 = src[0], x1 = src[1];
+                    kv[x][0] = x0.x; kv[x][1] = x0.y; kv[x][2] = x0.z; kv[x][3] = x0.w;
+                    kv[x][4] = x1.x; kv[x][5] = x1.y; kv[x][6] = x1.z; kv[x][7] = x1.w;
                 }
-            } else {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(f.pool) + o);
-                const float4 x0 = src[0], x1 = src[1];
-                v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-                v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+            }
+        }
+        constexpr int VU = PAGE * RB_MAXD / BLK;   // V elements per thread
+        float vv[VU];
+#pragma unroll
+        for (int x = 0; x < VU; ++x) {
+            const int u = threadIdx.x + x * BLK;
+            const int d = u / PAGE, i = u % PAGE;
+            vv[x] = 0.0f;
+            if (u < PAGE * D && i < rows)
+                vv[x] = load_elem(f.pool, (int64_t)sblk[i] * bel + vb + ((int64_t)h * D + d) * f.block_size + soff[i],
+                                  f.dtype);
+        }
+#pragma unroll
+        for (int x = 0; x < KU; ++x) {
+            const int u = threadIdx.x + x * BLK;
+            if (u < PAGE * (D / 8)) {
+                const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sm.x[0][i][c8 + e] = kv[x][e];
             }
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sm.x[0][i][c8 + e] = v[e];
-    }
-    for (int u = threadIdx.x; u < PAGE * D; u += BLK) {
-        const int d = u / PAGE, i = u % PAGE;
-        float v = 0.0f;
-        if (i < rows) {
-            const int p = pos_of(r0 + i);
-            const int32_t blk = paged_block(f, s, L, p);
-            const int64_t o = (int64_t)blk * bel + vb + ((int64_t)h * D + d) * f.block_size + p % f.block_size;
-            v = load_elem(f.pool, o, f.dtype);
+        for (int x = 0; x < VU; ++x) {
+            const int u = threadIdx.x + x * BLK;
+            if (u < PAGE * D) sm.x[1][u % PAGE][u / PAGE] = vv[x];
         }
-        sm.x[1][i][d] = v;
     }
     __syncthreads();
 
@@ -643,7 +681,7 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
             score[r0 + i] = 0.0;
         }
     }
-    if (pf.cb == 32) return;
+    if (pf.cb == 32) continue;
     __syncthreads();
 
     // ---- 3. V code words: word ((a*4 + j)*NDT + t) holds channel d = 16t + a of
@@ -666,6 +704,7 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
             w |= code << (pf.cb == 4 ? code_shift(4, e) : code_shift(8, q));
         }
         vsec[pf.cb == 4 ? base : base * 2 + half] = w;
+    }
     }
 }
 
@@ -839,8 +878,11 @@ extern "C" int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_
     a.budget = budget;
     if (mirror->head_dim <= RB_MAXD && mirror->head_dim % 8 == 0) {
         DKV_REQUIRE((int64_t)mirror->batch * n_changed <= 65535, "dkv_drafter_rebuild: batch x layers too large");
-        hipLaunchKernelGGL(drafter_rebuild_page_kernel, dim3(mirror->cap / PAGE, mirror->n_kv_heads,
-                                                              mirror->batch * n_changed),
+        // a few blocks per (sequence, layer, head) segment, about 4096 in all;
+        // each walks its segment's pages while they hold rows
+        const int segs = mirror->n_kv_heads * mirror->batch * n_changed;
+        const int per_seg = std::min(mirror->cap / PAGE, std::max(1, (4096 + segs - 1) / segs));
+        hipLaunchKernelGGL(drafter_rebuild_page_kernel, dim3(per_seg, mirror->n_kv_heads, mirror->batch * n_changed),
                            dim3(BLK), 0, as_stream(stream), a);
     } else {
         hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(mirror->cap / PAGE, mirror->batch, n_changed), dim3(BLK), 0,
