@@ -653,55 +653,63 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     const int h = blockIdx.y, s = blockIdx.z;
     const int G = Hq / m.n_kv_heads;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    // the grid covers the splits of a few resident rounds; each wave walks
-    // splits blockIdx.x*4 + wave, + 4*gridDim.x, ... while they hold rows
-    if ((int)(blockIdx.x * 4 + wave) * rps >= n) return;
+    // This wave's splits are split0, split0 + stride, ... while they hold rows;
+    // their pages form one stream g = 0..T-1 (split j = g / PPS, page g % PPS),
+    // so the ring stays full across split boundaries. Only the segment's last
+    // split can be partial, and it is the wave's last.
+    const int PPS = rps / PAGE;
+    const int split0 = blockIdx.x * 4 + wave, stride = 4 * gridDim.x;
+    const int nsplit = min((n + rps - 1) / rps, n_splits);
+    if (split0 >= nsplit) return;
+    const int J = (nsplit - 1 - split0) / stride + 1;
+    const int last_rows = n - (split0 + (J - 1) * stride) * rps;   // rows of the wave's last split
+    const int T = (J - 1) * PPS + (min(last_rows, rps) + PAGE - 1) / PAGE;
+    const bool tail = last_rows < rps && last_rows % PAGE != 0;   // the stream's last page is partial
     const PageFmt f = page_fmt(cfg, D);
     const uint32_t kmb = (uint32_t)(f.vc - f.km);   // K meta bytes (= V meta bytes)
+
+    extern __shared__ __align__(16) char dma_smem[];
+    char* ring = dma_smem + (size_t)wave * S * SLOT;
+    int slot_in = 0, slot_out = 0;   // byte offsets of the next slot to fill / to read
+    auto page_of = [&](int g) { return (split0 + (g / PPS) * stride) * PPS + g % PPS; };
+    // source offset of each 1 KB load (the same for every page); the V code
+    // loads gather into lane order and need the lane's column
+    const int col = lane % 16, jj = lane / 16;
+    uint32_t src[LPP];
+    {
+#pragma unroll
+        for (int i = 0; i < LPP; ++i) {
+            uint32_t o;
+            if (i < 2) {
+                o = (uint32_t)f.kc + i * 1024 + lane * 16;
+            } else if (i < 2 + NVL) {
+                o = (uint32_t)f.vc + (col * 4 + jj) * Regs::NV * 4 + (i - 2) * 16;
+            } else {
+                const uint32_t mo = (i - 2 - NVL) * 1024 + lane * 16;
+                o = mo < kmb ? (uint32_t)f.km + mo : (mo < 2 * kmb ? (uint32_t)f.vm + (mo - kmb) : (uint32_t)f.km);
+            }
+            src[i] = o;
+        }
+    }
+    auto issue = [&](int g) {
+        const uint8_t* pg = page_ptr(m, s, layer, h, page_of(g));
+        const uint32_t dst = lds_addr(ring + slot_in);
+#pragma unroll
+        for (int i = 0; i < LPP; ++i) dma16(pg, src[i], dst + i * 1024);
+        slot_in = slot_in + SLOT == S * SLOT ? 0 : slot_in + SLOT;
+    };
+    // the first pages go out before the query loads, so their latency overlaps
+    for (int j = 0; j < S - 1; ++j)
+        if (j < T) issue(j);
+
     Core c;
     c.init(q, s, h, Hq, G, cfg.group, lane, scale);
-
-    // source offset of each 1 KB load (the same for every page)
-    uint32_t src[LPP];
-#pragma unroll
-    for (int i = 0; i < LPP; ++i) {
-        uint32_t o;
-        if (i < 2) {
-            o = (uint32_t)f.kc + i * 1024 + lane * 16;
-        } else if (i < 2 + NVL) {
-            o = (uint32_t)f.vc + (c.col * 4 + c.jj) * Regs::NV * 4 + (i - 2) * 16;
-        } else {
-            const uint32_t mo = (i - 2 - NVL) * 1024 + lane * 16;
-            o = mo < kmb ? (uint32_t)f.km + mo : (mo < 2 * kmb ? (uint32_t)f.vm + (mo - kmb) : (uint32_t)f.km);
-        }
-        src[i] = o;
-    }
     // LDS offsets of the lane's operands inside a slot
     constexpr uint32_t mbase = (2 + NVL) * 1024;
     const uint32_t o_k = (c.col * 4 + c.jj) * 16;   // + a * 1024
     const uint32_t o_v = 2 * 1024 + lane * 16;      // + x * 1024
     const uint32_t o_km = mbase + (c.gmeta * PAGE + 4 * c.jj) * f.metaB;   // + 16 a * metaB
     const uint32_t o_vm = mbase + kmb + (c.gmeta * PAGE + 8 * c.jj) * f.metaB;
-
-    extern __shared__ __align__(16) char dma_smem[];
-    char* ring = dma_smem + (size_t)wave * S * SLOT;
-    const bool writer = c.cvalid && c.gcol == 0;
-    for (int split = blockIdx.x * 4 + wave; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
-    const int r_begin = split * rps;
-    const int r_end = min(r_begin + rps, n);
-    c.reset();
-    const int np = (r_end - r_begin + PAGE - 1) / PAGE;
-    const int nfull = (r_end - r_begin) / PAGE;
-    const int pg0 = r_begin / PAGE;
-    // page j goes to slot j % S; the slot offsets advance by addition
-    int slot_in = 0, slot_out = 0;   // byte offsets of the next slot to fill / to read
-    auto issue = [&](int j) {
-        const uint8_t* pg = page_ptr(m, s, layer, h, pg0 + j);
-        const uint32_t dst = lds_addr(ring + slot_in);
-#pragma unroll
-        for (int i = 0; i < LPP; ++i) dma16(pg, src[i], dst + i * 1024);
-        slot_in = slot_in + SLOT == S * SLOT ? 0 : slot_in + SLOT;
-    };
     auto operands = [&](Regs& r) {
         const char* sl = ring + slot_out;
 #pragma unroll
@@ -722,6 +730,7 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     };
     // logits of a page straight to the workspace: lanes of group column 0
     // hold rows 4jj..4jj+3 and 16+4jj..16+4jj+3 of head hcol
+    const bool writer = c.cvalid && c.gcol == 0;
     float* lrow = STORE ? logits + ((int64_t)s * Hq + h * G + c.hcol) * m.cap + 4 * c.jj : nullptr;
     auto store = [&](const float (&pv)[8], int p0) {
         if (STORE && writer) {
@@ -729,31 +738,35 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
             *reinterpret_cast<float4*>(lrow + p0 + 16) = make_float4(pv[4], pv[5], pv[6], pv[7]);
         }
     };
-    // In flight after page k's loads: the loads of the pages issued after it
-    // (at most S-2 ahead) and the stores of the pages computed since it was
-    // issued (at most S-1). The steady state is one immediate.
+    // In flight after page g's loads: the loads of the pages issued after it
+    // (at most S-2 ahead) and the logit stores of the pages computed since it
+    // was issued (at most S-1). The partial stores at split ends are not
+    // counted, which only makes a wait stricter. The steady state is one immediate.
     constexpr int N_STEADY = LPP * (S - 2) + SPP * (S - 1);
-    auto wait_page = [&](int k) {
-        const int ahead = min(S - 2, np - 1 - k), since = min(k, S - 1);
+    auto wait_page = [&](int g) {
+        const int ahead = min(S - 2, T - 1 - g), since = min(g, S - 1);
         if (ahead == S - 2 && since == S - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_STEADY) : "memory");
         else vm_wait(LPP * ahead + SPP * since);
     };
 
-    for (int j = 0; j < S - 1; ++j)
-        if (j < np) issue(j);
     Regs cur;
-    for (int k = 0; k < nfull; ++k) {
-        wait_page(k);
-        if (k + S - 1 < np) issue(k + S - 1);
+    const int gfull = tail ? T - 1 : T;   // pages computed in the loop (all rows live)
+    for (int g = 0; g < gfull; ++g) {
+        wait_page(g);
+        if (g + S - 1 < T) issue(g + S - 1);
+        const int j = g / PPS, k = g % PPS, split = split0 + j * stride;
+        if (k == 0) c.reset();
         operands(cur);
-        c.template page<false>(cur, r_begin + k * PAGE, r_end, store);
+        c.template page<false>(cur, split * rps + k * PAGE, n, store);
+        if (k == PPS - 1 || g == T - 1) c.finish(part, s, h, Hq, G, n_splits, split);
     }
-    if (nfull < np) {
-        wait_page(nfull);
+    if (tail) {
+        const int g = T - 1, j = g / PPS, k = g % PPS, split = split0 + j * stride;
+        wait_page(g);
+        if (k == 0) c.reset();
         operands(cur);
-        c.template page<true>(cur, r_begin + nfull * PAGE, r_end, store);
-    }
-    c.finish(part, s, h, Hq, G, n_splits, split);
+        c.template page<true>(cur, split * rps + k * PAGE, n, store);
+        c.finish(part, s, h, Hq, G, n_splits, split);
     }
 }
 
@@ -903,7 +916,10 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         // CU for the LDS-staged kernel, 12 for the register-staged one); each
         // wave walks its further splits, so any row count up to cap is covered
         const bool dma = cfg.bits <= 4 && m.head_dim == 128;
-        const int per_seg = std::max(1, (2 * 256 * (dma ? 8 : 12) / 4) / std::max(1, m.n_kv_heads * m.batch));
+        // the LDS-staged kernel runs one resident round (8 waves per CU), its
+        // waves streaming pages across their splits; the register-staged one
+        // about two rounds (12 waves per CU)
+        const int per_seg = std::max(1, ((dma ? 1 : 2) * 256 * (dma ? 8 : 12) / 4) / std::max(1, m.n_kv_heads * m.batch));
         const dim3 grid(std::min((ns + 3) / 4, per_seg), m.n_kv_heads, m.batch);
         if (dma) {
             // 4-bit codes: pages streamed through an LDS ring, S-1 ahead; the
