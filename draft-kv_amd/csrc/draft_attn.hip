@@ -529,10 +529,13 @@ __global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m
     const bool writer = c.cvalid && c.gcol == 0;
     const int slog_base = writer ? c.hcol * rps + 4 * c.jj : G * rps + 8 * lane;
     const int slog_step = writer ? 1 : 0, slog_second = writer ? 16 : 4;
-    for (int split = blockIdx.x * 4 + wave; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
+    // one softmax state across all of the wave's splits: the wave writes a
+    // single partial, in slot blockIdx.x*4 + wave
+    c.reset();
+    const int part_slot = blockIdx.x * 4 + wave;
+    for (int split = part_slot; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
     const int r_begin = split * rps;
     const int r_end = min(r_begin + rps, n);
-    c.reset();
 
     // Logits for note_attention are staged in this wave's LDS region
     // [head][row - r_begin]; lanes that hold a head's logits (group column
@@ -585,8 +588,8 @@ __global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m
             logits[((int64_t)s * Hq + h * G + g) * m.cap + r_begin + r] = slog[g * rps + r];
         }
     }
-    c.finish(part, s, h, Hq, G, n_splits, split);
     }
+    c.finish(part, s, h, Hq, G, n_splits, part_slot);
 }
 
 // ---- LDS-staged kernel (4-bit codes). Each wave streams its pages through a
@@ -702,8 +705,11 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     for (int j = 0; j < S - 1; ++j)
         if (j < T) issue(j);
 
+    // one softmax state across the wave's whole stream: a single partial, in
+    // slot split0
     Core c;
     c.init(q, s, h, Hq, G, cfg.group, lane, scale);
+    c.reset();
     // LDS offsets of the lane's operands inside a slot
     constexpr uint32_t mbase = (2 + NVL) * 1024;
     const uint32_t o_k = (c.col * 4 + c.jj) * 16;   // + a * 1024
@@ -740,8 +746,7 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     };
     // In flight after page g's loads: the loads of the pages issued after it
     // (at most S-2 ahead) and the logit stores of the pages computed since it
-    // was issued (at most S-1). The partial stores at split ends are not
-    // counted, which only makes a wait stricter. The steady state is one immediate.
+    // was issued (at most S-1). The steady state is one immediate.
     constexpr int N_STEADY = LPP * (S - 2) + SPP * (S - 1);
     auto wait_page = [&](int g) {
         const int ahead = min(S - 2, T - 1 - g), since = min(g, S - 1);
@@ -755,50 +760,73 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
         wait_page(g);
         if (g + S - 1 < T) issue(g + S - 1);
         const int j = g / PPS, k = g % PPS, split = split0 + j * stride;
-        if (k == 0) c.reset();
         operands(cur);
         c.template page<false>(cur, split * rps + k * PAGE, n, store);
-        if (k == PPS - 1 || g == T - 1) c.finish(part, s, h, Hq, G, n_splits, split);
     }
     if (tail) {
         const int g = T - 1, j = g / PPS, k = g % PPS, split = split0 + j * stride;
         wait_page(g);
-        if (k == 0) c.reset();
         operands(cur);
         c.template page<true>(cur, split * rps + k * PAGE, n, store);
-        c.finish(part, s, h, Hq, G, n_splits, split);
     }
+    c.finish(part, s, h, Hq, G, n_splits, split0);
 }
 
 // ---------------------------------------------------------------- combine + mass
-// Merge splits per (seq, query head) and record the final (max, sum). The
-// global max comes first, so the weighted sums over the splits are
-// independent terms and their loads can all be in flight (8 at a time).
-__global__ void __launch_bounds__(128) draft_combine_kernel(dkv_drafter_t m, int layer, const float* __restrict__ part,
-                                                            int Hq, int rps, int n_splits, float* __restrict__ out,
-                                                            float* __restrict__ stats) {
+// Merge the partials of (seq, query head) and record the final (max, sum).
+// Partial slots [0, min(live splits, n_parts)) hold data. The global max
+// comes first, so the weighted sums over the partials are independent terms:
+// wave w of the block takes partials w, w + nw, ... (lane: channels lane and
+// lane + 64), 8 of them in flight, and the waves' sums meet in LDS in a
+// fixed order.
+constexpr int COMB_WAVES = 16;
+__global__ void __launch_bounds__(64 * COMB_WAVES) draft_combine_kernel(dkv_drafter_t m, int layer,
+                                                                        const float* __restrict__ part, int Hq,
+                                                                        int rps, int n_splits, int n_parts,
+                                                                        float* __restrict__ out,
+                                                                        float* __restrict__ stats) {
     const int hq = blockIdx.x, s = blockIdx.y;
-    const int D = m.head_dim;
+    const int D = m.head_dim, PD = D + 2;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int ns = min((n + rps - 1) / rps, n_splits);
-    const float* p = part + ((int64_t)s * Hq + hq) * n_splits * (D + 2);
+    const int ns = min(min((n + rps - 1) / rps, n_splits), n_parts);
+    const float* p = part + ((int64_t)s * Hq + hq) * n_splits * PD;
+    const int nw = blockDim.x / WAVE, w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    __shared__ float smax[COMB_WAVES], sl[COMB_WAVES];
+    __shared__ float so[COMB_WAVES][2 * WAVE];
     float mm = -INFINITY;
+    for (int c = threadIdx.x; c < ns; c += blockDim.x) mm = fmaxf(mm, p[(int64_t)c * PD + D]);
+    for (int o = WAVE / 2; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+    if (lane == 0) smax[w] = mm;
+    __syncthreads();
+    mm = smax[0];
+    for (int i = 1; i < nw; ++i) mm = fmaxf(mm, smax[i]);
+    const bool a0 = lane < D, a1 = lane + WAVE < D;
+    float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll 8
-    for (int c = 0; c < ns; ++c) mm = fmaxf(mm, p[(int64_t)c * (D + 2) + D]);
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float l = 0.0f, o = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < ns; ++c) {
-            const float* pc = p + (int64_t)c * (D + 2);
-            const float mc = pc[D];
-            const float w = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
-            l = fmaf(pc[D + 1], w, l);
-            o = fmaf(pc[d], w, o);
+    for (int c = w; c < ns; c += nw) {
+        const float* pc = p + (int64_t)c * PD;
+        const float mc = pc[D], lc = pc[D + 1];
+        const float x0 = a0 ? pc[lane] : 0.0f, x1 = a1 ? pc[lane + WAVE] : 0.0f;
+        const float wt = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
+        l = fmaf(lc, wt, l);
+        o0 = fmaf(x0, wt, o0);
+        o1 = fmaf(x1, wt, o1);
+    }
+    so[w][lane] = o0;
+    so[w][lane + WAVE] = o1;
+    if (lane == 0) sl[w] = l;
+    __syncthreads();
+    if (threadIdx.x < D) {
+        const int d = threadIdx.x;
+        float lt = 0.0f, ot = 0.0f;
+        for (int i = 0; i < nw; ++i) {
+            lt += sl[i];
+            ot += so[i][d];
         }
-        out[((int64_t)s * Hq + hq) * D + d] = (l > 0.0f) ? o / l : 0.0f;
+        out[((int64_t)s * Hq + hq) * D + d] = (lt > 0.0f) ? ot / lt : 0.0f;
         if (d == 0 && stats) {
             stats[((int64_t)s * Hq + hq) * 2] = mm;
-            stats[((int64_t)s * Hq + hq) * 2 + 1] = l;
+            stats[((int64_t)s * Hq + hq) * 2 + 1] = lt;
         }
     }
 }
@@ -910,17 +938,17 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     float* logits = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.logits_off) : nullptr;
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
+    int n_parts = ns;   // partial slots written (one per split in the generic kernel)
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
-        // blocks of 4 splits, enough for about two resident rounds (8 waves per
-        // CU for the LDS-staged kernel, 12 for the register-staged one); each
-        // wave walks its further splits, so any row count up to cap is covered
+        // blocks of 4 waves; each wave walks splits blockIdx.x*4 + wave, +
+        // 4*gridDim.x, ..., so any row count up to cap is covered. The
+        // LDS-staged kernel runs one resident round (8 waves per CU), the
+        // register-staged one about two rounds (12 waves per CU).
         const bool dma = cfg.bits <= 4 && m.head_dim == 128;
-        // the LDS-staged kernel runs one resident round (8 waves per CU), its
-        // waves streaming pages across their splits; the register-staged one
-        // about two rounds (12 waves per CU)
         const int per_seg = std::max(1, ((dma ? 1 : 2) * 256 * (dma ? 8 : 12) / 4) / std::max(1, m.n_kv_heads * m.batch));
         const dim3 grid(std::min((ns + 3) / 4, per_seg), m.n_kv_heads, m.batch);
+        n_parts = 4 * (int)grid.x;   // one partial per wave
         if (dma) {
             // 4-bit codes: pages streamed through an LDS ring, S-1 ahead; the
             // kernel is instantiated per loads-per-page count, which fixes its
@@ -977,8 +1005,10 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     }
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
-    hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(128), 0, st, m, layer, part, n_q_heads,
-                       rps, ns, out, stats);
+    // one wave of the combine per 8 partials, up to 16 waves
+    const int comb_waves = std::min(COMB_WAVES, std::max(1, (std::min(n_parts, ns) + 7) / 8));
+    hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(WAVE * comb_waves), 0, st, m, layer,
+                       part, n_q_heads, rps, ns, n_parts, out, stats);
     if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
     if (want_mass) {
         const int per_block = 256 * MASS_ROWS;

@@ -126,6 +126,12 @@ __device__ __forceinline__ void quant_row(LoadK ldk, LoadV ldv, const PageFmt& f
 }
 
 // ------------------------------------------------------------ block helpers
+// The append/truncate/evict op runs one block of OP_BLK threads per
+// (sequence, layer); these helpers and the compaction below assume it.
+constexpr int OP_BLK = 1024;
+constexpr int OP_WAVES = OP_BLK / WAVE;
+constexpr int DEADLIST = 1024;   // dead rows a list compaction takes (more: the general one)
+
 __device__ int block_sum_int(int v, int* red) {
     v = wave_sum_i(v);
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -133,7 +139,7 @@ __device__ int block_sum_int(int v, int* red) {
     if (lane == 0) red[w] = v;
     __syncthreads();
     int t = 0;
-    for (int i = 0; i < NWAVES; ++i) t += red[i];
+    for (int i = 0; i < OP_WAVES; ++i) t += red[i];
     return t;
 }
 
@@ -148,7 +154,7 @@ __device__ int block_rank(int flag, int* red, int* total) {
     if (lane == 0) red[w] = wcount;
     __syncthreads();
     int off = 0, tot = 0;
-    for (int i = 0; i < NWAVES; ++i) {
+    for (int i = 0; i < OP_WAVES; ++i) {
         if (i < w) off += red[i];
         tot += red[i];
     }
@@ -214,13 +220,13 @@ __device__ void copy_row_head(const RowCtx& c, int h, int from, int to, int lane
 // [0, new_n). Returns new_n. Whole block participates.
 __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes, int* movers) {
     int keep = 0;
-    for (int r = threadIdx.x; r < n; r += BLK) keep += (c.pos[r] < thr);
+    for (int r = threadIdx.x; r < n; r += OP_BLK) keep += (c.pos[r] < thr);
     const int new_n = block_sum_int(keep, red);
     if (new_n == n) return n;
     for (int base = 0;; base += MAXMOVE) {
         int seen_h = 0, seen_m = 0;
         __syncthreads();
-        for (int r0 = 0; r0 < new_n; r0 += BLK) {
+        for (int r0 = 0; r0 < new_n; r0 += OP_BLK) {
             const int r = r0 + threadIdx.x;
             const int fl = (r < new_n) && (c.pos[r] >= thr);
             int tot;
@@ -228,7 +234,7 @@ __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes
             if (fl && rk >= base && rk < base + MAXMOVE) holes[rk - base] = r;
             seen_h += tot;
         }
-        for (int r0 = new_n; r0 < n; r0 += BLK) {
+        for (int r0 = new_n; r0 < n; r0 += OP_BLK) {
             const int r = r0 + threadIdx.x;
             const int fl = (r < n) && (c.pos[r] < thr);
             int tot;
@@ -241,7 +247,7 @@ __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes
         if (np <= 0) break;
         // sources (>= new_n) and destinations (< new_n) are disjoint; one wave
         // per head walks the pairs in order
-        for (int h = threadIdx.x / WAVE; h < c.m->n_kv_heads; h += NWAVES)
+        for (int h = threadIdx.x / WAVE; h < c.m->n_kv_heads; h += OP_WAVES)
             for (int p = 0; p < np; ++p) copy_row_head(c, h, movers[p], holes[p], threadIdx.x % WAVE);
         __syncthreads();
         if (seen_h - base <= MAXMOVE) break;
@@ -249,88 +255,233 @@ __device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes
     return new_n;
 }
 
+// LDS working set of the op (one block per (sequence, layer)).
+struct OpShared {
+    int red[OP_WAVES];
+    double redd[OP_WAVES];
+    int32_t rpos[OP_WAVES];
+    int rslot[OP_WAVES];
+    int list[DEADLIST];      // dead slots (truncated rows, then victims), any order
+    int sorted[DEADLIST];    // the dead slots ascending / the general compaction's holes
+    int movers[DEADLIST];
+    unsigned bits_lo[WIN / 32], bits_hi[WIN / 32];
+    int count;
+    int32_t bounds[2];
+};
+static_assert(DEADLIST <= OP_BLK && DEADLIST <= MAXMOVE, "a list compaction ranks one slot per thread");
+
+// Compaction when the k dead slots (distinct, below n) are known, in any
+// order in list[0..k). Same result as compact(): the holes are the dead
+// slots below n - k in slot order, the movers the live slots of [n - k, n)
+// in slot order, paired by rank; no pass over the other rows.
+__device__ int compact_list(const RowCtx& c, int n, int k, OpShared& sh) {
+    if (k == 0) return n;
+    const int new_n = n - k;
+    for (int i = threadIdx.x; i < k; i += OP_BLK) {
+        const int v = sh.list[i];
+        int rk = 0;
+        for (int j = 0; j < k; ++j) rk += (sh.list[j] < v);
+        sh.sorted[rk] = v;
+    }
+    __syncthreads();
+    // slot new_n + t of the tail, live unless it is among the dead
+    const int t = threadIdx.x, r = new_n + t;
+    int live = 0;
+    if (t < k) {
+        int lo = 0, hi = k;
+        while (lo < hi) {
+            const int mid = (lo + hi) / 2;
+            if (sh.sorted[mid] < r) lo = mid + 1; else hi = mid;
+        }
+        live = !(lo < k && sh.sorted[lo] == r);
+    }
+    int np;
+    const int rk = block_rank(live, sh.red, &np);   // np = dead slots below new_n
+    if (live) sh.movers[rk] = r;
+    __syncthreads();
+    for (int h = threadIdx.x / WAVE; h < c.m->n_kv_heads; h += OP_WAVES)
+        for (int p = 0; p < np; ++p) copy_row_head(c, h, sh.movers[p], sh.sorted[p], threadIdx.x % WAVE);
+    __syncthreads();
+    return new_n;
+}
+
+// One pass over the positions of rows [0, n), 16 rows per thread per step
+// (four 16-byte loads in flight): rows at or past p0 (when trunc) go to the
+// dead list (counted past DEADLIST, not listed); when bits, the other rows'
+// positions below WIN and within WIN under maxpos set the window bitmaps.
+// Returns the dead count.
+__device__ int scan_rows(const RowCtx& c, int n, bool trunc, int32_t p0, bool bits, int32_t maxpos, OpShared& sh) {
+    if (bits)
+        for (int i = threadIdx.x; i < WIN / 32; i += OP_BLK) {
+            sh.bits_lo[i] = 0u;
+            sh.bits_hi[i] = 0u;
+        }
+    if (threadIdx.x == 0) sh.count = 0;
+    __syncthreads();
+    for (int base = 0; base < n; base += 16 * OP_BLK) {
+        int4 pv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK);
+            pv[j] = r < n ? *reinterpret_cast<const int4*>(c.pos + r) : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int32_t pe[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK) + e;
+                if (r >= n) continue;
+                const int32_t p = pe[e];
+                if (trunc && p >= p0) {
+                    const int i = atomicAdd(&sh.count, 1);
+                    if (i < DEADLIST) sh.list[i] = r;
+                } else if (bits) {
+                    if (p < WIN) atomicOr(&sh.bits_lo[p / 32], 1u << (p % 32));
+                    const int32_t dtop = maxpos - p;
+                    if (dtop >= 0 && dtop < WIN) atomicOr(&sh.bits_hi[dtop / 32], 1u << (dtop % 32));
+                }
+            }
+        }
+    }
+    __syncthreads();
+    return sh.count;
+}
+
+// The lowest (score, position) row with sink_max < pos < recent_min, marked
+// DEAD and put in the dead list at index k; every thread gets its slot (-1
+// when no row qualifies). 16 rows per thread per step.
+__device__ int select_victim(const RowCtx& c, int n, int32_t sink_max, int32_t recent_min, int k, OpShared& sh) {
+    double best = INFINITY;
+    int32_t bpos = INT_MAX;
+    int bslot = -1;
+    for (int base = 0; base < n; base += 16 * OP_BLK) {
+        int4 pv[4];
+        double2 sa[4], sb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK);
+            if (r < n) {
+                pv[j] = *reinterpret_cast<const int4*>(c.pos + r);
+                sa[j] = *reinterpret_cast<const double2*>(c.score + r);
+                sb[j] = *reinterpret_cast<const double2*>(c.score + r + 2);
+            } else {
+                pv[j] = make_int4(DEAD, DEAD, DEAD, DEAD);
+                sa[j] = sb[j] = make_double2(0.0, 0.0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int32_t pe[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+            const double se[4] = {sa[j].x, sa[j].y, sb[j].x, sb[j].y};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK) + e;
+                const int32_t p = pe[e];
+                if (r >= n || p == DEAD || p <= sink_max || p >= recent_min) continue;
+                if (se[e] < best || (se[e] == best && p < bpos)) {
+                    best = se[e];
+                    bpos = p;
+                    bslot = r;
+                }
+            }
+        }
+    }
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const double ob = __shfl_xor(best, o);
+        const int32_t op = __shfl_xor(bpos, o);
+        const int os = __shfl_xor(bslot, o);
+        if (ob < best || (ob == best && op < bpos)) {
+            best = ob;
+            bpos = op;
+            bslot = os;
+        }
+    }
+    const int w = threadIdx.x / WAVE;
+    __syncthreads();
+    if (threadIdx.x % WAVE == 0) {
+        sh.redd[w] = best;
+        sh.rpos[w] = bpos;
+        sh.rslot[w] = bslot;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double b = sh.redd[0];
+        int32_t bp = sh.rpos[0];
+        int bs = sh.rslot[0];
+        for (int i = 1; i < OP_WAVES; ++i)
+            if (sh.redd[i] < b || (sh.redd[i] == b && sh.rpos[i] < bp)) {
+                b = sh.redd[i];
+                bp = sh.rpos[i];
+                bs = sh.rslot[i];
+            }
+        if (bs >= 0) {
+            c.pos[bs] = DEAD;
+            if (k < DEADLIST) sh.list[k] = bs;
+        }
+        sh.count = bs;
+    }
+    __syncthreads();
+    const int bs = sh.count;
+    __syncthreads();
+    return bs;
+}
+
 // Evict down to `budget` (compress.py:159-179): protected = the `sink` lowest
 // and `recent` highest live positions (recent == 0 protects all); drop the
-// n - budget lowest (score, position) of the rest.
-__device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t maxpos, int* red, int* holes,
-                     int* movers, unsigned* bits_lo, unsigned* bits_hi, double* redd) {
+// n - budget lowest (score, position) of the rest. have_bits: the window
+// bitmaps already hold every live row but the `cnt` appended at p0.. (maxpos
+// = p0 + cnt - 1).
+__device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t p0, int cnt, bool have_bits,
+                     OpShared& sh) {
     if (n <= budget || cfg.recent == 0) return n;
     const int n_drop = n - budget;
+    const int32_t maxpos = p0 + cnt - 1;
     // sink-th smallest and recent-th largest live positions, from bitmaps of
     // the windows [0, WIN) and (maxpos - WIN, maxpos]
-    for (int i = threadIdx.x; i < WIN / 32; i += BLK) {
-        bits_lo[i] = 0u;
-        bits_hi[i] = 0u;
+    if (have_bits) {
+        for (int t = threadIdx.x; t < cnt; t += OP_BLK) {
+            const int32_t p = p0 + t;
+            if (p < WIN) atomicOr(&sh.bits_lo[p / 32], 1u << (p % 32));
+            const int32_t dtop = maxpos - p;
+            if (dtop >= 0 && dtop < WIN) atomicOr(&sh.bits_hi[dtop / 32], 1u << (dtop % 32));
+        }
+        __syncthreads();
+    } else {
+        scan_rows(c, n, false, 0, true, maxpos, sh);
     }
-    __syncthreads();
-    for (int r = threadIdx.x; r < n; r += BLK) {
-        const int32_t p = c.pos[r];
-        if (p < WIN) atomicOr(&bits_lo[p / 32], 1u << (p % 32));
-        const int32_t dtop = maxpos - p;
-        if (dtop >= 0 && dtop < WIN) atomicOr(&bits_hi[dtop / 32], 1u << (dtop % 32));
-    }
-    __syncthreads();
-    __shared__ int32_t s_bounds[2];
     if (threadIdx.x == 0) {
         int32_t sink_max = -1;          // rows with pos <= sink_max are protected
-        int cnt = 0;
-        for (int p = 0; p < WIN && cnt < cfg.sink; ++p)
-            if (bits_lo[p / 32] >> (p % 32) & 1u) { ++cnt; sink_max = p; }
+        int cnt_lo = 0;
+        for (int p = 0; p < WIN && cnt_lo < cfg.sink; ++p)
+            if (sh.bits_lo[p / 32] >> (p % 32) & 1u) { ++cnt_lo; sink_max = p; }
         int32_t recent_min = INT_MAX;   // rows with pos >= recent_min are protected
-        cnt = 0;
-        for (int dt = 0; dt < WIN && cnt < cfg.recent; ++dt)
-            if (bits_hi[dt / 32] >> (dt % 32) & 1u) { ++cnt; recent_min = maxpos - dt; }
-        s_bounds[0] = (cnt >= cfg.recent || cnt == n) ? recent_min : -2;   // -2: not within the window
-        s_bounds[1] = sink_max;
+        int cnt_hi = 0;
+        for (int dt = 0; dt < WIN && cnt_hi < cfg.recent; ++dt)
+            if (sh.bits_hi[dt / 32] >> (dt % 32) & 1u) { ++cnt_hi; recent_min = maxpos - dt; }
+        sh.bounds[0] = (cnt_hi >= cfg.recent || cnt_hi == n) ? recent_min : -2;   // -2: not within the window
+        sh.bounds[1] = sink_max;
     }
     __syncthreads();
-    int32_t recent_min = s_bounds[0];
-    const int32_t sink_max = s_bounds[1];
+    int32_t recent_min = sh.bounds[0];
+    const int32_t sink_max = sh.bounds[1];
     if (recent_min == -2) {
         // binary search the recent-th largest live position
         int32_t lo = 0, hi = maxpos;
         while (lo < hi) {
             const int32_t mid = lo + (hi - lo + 1) / 2;
-            int cnt = 0;
-            for (int r = threadIdx.x; r < n; r += BLK) cnt += (c.pos[r] >= mid);
-            cnt = block_sum_int(cnt, red);
-            if (cnt >= cfg.recent) lo = mid; else hi = mid - 1;
+            int cnt_ge = 0;
+            for (int r = threadIdx.x; r < n; r += OP_BLK) cnt_ge += (c.pos[r] >= mid);
+            cnt_ge = block_sum_int(cnt_ge, sh.red);
+            if (cnt_ge >= cfg.recent) lo = mid; else hi = mid - 1;
         }
         recent_min = lo;
     }
-    __shared__ int s_slot[NWAVES];
-    __shared__ int32_t s_pos[NWAVES];
-    for (int k = 0; k < n_drop; ++k) {
-        double best = INFINITY;
-        int32_t bpos = INT_MAX;
-        int bslot = -1;
-        for (int r = threadIdx.x; r < n; r += BLK) {
-            const int32_t p = c.pos[r];
-            if (p == DEAD || p <= sink_max || p >= recent_min) continue;
-            const double sc = c.score[r];
-            if (sc < best || (sc == best && p < bpos)) { best = sc; bpos = p; bslot = r; }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            const double ob = __shfl_xor(best, o);
-            const int32_t op = __shfl_xor(bpos, o);
-            const int os = __shfl_xor(bslot, o);
-            if (ob < best || (ob == best && op < bpos)) { best = ob; bpos = op; bslot = os; }
-        }
-        const int w = threadIdx.x / WAVE;
-        __syncthreads();
-        if (threadIdx.x % WAVE == 0) { redd[w] = best; s_pos[w] = bpos; s_slot[w] = bslot; }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double b = redd[0];
-            int32_t bp = s_pos[0];
-            int bs = s_slot[0];
-            for (int i = 1; i < NWAVES; ++i)
-                if (redd[i] < b || (redd[i] == b && s_pos[i] < bp)) { b = redd[i]; bp = s_pos[i]; bs = s_slot[i]; }
-            if (bs >= 0) c.pos[bs] = DEAD;
-        }
-        __syncthreads();
-    }
-    return compact(c, n, DEAD, red, holes, movers);
+    int nv = 0;
+    for (; nv < n_drop; ++nv)
+        if (select_victim(c, n, sink_max, recent_min, nv, sh) < 0) break;
+    if (nv <= DEADLIST) return compact_list(c, n, nv, sh);
+    return compact(c, n, DEAD, sh.red, sh.sorted, sh.movers);
 }
 
 // ------------------------------------------------------------ fused layer op
@@ -350,29 +501,33 @@ struct OpArgs {
     int budget_per_layer;
 };
 
-__global__ void __launch_bounds__(BLK) drafter_op_kernel(OpArgs a) {
+__global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
     const int s = blockIdx.x, L = a.layer0 + blockIdx.y;
     const dkv_drafter_t& m = a.m;
     const dkv_qcfg_t cfg = a.cfgs[L];
     const int D = m.head_dim, H = m.n_kv_heads;
-    __shared__ int red[NWAVES];
-    __shared__ double redd[NWAVES];
-    __shared__ int holes[MAXMOVE], movers[MAXMOVE];
-    __shared__ unsigned bits_lo[WIN / 32], bits_hi[WIN / 32];
+    __shared__ OpShared sh;
 
     RowCtx c{&a.m, s, L, cfg.bits, page_fmt(cfg, D), m.pos + row_index(m, s, L), m.score + row_index(m, s, L)};
     int32_t* nrows_p = m.n_rows + (int64_t)s * m.n_layers + L;
     int n = *nrows_p;
     const int32_t p0 = a.start[s];
+    int want = a.src_full ? (a.end[s] - p0) : (a.count ? a.count[s] : a.T);
+    if (want < 0) want = 0;
+    // When the rows fit without clipping at cap, the eviction window (maxpos
+    // = p0 + want - 1) is known before the truncation, and one pass over the
+    // positions finds the truncated rows and fills the window bitmaps.
+    const bool one_pass = a.do_trunc && want > 0 && n + want <= m.cap && cfg.recent != 0;
+    bool have_bits = false;
     if (a.do_trunc) {
-        __syncthreads();
-        n = compact(c, n, p0, red, holes, movers);
+        const int nd = scan_rows(c, n, true, p0, one_pass, p0 + want - 1, sh);
+        have_bits = one_pass;
+        n = (nd <= DEADLIST) ? compact_list(c, n, nd, sh) : compact(c, n, p0, sh.red, sh.sorted, sh.movers);
     }
-    int cnt = a.src_full ? (a.end[s] - p0) : (a.count ? a.count[s] : a.T);
-    if (cnt < 0) cnt = 0;
+    int cnt = want;
     if (n + cnt > m.cap) cnt = max(0, m.cap - n);   // the host sizes cap; never write past it
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
-    for (int h = w; h < H; h += NWAVES) {          // one wave per head segment
+    for (int h = w; h < H; h += OP_WAVES) {        // one wave per head segment
         for (int t = 0; t < cnt; ++t) {
             const int slot = n + t;
             uint8_t* page = page_ptr(m, s, L, h, slot / PAGE);
@@ -400,7 +555,7 @@ __global__ void __launch_bounds__(BLK) drafter_op_kernel(OpArgs a) {
     n += cnt;
     if (cnt > 0) {
         const int budget = a.budget[a.budget_per_layer ? (L * m.batch + s) : s];
-        n = evict(c, n, budget, cfg, p0 + cnt - 1, red, holes, movers, bits_lo, bits_hi, redd);
+        n = evict(c, n, budget, cfg, p0, cnt, have_bits && cnt == want, sh);
     }
     __syncthreads();
     if (threadIdx.x == 0) *nrows_p = n;
@@ -754,6 +909,9 @@ __global__ void __launch_bounds__(BLK) drafter_gather_kernel(dkv_drafter_t m, in
 int check_mirror(const dkv_drafter_t* m, const char* fn) {
     DKV_REQUIRE(m != nullptr, std::string(fn) + ": mirror is NULL");
     DKV_REQUIRE(m->pages && m->pos && m->score && m->n_rows, std::string(fn) + ": mirror has a NULL buffer");
+    // the row scans read pos and score with 16-byte loads
+    DKV_REQUIRE(reinterpret_cast<uintptr_t>(m->pos) % 16 == 0 && reinterpret_cast<uintptr_t>(m->score) % 16 == 0,
+                std::string(fn) + ": pos and score must be 16-byte aligned");
     DKV_REQUIRE(m->batch > 0 && m->n_layers > 0 && m->n_layers <= 64 && m->n_kv_heads > 0 && m->cap > 0 &&
                     m->cap % PAGE == 0,
                 std::string(fn) + ": bad mirror shape (n_layers 1..64, cap a positive multiple of 32)");
@@ -804,7 +962,7 @@ extern "C" int dkv_drafter_append(const dkv_drafter_t* mirror, int32_t layer, dk
     a.start = start;
     a.count = count;
     a.budget = budget;
-    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, 1), dim3(BLK), 0, as_stream(stream), a);
+    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, 1), dim3(OP_BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_append");
 }
 
@@ -823,7 +981,7 @@ extern "C" int dkv_drafter_truncate(const dkv_drafter_t* mirror, const dkv_qcfg_
     a.T = 0;              // nothing appended, so no eviction and budget is never read
     a.start = start;
     a.budget = start;
-    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(BLK), 0, as_stream(stream), a);
+    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(OP_BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_truncate");
 }
 
@@ -852,7 +1010,7 @@ extern "C" int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* 
     a.end = end;
     a.budget = budget;
     a.budget_per_layer = 1;
-    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(BLK), 0, as_stream(stream), a);
+    hipLaunchKernelGGL(drafter_op_kernel, dim3(mirror->batch, mirror->n_layers), dim3(OP_BLK), 0, as_stream(stream), a);
     return check_launch("dkv_drafter_sync");
 }
 

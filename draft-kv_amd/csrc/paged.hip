@@ -444,28 +444,57 @@ __global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, 
     }
 }
 
-// Merge the chunk partials of each query row in chunk order; chunks that
-// start past the row's position were never computed for it and are skipped.
-__global__ void __launch_bounds__(256) paged_combine_kernel(const float* __restrict__ part, int T, int Hq, int D,
-                                                            const int32_t* __restrict__ start, int CH,
-                                                            int n_chunks, float* __restrict__ out) {
+// Merge the chunk partials of each query row; chunks that start past the
+// row's position were never computed for it and are skipped. The global max
+// comes first, so the weighted sums are independent terms: wave w sums
+// chunks w, w + 4, ... (lane: channels lane and lane + 64, 8 chunks' loads in
+// flight) and the 4 waves' sums meet in LDS in wave order. The result depends
+// only on the row's own chunks, never on the batch or the launch shape.
+constexpr int PCOMB_WAVES = 4;
+__global__ void __launch_bounds__(64 * PCOMB_WAVES) paged_combine_kernel(const float* __restrict__ part, int T,
+                                                                         int Hq, int D,
+                                                                         const int32_t* __restrict__ start, int CH,
+                                                                         int n_chunks, float* __restrict__ out) {
     const int hq = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
     const int qpos = start[s] + t;
     const int nc = min(qpos / CH + 1, n_chunks);   // never past the workspace
-    const float* p = part + (((int64_t)s * T + t) * Hq + hq) * n_chunks * (D + 2);
+    const int PD = D + 2;
+    const float* p = part + (((int64_t)s * T + t) * Hq + hq) * n_chunks * PD;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    __shared__ float smax[PCOMB_WAVES], sl[PCOMB_WAVES];
+    __shared__ float so[PCOMB_WAVES][2 * WAVE];
+    float mm = -INFINITY;
+    for (int c = threadIdx.x; c < nc; c += blockDim.x) mm = fmaxf(mm, p[(int64_t)c * PD + D]);
+    for (int o = WAVE / 2; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+    if (lane == 0) smax[w] = mm;
+    __syncthreads();
+    mm = smax[0];
+#pragma unroll
+    for (int i = 1; i < PCOMB_WAVES; ++i) mm = fmaxf(mm, smax[i]);
+    const bool a0 = lane < D, a1 = lane + WAVE < D;
+    float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
+    for (int c = w; c < nc; c += PCOMB_WAVES) {
+        const float* pc = p + (int64_t)c * PD;
+        const float mc = pc[D], lc = pc[D + 1];
+        const float x0 = a0 ? pc[lane] : 0.0f, x1 = a1 ? pc[lane + WAVE] : 0.0f;
+        const float wt = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
+        l = fmaf(lc, wt, l);
+        o0 = fmaf(x0, wt, o0);
+        o1 = fmaf(x1, wt, o1);
+    }
+    so[w][lane] = o0;
+    so[w][lane + WAVE] = o1;
+    if (lane == 0) sl[w] = l;
+    __syncthreads();
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float m = -INFINITY, l = 0.0f, o = 0.0f;
-        for (int ch = 0; ch < nc; ++ch) {
-            const float* pc = p + (int64_t)ch * (D + 2);
-            const float mc = pc[D], lc = pc[D + 1];
-            const float mn = fmaxf(m, mc);
-            const float a = (m == -INFINITY) ? 0.0f : __expf(m - mn);
-            const float b = (mc == -INFINITY) ? 0.0f : __expf(mc - mn);
-            l = l * a + lc * b;
-            o = o * a + pc[d] * b;
-            m = mn;
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PCOMB_WAVES; ++i) {
+            lt += sl[i];
+            ot += so[i][d];
         }
-        out[(((int64_t)s * T + t) * Hq + hq) * D + d] = o / l;
+        out[(((int64_t)s * T + t) * Hq + hq) * D + d] = ot / lt;
     }
 }
 
@@ -567,7 +596,7 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
     }
     int rc = dkv::check_launch("dkv_paged_attention");
     if (rc) return rc;
-    hipLaunchKernelGGL(dkv::paged_combine_kernel, dim3(n_q_heads, T, c.batch), dim3(128), 0, st,
+    hipLaunchKernelGGL(dkv::paged_combine_kernel, dim3(n_q_heads, T, c.batch), dim3(dkv::WAVE * dkv::PCOMB_WAVES), 0, st,
                        static_cast<const float*>(work), T, n_q_heads, c.head_dim, start, chunk_keys, n_chunks, out);
     return dkv::check_launch("dkv_paged_attention(combine)");
 }
