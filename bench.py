@@ -5,15 +5,21 @@ Default workload (``--workload e2e``): Llama-3-8B shape (32 layers, d_model
 4096, 32/8 GQA heads, head_dim 128, SwiGLU 14336, RoPE theta 500000, vocab
 128256), bf16 random weights N(0, 0.02), batch 32, context 32768 tokens of
 synthetic bf16 KV (N(0,1), 1% outlier channels x8) in 16-token pages with
-shuffled block tables, drafter mirror int4 group-32 (fp16 scale/zero)
-keep 0.25, gamma 8, temperature 0.8 rejection sampling. A step is one decode
-round over the batch: 8 draft forwards against the mirror, one 9-row verify
-forward against the full cache, acceptance, rollback and mirror resync.
+shuffled block tables, drafter arms int8 group-64 keep 1.0 and int4 group-32
+(fp16 scale/zero) keep 0.25 switched every 64 rounds (each switch
+requantizes the mirror), gamma chosen each round by the cost model (at most
+16), temperature 0.8 rejection sampling. A step is one decode round over the
+batch: gamma draft forwards against the mirror (replayed from a recorded HIP
+graph per mirror layout; ``--eager`` runs them op by op), one gamma+1-row
+verify forward against the full cache, acceptance, rollback and mirror
+resync.
 
 Printed on one line: accepted (emitted) tokens per second over the timed
 rounds, plus ``roofline`` for the drafter attention (algorithmic bytes per
-call / average call time from HIP events on the launch stream vs 8 TB/s) and
-``cpu_baseline`` (the numpy oracle on a bounded sample of the same round).
+call / average call time from HIP events on the launch stream vs 8 TB/s;
+with graphs the calls are timed right after the rounds on the run's own
+mirror, under each arm) and ``cpu_baseline`` (the numpy oracle on a bounded
+sample of the same round).
 
 ``--workload kernels`` times the attention kernels alone at the same shape
 (drafter pass and 9-query verify pass over rotating layers) for profiling.
@@ -56,6 +62,7 @@ def parse():
     ap.add_argument("--group", type=int, default=32)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="run the draft steps eagerly (no HIP graphs)")
     return ap.parse_args()
 
 
@@ -157,6 +164,10 @@ class EventTimer:
 
         setattr(obj, name, wrapped)
 
+    def restore(self):
+        self.on = False
+        setattr(self.obj, self.name, self.orig)
+
     def times_ms(self):
         return [s.elapsed_time(e) for s, e in self.pairs]
 
@@ -167,6 +178,37 @@ class EventTimer:
 
 
 # ---------------------------------------------------------------- CPU baseline
+def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
+    """Drafter attention calls timed with HIP events on the launch stream, on
+    the decode run's own mirror rebuilt under each arm in turn: every layer,
+    ``reps`` times, with N(0,1) queries and the attention mass on (as in the
+    draft steps). Returns {arm: [algorithmic bytes, us, calls]}."""
+    import numpy as np
+    import torch
+    L, b = comp.n_layers, comp.batch
+    g = torch.Generator(device=comp.device)
+    g.manual_seed(7)
+    q = torch.randn((b, n_q_heads, comp.d_head), generator=g, device=comp.device)
+    out = {}
+    for arm in arms:
+        if list(comp.cfgs) != [arm] * L:
+            comp.rebuild_layers(full, list(range(L)), [arm] * L)
+        comp.attend(0, q)
+        torch.cuda.synchronize()
+        t = EventTimer(comp, "attend")
+        t.on = True
+        for _ in range(reps):
+            for layer in range(L):
+                comp.attend(layer, q)
+        torch.cuda.synchronize()
+        t.restore()
+        rows = comp.rows()
+        nbytes = reps * sum(drafter_bytes(rows[:, layer].astype(np.float64), comp.n_kv_heads, comp.d_head,
+                                          arm.bits, arm.group, n_q_heads) for layer in range(L))
+        out[arm] = [nbytes, sum(t.times_ms()) * 1e3, len(t.pairs)]
+    return out
+
+
 def cpu_baseline(ctx: int, gamma: int, T: float, bits: int, keep: float, group: int, tokens_per_round: float):
     """The numpy oracle on a bounded sample of the same round: one sequence,
     one decode round (gamma drafts, verify, accept, rollback, resync) of the
@@ -298,6 +340,7 @@ class ScheduledArms:
         g, _ = self.best_gamma(self.cost, arm, a / (a + b), ctx, self.gamma_max)
         self.round += 1
         self.gammas.append(g)
+        self.last_arm = arm
         return arm, max(1, g)
 
     def update(self, cfg, gamma, accepted, ctx, key=None):
@@ -338,28 +381,39 @@ def run_e2e(args):
                      batch=b)
     ctrl = ScheduledArms(arms, args.period, cost, ctx, gamma_max=gmax)
     eng = DraftKVEngine(model, ctrl, seed=0)
-    batch = DecodeBatch(eng, toks, full, max_new, args.temperature, reserve_cfgs=arms)
+    batch = DecodeBatch(eng, toks, full, max_new, args.temperature, reserve_cfgs=arms, graphs=not args.eager)
     log("warmup rounds (the first builds the drafter mirror)")
     for _ in range(max(1, args.warmup)):
         batch.step()
     torch.cuda.synchronize()
     comp = batch.comp
-    t_draft = EventTimer(comp, "attend", tag=lambda layer, *a, **k: (comp.cfgs[layer],
-                                                                      comp.seen.copy()))
+    # drafter calls are timed live when the draft steps run eagerly; replayed
+    # draft-step graphs never pass through the Python call, so then the
+    # drafter is timed right after the rounds, on the same mirror
+    live = not batch.use_graphs
+    t_draft = EventTimer(comp, "attend", tag=lambda layer, *a, **k: (comp.cfgs[layer], comp.seen.copy())) \
+        if live else None
     t_ver = EventTimer(full, "attend")
     t_req = EventTimer(comp, "rebuild_layers")
-    for t in (t_draft, t_ver, t_req):
+    timers = [t for t in (t_draft, t_ver, t_req) if t is not None]
+    for t in timers:
         t.on = True
     log(f"timing {args.steps} rounds (arm switch every {args.period} rounds)")
     emitted = 0
+    arm_time = {}      # arm -> [seconds, tokens, rounds] (each round ends in a host read-back)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
+        tr = time.perf_counter()
         batch.step()
         emitted += batch.last_emitted
+        at = arm_time.setdefault(ctrl.last_arm, [0.0, 0, 0])
+        at[0] += time.perf_counter() - tr
+        at[1] += batch.last_emitted
+        at[2] += 1
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    for t in (t_draft, t_ver, t_req):
+    for t in timers:
         t.on = False
     per_arm = {}
     for r in batch.res:
@@ -370,13 +424,17 @@ def run_e2e(args):
             st[2] += 1
     # drafter attention: bytes of each timed call from the rows the mirror held
     arm_calls = {}
-    for (s_ev, e_ev), (cfg, seen) in zip(t_draft.pairs, t_draft.tags):
-        rows = [min(int(n), _budget(cfg, int(n))) for n in seen]
-        nbytes = drafter_bytes(rows, Hkv, D, cfg.bits, cfg.group, Hq)
-        c = arm_calls.setdefault(cfg, [0.0, 0.0, 0])
-        c[0] += nbytes
-        c[1] += s_ev.elapsed_time(e_ev) * 1e3
-        c[2] += 1
+    if live:
+        for (s_ev, e_ev), (cfg, seen) in zip(t_draft.pairs, t_draft.tags):
+            rows = [min(int(n), _budget(cfg, int(n))) for n in seen]
+            nbytes = drafter_bytes(rows, Hkv, D, cfg.bits, cfg.group, Hq)
+            c = arm_calls.setdefault(cfg, [0.0, 0.0, 0])
+            c[0] += nbytes
+            c[1] += s_ev.elapsed_time(e_ev) * 1e3
+            c[2] += 1
+    else:
+        log("drafter attention timed per call on the run's mirror, under each arm")
+        arm_calls = time_drafter(comp, full, arms, Hq)
     main_arm = arms[1]
     mb, mus, mn = arm_calls.get(main_arm, [float("nan"), float("nan"), 0])
     achieved = mb / (mus * 1e-6) / 1e9 if mn else float("nan")
@@ -403,6 +461,20 @@ def run_e2e(args):
     torch.cuda.synchronize()
     base_tps = b * args.baseline_steps / (time.perf_counter() - tb0)
     value = emitted / dt
+    # measured round speedup per arm against the cost model at 8 TB/s: its
+    # ceiling (alpha -> 1, gamma -> inf) and its prediction at the measured
+    # acceptance and mean gamma of that arm
+    cost_model = {}
+    for arm, (secs, tok, nr) in arm_time.items():
+        st_ = per_arm.get(arm.label(), [0, 0, 0])
+        alpha_a = st_[0] / max(st_[1], 1)
+        gam = max(1, round(st_[1] / max(st_[2], 1)))
+        meas = (tok / secs) / base_tps
+        cost_model[arm.label()] = {
+            "rounds": nr, "tok_s": tok / secs, "measured_speedup": meas,
+            "ceiling": cost.ceiling(arm, ctx), "frac_of_ceiling": meas / cost.ceiling(arm, ctx),
+            "modeled_speedup": cost.speedup(arm, gam, alpha_a, ctx), "gamma": gam, "alpha": alpha_a,
+            "frac_of_modeled": meas / cost.speedup(arm, gam, alpha_a, ctx)}
     acc_total = sum(v[0] for v in per_arm.values())
     drafted = sum(v[1] for v in per_arm.values())
     alpha = {k: v[0] / max(v[1], 1) for k, v in per_arm.items()}
@@ -430,7 +502,8 @@ def run_e2e(args):
                    "gamma_mean": float(np.mean(ctrl.gammas[-args.steps:])),
                    "tokens_per_round": emitted / args.steps / b,
                    "full_kv_decode_tok_s": base_tps, "speedup_vs_full_kv_decode": value / base_tps,
-                   "requantize_ms": [round(t, 3) for t in t_req.times_ms()]},
+                   "requantize_ms": [round(t, 3) for t in t_req.times_ms()],
+                   "draft_graphs": batch.use_graphs, "cost_model_8tbs": cost_model},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": "profiles/attention_hbm_traffic_b32_ctx32k.md (FETCH_SIZE x 2.0 + "

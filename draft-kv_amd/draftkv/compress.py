@@ -81,6 +81,12 @@ class FullKVCache(PagedKVCache):
         self.n_blocks = new
         self._dirty = (0, self.max_blocks)
 
+    def _make_room(self, s: int, n: int) -> None:
+        # growing only adds ids under the free list, so the ids handed out, and
+        # the final pool size, are those of growing block by block
+        while self.pools[s].n_free < n:
+            self._grow()
+
     def _ensure_capacity(self, s, layer, extra):
         while True:
             need_blocks = -(-(int(self.n_tokens[s, layer]) + extra) // self.block_size) - int(self.table_len[s, layer])
@@ -182,21 +188,33 @@ class CompressedKVCache:
         return [self.qcfg(L) for L in range(self.n_layers)]
 
     def _i32(self, a) -> torch.Tensor:
-        return torch.as_tensor(np.asarray(a, np.int32), device=self.device)
+        return ops.to_device(np.asarray(a, np.int32), self.device)
 
     # ------------------------------------------------------------ batched device ops
     def budgets(self) -> np.ndarray:
-        """int32 [n_layers, batch] budgets at the current ``seen``."""
-        return np.array([[_budget(self.cfgs[L], int(self.seen[s])) for s in range(self.batch)]
-                         for L in range(self.n_layers)], np.int32)
+        """int32 [n_layers, batch] budgets at the current ``seen``: _budget of
+        every (layer, sequence), one vector evaluation per distinct arm (numpy's
+        rint rounds half to even, as Python's round does)."""
+        seen = np.maximum(self.seen, 1).astype(np.float64)
+        out = np.empty((self.n_layers, self.batch), np.int32)
+        by_cfg: dict = {}
+        for L, c in enumerate(self.cfgs):
+            by_cfg.setdefault(c, []).append(L)
+        for c, layers in by_cfg.items():
+            out[layers] = np.maximum(np.rint(c.keep_frac * seen).astype(np.int64), c.sink + c.recent)
+        return out
 
-    def begin_step(self, start: Sequence[int], count: Sequence[int]) -> torch.Tensor:
+    def step_budgets(self, start: Sequence[int], count: Sequence[int]) -> np.ndarray:
         """Account a forward that appends ``count[s]`` rows at ``start[s]`` to
         every layer (layer 0 moves ``seen``, compress.py:131-132) and return the
-        per-layer budgets as a device int32 [n_layers, batch] tensor."""
+        per-layer budgets, int32 [n_layers, batch] on the host."""
         st, ct = np.asarray(start, np.int64), np.asarray(count, np.int64)
         self.seen = np.where(ct > 0, np.maximum(self.seen, st + ct), self.seen)
-        return self._i32(self.budgets())
+        return self.budgets()
+
+    def begin_step(self, start: Sequence[int], count: Sequence[int]) -> torch.Tensor:
+        """step_budgets as a device int32 [n_layers, batch] tensor."""
+        return self._i32(self.step_budgets(start, count))
 
     def append_layer(self, layer: int, k: torch.Tensor, v: torch.Tensor, start: torch.Tensor,
                      budget_row: torch.Tensor, count: Optional[torch.Tensor] = None) -> None:

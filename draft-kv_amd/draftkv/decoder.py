@@ -159,9 +159,8 @@ class Decoder:
         if self.pos_table is not None and max_pos > self.pos_table.shape[0]:
             raise IndexError(f"position {max_pos - 1} beyond the position table ({self.pos_table.shape[0]})")
         dev = self.device
-        positions = torch.as_tensor(pos.reshape(-1)).to(dev, non_blocking=True)
+        positions = ops.to_device(pos.reshape(-1), dev)
         tok = tokens.reshape(-1).to(torch.int32).contiguous()
-        R = b * T
         cs, cs_len = (None, 0)
         if self.rope_theta is not None:
             cs, cs_len = self._cos_sin(max_pos)
@@ -174,6 +173,15 @@ class Decoder:
             raise TypeError(f"unsupported cache type {type(cache).__name__}: the GPU forward runs against "
                             "draftkv.paged.PagedKVCache / compress.FullKVCache / compress.CompressedKVCache")
 
+        logits = self._core(tok, positions, b, T, attn, cs, cs_len)
+        attn.finish()
+        return logits
+
+    def _core(self, tok: torch.Tensor, positions: torch.Tensor, b: int, T: int, attn, cs, cs_len) -> torch.Tensor:
+        """The device part of a forward: embed, the decoder layers (attention
+        through ``attn(L, q, k, v)``), final norm and head; no host sync and no
+        host-dependent shapes, so a HIP graph can record it."""
+        R = b * T
         h = ops.embed(self.emb, tok, self.pos_table, positions if self.pos_table is not None else None)
         Hq, Hkv, D = self.n_heads, self.n_kv_heads, self.d_head
         nL = len(self.layers)
@@ -187,9 +195,7 @@ class Decoder:
             nxt = self.layers[L + 1] if L + 1 < nL else None
             nw, nb = (nxt.n1w, nxt.n1b) if nxt is not None else (self.nfw, self.nfb)
             x = self._residual(h, self._mlp_inner(x, p), p.w2, p.b2, nw, nb)
-        logits = self._head(x).view(b, T, self.vocab_size)
-        attn.finish()
-        return logits
+        return self._head(x).view(b, T, self.vocab_size)
 
     # ------------------------------------------------------------ caches
     def _paged_attention(self, cache: PagedKVCache, b, T, st, ct, max_pos):
@@ -207,8 +213,8 @@ class Decoder:
                 raise ValueError(f"sequence {s}: rows must be appended at the cache end "
                                  f"(start {st[s]}, cache holds {have[s]})")
         cache.reserve(ct)
-        start_d = torch.as_tensor(st.astype(np.int32)).to(self.device, non_blocking=True)
-        count_d = None if np.all(ct == T) else torch.as_tensor(ct.astype(np.int32)).to(self.device, non_blocking=True)
+        start_d = ops.to_device(st.astype(np.int32), self.device)
+        count_d = None if np.all(ct == T) else ops.to_device(ct.astype(np.int32), self.device)
 
         def attn(L, q, k, v):
             cache.append_layer(L, k, v, start_d, count_d)
@@ -220,25 +226,35 @@ class Decoder:
     def _mirror_attention(self, cache: CompressedKVCache, b, T, st, ct):
         if T != 1:
             raise ValueError("the drafter mirror takes one row per sequence per forward")
+        # a segment never holds more rows than positions
+        self.prepare_mirror(cache, b, int((st + ct).max()) if b else 0)
+        budgets = cache.begin_step(st, ct)
+        start_d = ops.to_device(st.astype(np.int32), self.device)
+        count_d = None if np.all(ct == 1) else ops.to_device(ct.astype(np.int32), self.device)
+        return self.mirror_attn(cache, b, start_d, budgets, count_d)
+
+    def mirror_attn(self, cache: CompressedKVCache, b: int, start_d, budgets_d, count_d):
+        """attn(L, q, k, v) of a draft forward over device tensors: append the
+        step's row to layer L of the mirror (evicting to budgets_d[L]), then
+        attend its query over the live rows."""
+        def attn(L, q, k, v):
+            cache.append_layer(L, k, v, start_d, budgets_d[L], count_d)
+            return cache.attend(L, q.view(b, self.n_heads, self.d_head))
+
+        attn.finish = lambda: None
+        return attn
+
+    def prepare_mirror(self, cache: CompressedKVCache, b: int, need: int) -> None:
+        """Allocate the mirror on first use and grow it to hold ``need`` rows
+        per segment (the host half of a draft forward's setup)."""
         if not cache._ready:
             cache.batch = b
             cache.seen = np.zeros(b, np.int64)
             cache._alloc(self.n_kv_heads, self.d_head, max(cache._cap_hint or 0, 4096))
         if cache.batch != b:
             raise ValueError(f"mirror batch {cache.batch} != token batch {b}")
-        need = int((st + ct).max()) if b else 0
-        if need > cache.cap:                 # a segment never holds more rows than positions
+        if need > cache.cap:
             cache._regrow(max(2 * cache.cap, need))
-        budgets = cache.begin_step(st, ct)
-        start_d = torch.as_tensor(st.astype(np.int32)).to(self.device, non_blocking=True)
-        count_d = None if np.all(ct == 1) else torch.as_tensor(ct.astype(np.int32)).to(self.device, non_blocking=True)
-
-        def attn(L, q, k, v):
-            cache.append_layer(L, k, v, start_d, budgets[L], count_d)
-            return cache.attend(L, q.view(b, self.n_heads, self.d_head))
-
-        attn.finish = lambda: None
-        return attn
 
     # ------------------------------------------------------------ reference protocol
     def forward(self, tokens, cache, start_pos: int) -> np.ndarray:

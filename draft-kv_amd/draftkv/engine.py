@@ -22,6 +22,7 @@ consumed, so the stream stays where the reference's would be.
 
 from __future__ import annotations
 
+import warnings
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
 
@@ -30,6 +31,7 @@ import torch
 
 from . import ops
 from .compress import CompressedKVCache
+from .graphs import DraftStepGraph, graph_key
 from .config import CompressionConfig
 from .controller import Controller, FixedPolicy
 
@@ -88,6 +90,7 @@ class DraftKVEngine:
         self.full_cache_factory = full_cache_factory
         self.last_full = None       # the full cache of the last call (inspection, tests)
         self.last_mirror = None
+        self.draft_graphs = True    # replay draft steps from recorded HIP graphs (DecodeBatch)
 
     # ------------------------------------------------------------------ util
     def _g(self, s: int) -> np.random.Generator:
@@ -116,7 +119,7 @@ class DraftKVEngine:
         self.model.forward_batch(torch.as_tensor(tk).to(self.model.device), full, [0] * len(prompts), lens - 1)
 
     def _pending(self, toks) -> torch.Tensor:
-        return torch.as_tensor(np.array([t[-1] for t in toks], np.int32)).to(self.model.device)
+        return ops.to_device(np.array([t[-1] for t in toks], np.int32), self.model.device)
 
     @staticmethod
     def _check_prompts(prompts, vocab: int):
@@ -179,6 +182,9 @@ class DraftKVEngine:
         return batch.results()
 
 
+_RECORD = object()   # DecodeBatch._draft_graph: record a graph after this round's first step
+
+
 class DecodeBatch:
     """A batch in the middle of self-speculative decoding: token lists, the
     full cache (holding positions 0 .. len-2 of every sequence), the drafter
@@ -186,7 +192,8 @@ class DecodeBatch:
     (engine.py:138-221) for every unfinished sequence."""
 
     def __init__(self, engine: DraftKVEngine, toks: list, full, max_new_tokens: int, temperature: float = 0.0,
-                 context_key: Optional[str] = None, reserve_cfgs: Sequence = ()) -> None:
+                 context_key: Optional[str] = None, reserve_cfgs: Sequence = (),
+                 graphs: Optional[bool] = None) -> None:
         self.engine, self.model = engine, engine.model
         self.toks = toks
         self.full = full
@@ -205,9 +212,54 @@ class DecodeBatch:
         self.last_emitted = 0             # tokens emitted by the last step, summed over the batch
         # arms the mirror may switch to: its pages are sized for the widest from the start
         self.reserve_cfgs = list(reserve_cfgs) or list(getattr(engine.controller, "arms", ()))
+        # draft steps replayed from recorded HIP graphs (one per mirror layout)
+        if graphs is None:
+            graphs = getattr(engine, "draft_graphs", True)
+        self.use_graphs = bool(graphs) and self.model.device.type == "cuda"
+        self._graphs: dict = {}
+        self._pool = None
+        self._pending_key = None
+        self.last_draft = None            # (tokens, logits) of the last round's draft steps
 
     def _sync(self, start) -> None:
         self.comp.sync_from(self.full, start)
+
+    # ------------------------------------------------------------ draft-step graphs
+    def _draft_graph(self, n, act, gamma):
+        """The recorded draft step for the mirror's current layout, _RECORD when
+        this round should record one after an eager first step, or None (no
+        graphs). Grows the mirror and the RoPE table for the round's positions
+        first, so nothing the graph points at moves during the round."""
+        model, comp, b = self.model, self.comp, self.b
+        last = np.where(act > 0, n - 2 + gamma, 0)
+        if model.pos_table is not None and int(last.max()) >= model.pos_table.shape[0]:
+            raise IndexError(f"position {int(last.max())} beyond the position table ({model.pos_table.shape[0]})")
+        model.prepare_mirror(comp, b, int((last + act).max()))
+        if model.rope_theta is not None:
+            model._cos_sin(int(last.max()) + 1)
+        key = graph_key(model, comp, b, self.T)
+        g = self._graphs.get(key)
+        if g is not None:
+            return g
+        self._pending_key = key
+        return _RECORD
+
+    def _record_graph(self):
+        key = self._pending_key
+        try:
+            if self._pool is None:
+                self._pool = torch.cuda.graph_pool_handle()
+            g = DraftStepGraph(self.model, self.comp, self.b, self.T, self._pool)
+        except Exception as e:            # keep decoding eagerly
+            warnings.warn(f"draft-step graph recording failed ({e}); decoding eagerly")
+            self.use_graphs = False
+            return None
+        if g.key != key:
+            raise RuntimeError("the mirror moved while a draft-step graph was recorded")
+        while len(self._graphs) >= 4:     # a few arms' layouts; the oldest goes first
+            self._graphs.pop(next(iter(self._graphs)))
+        self._graphs[key] = g
+        return g
 
     def results(self) -> list:
         for s in range(self.b):
@@ -222,6 +274,7 @@ class DecodeBatch:
         produced = n - self.plen
         active = produced < self.max_new
         self.last_emitted = 0
+        self.last_draft = None
         if not active.any():
             return False
         act = active.astype(np.int64)
@@ -234,7 +287,7 @@ class DecodeBatch:
         if gamma <= 0:
             logits = model.forward_batch(eng._pending(toks)[:, None], full, n - 1, act)[:, 0]
             u = np.array([eng._g(s).random() if active[s] else 0.5 for s in range(b)])
-            tok = ops.sample(logits, T, torch.as_tensor(u).to(dev)).cpu().numpy()
+            tok = ops.sample(logits, T, ops.to_device(u, dev)).cpu().numpy()
             for s in np.flatnonzero(active):
                 toks[s].append(int(tok[s]))
                 res[s].verify_passes += 1
@@ -273,20 +326,31 @@ class DecodeBatch:
             u_draft[:, s] = g.random(gamma)
             states[s] = g.bit_generator.state
             u_ver[s] = g.random(gamma + 1)
-        u_draft_d = torch.as_tensor(u_draft).to(dev)
-        u_ver_d = torch.as_tensor(u_ver).to(dev)
+        u_draft_d = ops.to_device(u_draft, dev)
+        u_ver_d = ops.to_device(u_ver, dev)
 
         # -- draft
         x = eng._pending(toks)
         pending = x
         draft_tok = torch.empty((b, gamma), dtype=torch.int32, device=dev)
         draft_logits = torch.empty((b, gamma, V), dtype=torch.float32, device=dev) if T > 0 else None
-        for i in range(gamma):
+        graph = self._draft_graph(n, act, gamma) if self.use_graphs else None
+        # with a graph for this layout recorded, every step replays it; on the
+        # layout's first round step 0 runs eagerly (warming every kernel and GEMM
+        # shape) and the graph is recorded after it
+        n_eager = gamma if graph is None else (1 if graph is _RECORD else 0)
+        for i in range(n_eager):
             lg = model.forward_batch(x[:, None], comp, n - 1 + i, act)[:, 0]
             if draft_logits is not None:
                 draft_logits[:, i].copy_(lg)
             x = ops.sample(lg, T, u_draft_d[i])
             draft_tok[:, i] = x
+        if graph is _RECORD:
+            graph = self._record_graph()
+        if graph is not None:
+            graph.run(x, [n - 1 + i for i in range(n_eager, gamma)], act, u_draft[n_eager:], draft_tok,
+                      draft_logits, col0=n_eager)
+        self.last_draft = (draft_tok, draft_logits)
 
         # -- verify
         block = torch.cat([pending[:, None], draft_tok], 1).contiguous()

@@ -5,6 +5,7 @@ non-zero status. There is no CPU path."""
 
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 from typing import Optional, Sequence
 
@@ -57,6 +58,61 @@ class Workspace:
 
 
 _WS = Workspace()
+
+
+class Stager:
+    """Host-to-device copies through page-locked staging buffers: the copy is
+    queued on the current stream and the host returns at once (a copy out of
+    pageable memory makes the host wait until the GPU has drained the
+    stream). Slots are reused round-robin; a slot is refilled only after its
+    last copy has finished."""
+
+    def __init__(self, n_slots: int = 64) -> None:
+        self.slots: list = [None] * n_slots     # (pinned uint8 buffer, event of its last copy)
+        self.i = 0
+
+    def to_device(self, a, device) -> torch.Tensor:
+        import numpy as np
+        a = np.ascontiguousarray(a)
+        if torch.device(device).type != "cuda":
+            return torch.from_numpy(a.copy())
+        out = torch.empty(a.shape, dtype=torch.from_numpy(a[:0].reshape(-1)).dtype, device=device)
+        if a.nbytes == 0:
+            return out
+        k = self.i
+        self.i = (k + 1) % len(self.slots)
+        slot = self.slots[k]
+        if slot is not None:
+            slot[1].synchronize()
+        buf = slot[0] if slot is not None and slot[0].numel() >= a.nbytes else \
+            torch.empty(max(a.nbytes, 4096), dtype=torch.uint8, pin_memory=True)
+        buf.numpy()[: a.nbytes] = a.reshape(-1).view(np.uint8)
+        out.view(-1).view(torch.uint8).copy_(buf[: a.nbytes], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.slots[k] = (buf, ev)
+        return out
+
+
+_STAGER = Stager()
+
+
+def to_device(a, device) -> torch.Tensor:
+    """A numpy array (or anything np.asarray takes) as a new device tensor of
+    its dtype, copied asynchronously on the current stream."""
+    return _STAGER.to_device(a, device)
+
+
+@contextlib.contextmanager
+def private_workspace(ws: Workspace):
+    """Route every op's scratch to ``ws`` inside the block (a captured HIP
+    graph keeps the buffers it was recorded with, so it owns them)."""
+    global _WS
+    old, _WS = _WS, ws
+    try:
+        yield ws
+    finally:
+        _WS = old
 
 
 def qcfg(bits: int, group: int = 64, meta_f16: bool = False, sink: int = 4, recent: int = 32) -> QCfg:

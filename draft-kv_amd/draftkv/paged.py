@@ -47,6 +47,18 @@ class BlockPool:
         self._live.add(b)
         return b
 
+    def allocate_many(self, n: int) -> list:
+        """n allocate() calls at once: the blocks in the order they would be
+        handed out. Raises (allocating nothing) when fewer than n are free."""
+        if n > len(self._stack):
+            raise BlockPoolExhausted(f"{n} blocks wanted, {len(self._stack)} of {self.n_blocks} free")
+        if n <= 0:
+            return []
+        got = self._stack[-n:][::-1]
+        del self._stack[-n:]
+        self._live.update(got)
+        return got
+
     def free(self, block: int) -> None:
         if block not in self._live:
             raise RuntimeError(f"double free of block {block}")
@@ -127,14 +139,40 @@ class PagedKVCache:
             lo, hi = self._dirty or (idx, idx + 1)
             self._dirty = (min(lo, idx), max(hi, idx + 1))
 
+    def _make_room(self, s: int, n: int) -> None:
+        """Hook before sequence s takes n blocks (a fixed pool raises when short)."""
+
     def reserve(self, counts: Sequence[int]) -> None:
         """Allocate blocks for ``counts[s]`` more tokens in every layer, layer by
-        layer as the reference's per-layer appends would, and push the new
-        table entries to the device."""
-        for layer in range(self.n_layers):
-            for s in range(self.batch):
-                if counts[s] > 0:
-                    self._ensure_capacity(s, layer, int(counts[s]))
+        layer as the reference's per-layer appends would (each sequence's pool
+        hands its blocks to layer 0 first, then layer 1, ...), and push the new
+        table entries to the device. Vectorized over (sequence, layer): only the
+        pairs that need a block are visited."""
+        cnt = np.asarray(counts, np.int64).reshape(self.batch)
+        grow = cnt > 0
+        if not grow.any():
+            return
+        bs = self.block_size
+        need = self.n_tokens + cnt[:, None]
+        want = np.where(grow[:, None], np.maximum(-(-need // bs), self.table_len), self.table_len)
+        if int(want.max()) > self.max_blocks:
+            s = int(np.flatnonzero((want > self.max_blocks).any(axis=1))[0])
+            raise BlockPoolExhausted(f"sequence {s} exceeds max_tokens={self.max_tokens}")
+        add = want - self.table_len
+        for s in np.flatnonzero(add.any(axis=1)):
+            self._make_room(int(s), int(add[s].sum()))
+            got = self.pools[s].allocate_many(int(add[s].sum()))
+            i = 0
+            for L in np.flatnonzero(add[s]):
+                k, t0 = int(add[s, L]), int(self.table_len[s, L])
+                self.tables[s, L, t0: t0 + k] = got[i: i + k]
+                i += k
+        if add.any():
+            lo = int(self.table_len[add > 0].min())
+            hi = int(want.max())
+            dl, dh = self._dirty or (lo, hi)
+            self._dirty = (min(dl, lo), max(dh, hi))
+            self.table_len = want
         self._upload()
 
     def _upload(self) -> None:
@@ -143,7 +181,7 @@ class PagedKVCache:
         lo, hi = self._dirty
         phys = self.tables[:, :, lo:hi] + (np.arange(self.batch, dtype=np.int32) * self.n_blocks)[:, None, None]
         phys = np.where(self.tables[:, :, lo:hi] >= 0, phys, 0).astype(np.int32)
-        self.d_tables[:, :, lo:hi].copy_(torch.from_numpy(np.ascontiguousarray(phys)))
+        self.d_tables[:, :, lo:hi].copy_(ops.to_device(phys, self.device))
         self._dirty = None
 
     # ------------------------------------------------------------ batched device ops
@@ -200,18 +238,18 @@ class PagedKVCache:
     def truncate(self, n_pos) -> None:                                 # paged.py:144-162
         """Drop positions >= n_pos (an int for every sequence, or one per sequence)."""
         cut = np.broadcast_to(np.asarray(n_pos, np.int64), (self.batch,))
-        for s in range(self.batch):
-            for L in range(self.n_layers):
-                keep = min(int(self.n_tokens[s, L]), int(cut[s]))
-                if keep == self.n_tokens[s, L]:
-                    continue
-                self.n_tokens[s, L] = keep
-                need = -(-keep // self.block_size)
-                while self.table_len[s, L] > need:
-                    self.table_len[s, L] -= 1
-                    idx = int(self.table_len[s, L])
-                    self.pools[s].free(int(self.tables[s, L, idx]))
-                    self.tables[s, L, idx] = -1
+        keep = np.minimum(self.n_tokens, cut[:, None])
+        changed = keep != self.n_tokens
+        if not changed.any():
+            return
+        self.n_tokens = np.where(changed, keep, self.n_tokens)
+        need = np.where(changed, -(-keep // self.block_size), self.table_len)
+        # emptied tail blocks go back per sequence, layer by layer, last first
+        for s, L in zip(*np.nonzero(self.table_len > need)):
+            for idx in range(int(self.table_len[s, L]) - 1, int(need[s, L]) - 1, -1):
+                self.pools[s].free(int(self.tables[s, L, idx]))
+                self.tables[s, L, idx] = -1
+            self.table_len[s, L] = need[s, L]
 
     @property
     def block_table(self) -> list:

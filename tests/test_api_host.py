@@ -98,3 +98,68 @@ def test_block_pool_semantics():
     with pytest.raises(RuntimeError, match="double free"):
         p2.free(a)
     assert plan_blocks_needed(33, 3, 16) == 9
+
+
+def test_paged_reserve_truncate_match_reference_allocator():
+    """The batched cache's vectorized reserve/truncate hand out and return
+    blocks exactly as the reference's per-layer appends and truncate do
+    (paged.py:112-162), sequence by sequence: same block tables, same free
+    lists, same lengths. Host logic only (a CPU store of tiny rows)."""
+    from draftkv.paged import PagedKVCache
+    from oracle.caches import PagedKVCache as RefPaged
+    L, b, bs, nb = 3, 4, 4, 256
+    pc = PagedKVCache(L, 1, 2, block_size=bs, n_blocks=nb, batch=b, max_tokens=200, device="cpu")
+    refs = [RefPaged(L, 1, 2, bs, nb) for _ in range(b)]
+    rng = np.random.default_rng(0)
+    for _ in range(60):
+        if rng.random() < 0.6:
+            cnt = rng.integers(0, 9, b)
+            pc.reserve(cnt)
+            pc.commit(cnt)
+            for s in range(b):
+                n = refs[s].length
+                z = np.zeros((int(cnt[s]), 1, 2), np.float32)
+                if cnt[s] > 0:
+                    for layer in range(L):
+                        refs[s].append(layer, z, z, np.arange(n, n + cnt[s]))
+        else:
+            cut = np.maximum(pc.lengths() - rng.integers(0, 6, b), 0)
+            pc.truncate(cut)
+            for s in range(b):
+                refs[s].truncate(int(cut[s]))
+        for s in range(b):
+            assert [pc.tables[s, ly, : pc.table_len[s, ly]].tolist() for ly in range(L)] == refs[s].block_table
+            assert pc.pools[s]._stack == refs[s].pool.free_list
+            pc.pools[s].check_invariants()
+        assert pc.lengths().tolist() == [r.length for r in refs]
+    # the device table mirror holds every live block id (physical = local + s * n_blocks)
+    for s in range(b):
+        for ly in range(L):
+            n = int(pc.table_len[s, ly])
+            assert (pc.d_tables[s, ly, :n].numpy() == pc.tables[s, ly, :n] + s * nb).all()
+    with pytest.raises(BlockPoolExhausted):
+        pc.reserve([1000, 0, 0, 0])
+
+
+def test_growing_full_cache_reserve_matches_block_by_block():
+    """FullKVCache grows its pools instead of running dry; the vectorized
+    reserve hands out the same ids, and ends with the same pool size, as
+    allocating block by block through _ensure_capacity (its batch-1 path)."""
+    from draftkv.compress import FullKVCache
+    a = FullKVCache(2, 1, 2, batch=3, device="cpu", block_size=4, max_tokens=4096)
+    b = FullKVCache(2, 1, 2, batch=3, device="cpu", block_size=4, max_tokens=4096)
+    rng = np.random.default_rng(1)
+    for _ in range(12):
+        cnt = rng.integers(0, 90, 3)
+        a.reserve(cnt)
+        a.commit(cnt)
+        for layer in range(2):
+            for s in range(3):
+                if cnt[s] > 0:
+                    b._ensure_capacity(s, layer, int(cnt[s]))
+        b._upload()
+        b.commit(cnt)
+        assert a.n_blocks == b.n_blocks
+        assert (a.tables == b.tables).all() and (a.table_len == b.table_len).all()
+        assert all(p._stack == q._stack for p, q in zip(a.pools, b.pools))
+        assert (a.d_tables.numpy() == b.d_tables.numpy()).all()
