@@ -99,6 +99,37 @@ __device__ __forceinline__ int quant_code(float x, GroupMeta m, int bits) {
     return static_cast<int>(q);
 }
 
+// quant_code of 8 values of one group without a division on the common path.
+// With inv = rcp(scale) (hardware reciprocal, within 1 ulp) the product
+// q = RN(d * inv) lies within 2^-22 |Q| of the exact quotient Q = d / scale
+// (d = RN(x - lo)), and RN(Q) within 2^-24 |Q| of Q. So when q is farther
+// than 2^-20 |q| from every half-integer, rint(q) == rint(RN(Q)); for the
+// values that are not (rare) the correctly rounded division decides, behind
+// a wave-uniform branch. Same codes as quant_code for every input.
+__device__ __forceinline__ void quant_codes8(const float (&v)[8], GroupMeta m, int bits, uint32_t (&code)[8]) {
+#pragma clang fp contract(off)
+    const float levels = static_cast<float>((1 << bits) - 1);
+    const float inv = __builtin_amdgcn_rcpf(m.scale);
+    const bool bad = !(inv >= 1.17549435e-38f && inv <= 3.0e38f);   // a reciprocal out of the normal range
+    float r[8];
+    bool near[8];
+    bool any = bad;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float q = __fmul_rn(__fsub_rn(v[e], m.lo), inv);
+        r[e] = rintf(q);
+        near[e] = bad || fmaf(fabsf(q), 9.5367431640625e-07f, fabsf(__fsub_rn(q, r[e]))) >= 0.5f;   // 2^-20
+        any = any || near[e];
+    }
+    if (__any(any)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (near[e]) r[e] = rintf(__fdiv_rn(__fsub_rn(v[e], m.lo), m.scale));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = static_cast<uint32_t>(fminf(fmaxf(r[e], 0.0f), levels));
+}
+
 __device__ __forceinline__ float dequant(int code, GroupMeta m) {
     // the empty asm hides the product from the optimizer so it cannot be
     // contracted into an FMA: the reference rounds the product, then the sum

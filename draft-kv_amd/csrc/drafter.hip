@@ -8,6 +8,7 @@
 // on slots). Eviction and truncation keep the run dense by moving surviving
 // rows from the tail into the holes ("eviction compaction").
 #include <climits>
+#include <type_traits>
 
 #include "mirror_layout.h"
 
@@ -644,9 +645,12 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_kernel(RebuildArgs a) {
     }
 }
 
-// Rebuild, one block per (page, head, sequence x changed layer), head_dim <= 128:
+// Rebuild, one block per few pages of a (head, sequence x changed layer)
+// segment, head_dim <= 128. A block walks its pages with the next page's
+// source rows in flight while the current page is quantized:
 //   1. the page's kept rows of K and V (bf16/f32, from the paged full cache)
-//      are staged in LDS as float32 with coalesced loads;
+//      arrive in registers (coalesced loads, issued one page ahead) and are
+//      staged in LDS as float32;
 //   2. every lane quantizes 8 channels of one row (group min/max over the
 //      group's lanes, zero padding of a short last group included), writes K
 //      code words and the (scale, lo) pairs, and leaves V codes in LDS;
@@ -660,8 +664,98 @@ constexpr int RB_ROW = RB_MAXD + 4;
 struct RebuildSmem {
     float x[2][PAGE][RB_ROW];
     uint8_t vcode[PAGE][RB_MAXD];
+    int32_t blk[2][PAGE], off[2][PAGE];   // source block and slot of each row (two pages)
 };
 
+// The raw source words of one page held by a thread: K octets (8 channels of
+// a row) and V elements (one channel of a row), as loaded.
+template <bool BF>
+struct RawPage {
+    static constexpr int KU = PAGE * (RB_MAXD / 8) / BLK;   // K octets per thread
+    static constexpr int VU = PAGE * RB_MAXD / BLK;         // V elements per thread
+    using KWord = typename std::conditional<BF, uint4, float4>::type;
+    KWord k[KU][BF ? 1 : 2];
+    typename std::conditional<BF, uint16_t, float>::type v[VU];
+};
+
+template <bool BF>
+__device__ __forceinline__ void load_raw(RawPage<BF>& r, const dkv_paged_t& f, int h, int D, int rows,
+                                         const int32_t* sblk, const int32_t* soff) {
+    using R = RawPage<BF>;
+    const int64_t bel = paged_block_elems(f);
+    const int64_t vb = (int64_t)f.n_kv_heads * f.block_size * D;
+#pragma unroll
+    for (int x = 0; x < R::KU; ++x) {
+        const int u = threadIdx.x + x * BLK;
+        const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+        if (u < PAGE * (D / 8) && i < rows) {
+            const int64_t o = (int64_t)sblk[i] * bel + ((int64_t)h * f.block_size + soff[i]) * D + c8;
+            if constexpr (BF) {
+                r.k[x][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.pool) + o);
+            } else {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(f.pool) + o);
+                r.k[x][0] = src[0];
+                r.k[x][1] = src[1];
+            }
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < R::VU; ++x) {
+        const int u = threadIdx.x + x * BLK;
+        const int d = u / PAGE, i = u % PAGE;
+        if (u < PAGE * D && i < rows) {
+            const int64_t o = (int64_t)sblk[i] * bel + vb + ((int64_t)h * D + d) * f.block_size + soff[i];
+            if constexpr (BF) r.v[x] = static_cast<const uint16_t*>(f.pool)[o];
+            else r.v[x] = static_cast<const float*>(f.pool)[o];
+        }
+    }
+}
+
+template <bool BF>
+__device__ __forceinline__ void stage_raw(const RawPage<BF>& r, RebuildSmem& sm, int D, int rows) {
+    using R = RawPage<BF>;
+#pragma unroll
+    for (int x = 0; x < R::KU; ++x) {
+        const int u = threadIdx.x + x * BLK;
+        if (u < PAGE * (D / 8)) {
+            const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+            float kv[8];
+            if (i < rows) {
+                if constexpr (BF) {
+                    const uint32_t ww[4] = {r.k[x][0].x, r.k[x][0].y, r.k[x][0].z, r.k[x][0].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kv[2 * e] = bf16_to_f32(ww[e] & 0xffffu);
+                        kv[2 * e + 1] = bf16_to_f32(ww[e] >> 16);
+                    }
+                } else {
+                    kv[0] = r.k[x][0].x; kv[1] = r.k[x][0].y; kv[2] = r.k[x][0].z; kv[3] = r.k[x][0].w;
+                    kv[4] = r.k[x][1].x; kv[5] = r.k[x][1].y; kv[6] = r.k[x][1].z; kv[7] = r.k[x][1].w;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kv[e] = 0.0f;
+            }
+            *reinterpret_cast<float4*>(&sm.x[0][i][c8]) = make_float4(kv[0], kv[1], kv[2], kv[3]);
+            *reinterpret_cast<float4*>(&sm.x[0][i][c8 + 4]) = make_float4(kv[4], kv[5], kv[6], kv[7]);
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < R::VU; ++x) {
+        const int u = threadIdx.x + x * BLK;
+        if (u < PAGE * D) {
+            const int i = u % PAGE;
+            float v = 0.0f;
+            if (i < rows) {
+                if constexpr (BF) v = bf16_to_f32(r.v[x]);
+                else v = r.v[x];
+            }
+            sm.x[1][i][u / PAGE] = v;
+        }
+    }
+}
+
+template <bool BF>
 __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a) {
     const int h = blockIdx.y;
     const int s = blockIdx.z % a.m.batch, L = a.layers[blockIdx.z / a.m.batch];
@@ -682,184 +776,331 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
     kept = min(kept, m.cap);
     if (blockIdx.x == 0 && h == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
     __shared__ RebuildSmem sm;
-    __shared__ int32_t sblk[PAGE], soff[PAGE];   // source block and slot of each row of the page
     const PageFmt pf = page_fmt(cfg, D);
     auto pos_of = [&](int r) { return r < sink ? r : n - (kept - sink) + (r - sink); };
-    const int64_t bel = paged_block_elems(f);
-    const int64_t vb = (int64_t)f.n_kv_heads * f.block_size * D;
-    // the grid covers a few pages per segment; a block walks its segment's
-    // pages while they hold rows
-    for (int page = blockIdx.x; page * PAGE < kept; page += gridDim.x) {
-    const int r0 = page * PAGE;
-    const int rows = min(PAGE, kept - r0);
-    uint8_t* pg = page_ptr(m, s, L, h, page);
-    __syncthreads();   // the previous page is out of LDS
-    if (threadIdx.x < PAGE) {
-        const int i = threadIdx.x;
-        int32_t blk = 0, off = 0;
-        if (i < rows) {
-            const int p = pos_of(r0 + i);
-            blk = paged_block(f, s, L, p);
-            off = p % f.block_size;
+    // source block and slot of the rows of page pg, into table b (threads < PAGE)
+    auto lookup = [&](int pg, int b) {
+        if (threadIdx.x < PAGE) {
+            const int i = threadIdx.x, r = pg * PAGE + i;
+            int32_t blk = 0, off = 0;
+            if (r < kept) {
+                const int p = pos_of(r);
+                blk = paged_block(f, s, L, p);
+                off = p % f.block_size;
+            }
+            sm.blk[b][i] = blk;
+            sm.off[b][i] = off;
         }
-        sblk[i] = blk;
-        soff[i] = off;
-    }
+    };
+    const int step = gridDim.x;
+    int page = blockIdx.x;
+    if (page * PAGE >= kept) return;
+    RawPage<BF> raw;
+    lookup(page, 0);
     __syncthreads();
+    load_raw<BF>(raw, f, h, D, min(PAGE, kept - page * PAGE), sm.blk[0], sm.off[0]);
+    for (int it = 0; page * PAGE < kept; page += step, ++it) {
+        const int r0 = page * PAGE;
+        const int rows = min(PAGE, kept - r0);
+        const int nxt = page + step;
+        const bool more = nxt * PAGE < kept;
+        uint8_t* pg = page_ptr(m, s, L, h, page);
+        __syncthreads();   // the previous page's quantize and packing are done with LDS
+        stage_raw<BF>(raw, sm, D, rows);
+        if (more) lookup(nxt, (it + 1) & 1);
+        __syncthreads();
+        // the next page's rows go out now and arrive during this page's work
+        if (more) load_raw<BF>(raw, f, h, D, min(PAGE, kept - nxt * PAGE), sm.blk[(it + 1) & 1], sm.off[(it + 1) & 1]);
 
-    // ---- 1. stage K (rows contiguous in the block) and V (rows contiguous per
-    // channel); every load of a thread is issued before the LDS stores
-    {
-        constexpr int KU = PAGE * (RB_MAXD / 8) / BLK;   // K octets per thread
-        float kv[KU][8];
+        // ---- 2. quantize: lane = (tensor, row, octet); a row owns U2 lanes (power of two)
+        const int gl = pf.cb == 32 ? 1 : pf.group / 8;         // lanes per group
+        const int U = pf.cb == 32 ? D / 8 : pf.NG * gl;          // octets that belong to a group
+        int U2 = 1;
+        while (U2 < U) U2 <<= 1;
+        for (int u = threadIdx.x; u < 2 * PAGE * U2; u += BLK) {
+            const int t = u / (PAGE * U2), rem = u % (PAGE * U2);
+            const int i = rem / U2, oct = rem % U2, d0 = 8 * oct;
+            const bool live = i < rows;
+            float v[8];
+            if (d0 + 8 <= D) {
+                const float4 a0 = *reinterpret_cast<const float4*>(&sm.x[t][i][d0]);
+                const float4 a1 = *reinterpret_cast<const float4*>(&sm.x[t][i][d0 + 4]);
+                v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+                v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+            } else {
 #pragma unroll
-        for (int x = 0; x < KU; ++x) {
-            const int u = threadIdx.x + x * BLK;
-            const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+                for (int e = 0; e < 8; ++e) v[e] = (d0 + e < D) ? sm.x[t][i][d0 + e] : 0.0f;
+            }
+            if (pf.cb == 32) {
+                if (live && d0 < D) {
+                    float* dst = reinterpret_cast<float*>(pg + (t ? pf.vc : pf.kc)) + (int64_t)i * D + d0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kv[x][e] = 0.0f;
-            if (u < PAGE * (D / 8) && i < rows) {
-                const int64_t o = (int64_t)sblk[i] * bel + ((int64_t)h * f.block_size + soff[i]) * D + c8;
-                if (f.dtype == DKV_BF16) {
-                    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.pool) + o);
-                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+                    for (int e = 0; e < 8; ++e) dst[e] = v[e];
+                }
+                continue;
+            }
+            float mn = INFINITY, mx = -INFINITY;
+            if (oct < U) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kv[x][2 * e] = bf16_to_f32(ww[e] & 0xffffu);
-                        kv[x][2 * e + 1] = bf16_to_f32(ww[e] >> 16);
-                    }
-                } else {
-                    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(f.pool) + o);
-                    const float4 x0 = src[0], x1 = src[1];
-                    kv[x][0] = x0.x; kv[x][1] = x0.y; kv[x][2] = x0.z; kv[x][3] = x0.w;
-                    kv[x][4] = x1.x; kv[x][5] = x1.y; kv[x][6] = x1.z; kv[x][7] = x1.w;
+                for (int e = 0; e < 8; ++e) {
+                    mn = fminf(mn, v[e]);
+                    mx = fmaxf(mx, v[e]);
                 }
             }
-        }
-        constexpr int VU = PAGE * RB_MAXD / BLK;   // V elements per thread
-        float vv[VU];
+            for (int o = 1; o < gl; o <<= 1) {
+                mn = fminf(mn, __shfl_xor(mn, o));
+                mx = fmaxf(mx, __shfl_xor(mx, o));
+            }
+            const GroupMeta gm = group_meta(mn, mx, cfg.bits, pf.meta_f16);
+            uint32_t code[8];
+            quant_codes8(v, gm, cfg.bits, code);
+            if (oct >= U || d0 >= D) continue;
+            const bool first = d0 % pf.group == 0;
+            if (t == 0) {
+                if (!live) continue;
+                uint32_t* sec = reinterpret_cast<uint32_t*>(pg + pf.kc);
+                if (pf.cb == 4) {
+                    uint32_t w = 0;
 #pragma unroll
-        for (int x = 0; x < VU; ++x) {
-            const int u = threadIdx.x + x * BLK;
-            const int d = u / PAGE, i = u % PAGE;
-            vv[x] = 0.0f;
-            if (u < PAGE * D && i < rows)
-                vv[x] = load_elem(f.pool, (int64_t)sblk[i] * bel + vb + ((int64_t)h * D + d) * f.block_size + soff[i],
-                                  f.dtype);
-        }
+                    for (int e = 0; e < 8; ++e) w |= static_cast<uint32_t>(code[e]) << code_shift(4, e);
+                    sec[((int64_t)i * D + d0) / 8] = w;
+                } else {
+                    uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-        for (int x = 0; x < KU; ++x) {
-            const int u = threadIdx.x + x * BLK;
-            if (u < PAGE * (D / 8)) {
-                const int i = u / (D / 8), c8 = (u % (D / 8)) * 8;
+                    for (int e = 0; e < 4; ++e) {
+                        w0 |= static_cast<uint32_t>(code[e]) << code_shift(8, e);
+                        w1 |= static_cast<uint32_t>(code[4 + e]) << code_shift(8, e);
+                    }
+                    sec[((int64_t)i * D + d0) / 4] = w0;
+                    sec[((int64_t)i * D + d0) / 4 + 1] = w1;
+                }
+                if (first) write_meta(pg + k_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
+            } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sm.x[0][i][c8 + e] = kv[x][e];
+                for (int e = 0; e < 8; ++e)
+                    if (d0 + e < D) sm.vcode[i][d0 + e] = static_cast<uint8_t>(code[e]);
+                if (live && first) write_meta(pg + v_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
             }
         }
-#pragma unroll
-        for (int x = 0; x < VU; ++x) {
-            const int u = threadIdx.x + x * BLK;
-            if (u < PAGE * D) sm.x[1][u % PAGE][u / PAGE] = vv[x];
+        if (h == 0) {
+            int32_t* pos = m.pos + row_index(m, s, L);
+            double* score = m.score + row_index(m, s, L);
+            for (int i = threadIdx.x; i < rows; i += BLK) {
+                pos[r0 + i] = pos_of(r0 + i);
+                score[r0 + i] = 0.0;
+            }
+        }
+        if (pf.cb == 32) continue;
+        __syncthreads();
+
+        // ---- 3. V code words: word ((a*4 + j)*NDT + t) holds channel d = 16t + a of
+        // the rows (j, e) = {4j..4j+3, 16+4j..16+4j+3}; bytes: two words per (a, j, t)
+        uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
+        const int per = pf.cb == 4 ? 8 : 4;                     // rows per word
+        const int n_words = 16 * 4 * pf.NDT * (8 / per);
+        for (int u = threadIdx.x; u < n_words; u += BLK) {
+            const int half = pf.cb == 4 ? 0 : u % 2;
+            const int base = pf.cb == 4 ? u : u / 2;
+            const int t = base % pf.NDT, aj = base / pf.NDT;
+            const int j = aj % 4, acol = aj / 4;
+            const int d = 16 * t + acol;
+            if (d >= D) continue;
+            uint32_t w = 0;
+            for (int q = 0; q < per; ++q) {
+                const int e = half * 4 + q;
+                const int i = e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4);
+                const uint32_t code = sm.vcode[i][d];
+                w |= code << (pf.cb == 4 ? code_shift(4, e) : code_shift(8, q));
+            }
+            vsec[pf.cb == 4 ? base : base * 2 + half] = w;
         }
     }
-    __syncthreads();
+}
 
-    // ---- 2. quantize: lane = (tensor, row, octet); a row owns U2 lanes (power of two)
-    const int gl = pf.cb == 32 ? 1 : pf.group / 8;         // lanes per group
-    const int U = pf.cb == 32 ? D / 8 : pf.NG * gl;          // octets that belong to a group
-    int U2 = 1;
-    while (U2 < U) U2 <<= 1;
-    for (int u = threadIdx.x; u < 2 * PAGE * U2; u += BLK) {
-        const int t = u / (PAGE * U2), rem = u % (PAGE * U2);
-        const int i = rem / U2, oct = rem % U2, d0 = 8 * oct;
-        const bool live = i < rows;
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (d0 + e < D) ? sm.x[t][i][d0 + e] : 0.0f;
-        if (pf.cb == 32) {
-            if (live && d0 < D) {
-                float* dst = reinterpret_cast<float*>(pg + (t ? pf.vc : pf.kc)) + (int64_t)i * D + d0;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dst[e] = v[e];
+// ---- the common shape: bf16 source in 16-token blocks, head_dim 128, 4- or
+// 8-bit codes, group G. Same output as drafter_rebuild_page_kernel, with the
+// work laid out at compile time: thread tid quantizes octet tid % 16 (8
+// channels) of rows tid / 16 and tid / 16 + 16 of K and of V; its V loads are
+// one channel of one row each (channels tid / 32 + 8x), so all 16 share one
+// base address and differ by immediate offsets. V codes are staged by
+// channel (vt[d][row]), so a V code word is two 4-byte LDS reads.
+constexpr int RF_VT = PAGE + 4;   // bytes per channel of staged V codes
+struct RebuildFastSmem {
+    float x[2][PAGE][RB_ROW];
+    uint8_t vt[RB_MAXD][RF_VT];
+    int64_t kb[2][PAGE], vb[2][PAGE];   // element offsets of each row's K and V channel 0 (two pages)
+};
+
+template <int CB, int G, int MF>
+__global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a) {
+    constexpr int D = 128, BS = 16, GL = G / 8, NG = D / G;
+    const int h = blockIdx.y;
+    const int s = blockIdx.z % a.m.batch, L = a.layers[blockIdx.z / a.m.batch];
+    const dkv_drafter_t& m = a.m;
+    const dkv_paged_t& f = a.full;
+    const dkv_qcfg_t cfg = a.cfgs[L];
+    const int n = a.len[s];
+    const int B = a.budget[L * m.batch + s];
+    int kept, sink;
+    if (n <= B || cfg.recent == 0) {
+        kept = n;
+        sink = n;
+    } else {
+        kept = B;
+        sink = min(cfg.sink, n);
+    }
+    kept = min(kept, m.cap);
+    if (blockIdx.x == 0 && h == 0 && threadIdx.x == 0) m.n_rows[(int64_t)s * m.n_layers + L] = kept;
+    __shared__ RebuildFastSmem sm;
+    const PageFmt pf = page_fmt(cfg, D);   // container CB: 4 bits for 2-4-bit codes, bytes for 8
+    const int bits = cfg.bits;
+    const uint16_t* pool = static_cast<const uint16_t*>(f.pool);
+    const int64_t bel = paged_block_elems(f);
+    auto pos_of = [&](int r) { return r < sink ? r : n - (kept - sink) + (r - sink); };
+    auto lookup = [&](int pg, int b) {
+        if (threadIdx.x < PAGE) {
+            const int i = threadIdx.x, r = pg * PAGE + i;
+            int64_t kb = 0, vb = 0;
+            if (r < kept) {
+                const int p = pos_of(r);
+                const int64_t blk = paged_block(f, s, L, p);
+                kb = blk * bel + ((int64_t)h * BS + p % BS) * D;
+                vb = blk * bel + (int64_t)f.n_kv_heads * BS * D + (int64_t)h * D * BS + p % BS;
             }
-            continue;
+            sm.kb[b][i] = kb;
+            sm.vb[b][i] = vb;
         }
-        float mn = INFINITY, mx = -INFINITY;
-        if (oct < U) {
+    };
+    const int tid = threadIdx.x, oct = tid % 16, kr = tid / 16;   // K: rows kr, kr + 16
+    const int vi = tid % PAGE, vd = tid / PAGE;                  // V: row vi, channels vd + 8x
+    uint4 rk[2];
+    uint16_t rv[16];
+    auto load = [&](int b, int rows) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
+        for (int x = 0; x < 2; ++x)
+            if (kr + 16 * x < rows) rk[x] = *reinterpret_cast<const uint4*>(pool + sm.kb[b][kr + 16 * x] + 8 * oct);
+        if (vi < rows) {
+            const uint16_t* p = pool + sm.vb[b][vi] + vd * BS;
+#pragma unroll
+            for (int x = 0; x < 16; ++x) rv[x] = p[8 * BS * x];
+        }
+    };
+    auto stage = [&](int rows) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int i = kr + 16 * x;
+            float kv[8];
+            const uint32_t ww[4] = {rk[x].x, rk[x].y, rk[x].z, rk[x].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kv[2 * e] = i < rows ? bf16_to_f32(ww[e] & 0xffffu) : 0.0f;
+                kv[2 * e + 1] = i < rows ? bf16_to_f32(ww[e] >> 16) : 0.0f;
+            }
+            *reinterpret_cast<float4*>(&sm.x[0][i][8 * oct]) = make_float4(kv[0], kv[1], kv[2], kv[3]);
+            *reinterpret_cast<float4*>(&sm.x[0][i][8 * oct + 4]) = make_float4(kv[4], kv[5], kv[6], kv[7]);
+        }
+#pragma unroll
+        for (int x = 0; x < 16; ++x) sm.x[1][vi][vd + 8 * x] = vi < rows ? bf16_to_f32(rv[x]) : 0.0f;
+    };
+
+    const int step = gridDim.x;
+    int page = blockIdx.x;
+    if (page * PAGE >= kept) return;
+    lookup(page, 0);
+    __syncthreads();
+    load(0, min(PAGE, kept - page * PAGE));
+    for (int it = 0; page * PAGE < kept; page += step, ++it) {
+        const int r0 = page * PAGE;
+        const int rows = min(PAGE, kept - r0);
+        const int nxt = page + step;
+        const bool more = nxt * PAGE < kept;
+        uint8_t* pg = page_ptr(m, s, L, h, page);
+        __syncthreads();   // the previous page's quantize and packing are done with LDS
+        stage(rows);
+        if (more) lookup(nxt, (it + 1) & 1);
+        __syncthreads();
+        if (more) load((it + 1) & 1, min(PAGE, kept - nxt * PAGE));   // lands during this page's work
+
+        // ---- quantize: items (tensor t, row i) = (0, kr), (0, kr+16), (1, kr), (1, kr+16), octet oct
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const int t = x >> 1, i = kr + 16 * (x & 1);
+            const float4 a0 = *reinterpret_cast<const float4*>(&sm.x[t][i][8 * oct]);
+            const float4 a1 = *reinterpret_cast<const float4*>(&sm.x[t][i][8 * oct + 4]);
+            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            float mn = v[0], mx = v[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) {
                 mn = fminf(mn, v[e]);
                 mx = fmaxf(mx, v[e]);
             }
-        }
-        for (int o = 1; o < gl; o <<= 1) {
-            mn = fminf(mn, __shfl_xor(mn, o));
-            mx = fmaxf(mx, __shfl_xor(mx, o));
-        }
-        const GroupMeta gm = group_meta(mn, mx, cfg.bits, pf.meta_f16);
-        int code[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = quant_code(v[e], gm, cfg.bits);
-        if (oct >= U || d0 >= D) continue;
-        const bool first = d0 % pf.group == 0;
-        if (t == 0) {
-            if (!live) continue;
-            uint32_t* sec = reinterpret_cast<uint32_t*>(pg + pf.kc);
-            if (pf.cb == 4) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) w |= static_cast<uint32_t>(code[e]) << code_shift(4, e);
-                sec[((int64_t)i * D + d0) / 8] = w;
-            } else {
-                uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    w0 |= static_cast<uint32_t>(code[e]) << code_shift(8, e);
-                    w1 |= static_cast<uint32_t>(code[4 + e]) << code_shift(8, e);
-                }
-                sec[((int64_t)i * D + d0) / 4] = w0;
-                sec[((int64_t)i * D + d0) / 4 + 1] = w1;
+            for (int o = 1; o < GL; o <<= 1) {
+                mn = fminf(mn, __shfl_xor(mn, o));
+                mx = fmaxf(mx, __shfl_xor(mx, o));
             }
-            if (first) write_meta(pg + k_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
-        } else {
+            const GroupMeta gm = group_meta(mn, mx, bits, MF);
+            uint32_t code[8];
+            quant_codes8(v, gm, bits, code);
+            const bool first = oct % GL == 0, live = i < rows;
+            if (t == 0) {
+                if (live) {
+                    uint32_t* sec = reinterpret_cast<uint32_t*>(pg + pf.kc);
+                    if (CB == 4) {
+                        uint32_t w = 0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (d0 + e < D) sm.vcode[i][d0 + e] = static_cast<uint8_t>(code[e]);
-            if (live && first) write_meta(pg + v_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
+                        for (int e = 0; e < 8; ++e) w |= code[e] << code_shift(4, e);
+                        sec[i * 16 + oct] = w;
+                    } else {
+                        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            w0 |= code[e] << code_shift(8, e);
+                            w1 |= code[4 + e] << code_shift(8, e);
+                        }
+                        *reinterpret_cast<uint2*>(sec + i * 32 + 2 * oct) = make_uint2(w0, w1);
+                    }
+                    if (first) write_meta(pg + k_meta_off(pf, i, oct / GL), gm, MF);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sm.vt[8 * oct + e][i] = static_cast<uint8_t>(code[e]);
+                if (live && first) write_meta(pg + v_meta_off(pf, i, oct / GL), gm, MF);
+            }
         }
-    }
-    if (h == 0) {
-        int32_t* pos = m.pos + row_index(m, s, L);
-        double* score = m.score + row_index(m, s, L);
-        for (int i = threadIdx.x; i < rows; i += BLK) {
-            pos[r0 + i] = pos_of(r0 + i);
-            score[r0 + i] = 0.0;
+        if (h == 0) {
+            int32_t* pos = m.pos + row_index(m, s, L);
+            double* score = m.score + row_index(m, s, L);
+            if (tid < rows) {
+                pos[r0 + tid] = pos_of(r0 + tid);
+                score[r0 + tid] = 0.0;
+            }
         }
-    }
-    if (pf.cb == 32) continue;
-    __syncthreads();
+        __syncthreads();
 
-    // ---- 3. V code words: word ((a*4 + j)*NDT + t) holds channel d = 16t + a of
-    // the rows (j, e) = {4j..4j+3, 16+4j..16+4j+3}; bytes: two words per (a, j, t)
-    uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
-    const int per = pf.cb == 4 ? 8 : 4;                     // rows per word
-    const int n_words = 16 * 4 * pf.NDT * (8 / per);
-    for (int u = threadIdx.x; u < n_words; u += BLK) {
-        const int half = pf.cb == 4 ? 0 : u % 2;
-        const int base = pf.cb == 4 ? u : u / 2;
-        const int t = base % pf.NDT, aj = base / pf.NDT;
-        const int j = aj % 4, acol = aj / 4;
-        const int d = 16 * t + acol;
-        if (d >= D) continue;
-        uint32_t w = 0;
-        for (int q = 0; q < per; ++q) {
-            const int e = half * 4 + q;
-            const int i = e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4);
-            const uint32_t code = sm.vcode[i][d];
-            w |= code << (pf.cb == 4 ? code_shift(4, e) : code_shift(8, q));
+        // ---- V code words: word (a*4 + j)*8 + t holds channel d = 16t + a of the
+        // rows {4j..4j+3} (k-slots 0..3) and {16+4j..16+4j+3} (k-slots 4..7)
+        uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+            const int w = tid + BLK * y;   // 512 (a, j, t) triples
+            const int t = w % 8, aj = w / 8, j = aj % 4, acol = aj / 4;
+            const int d = 16 * t + acol;
+            const uint32_t lo = *reinterpret_cast<const uint32_t*>(&sm.vt[d][4 * j]);        // rows 4j..4j+3
+            const uint32_t hi = *reinterpret_cast<const uint32_t*>(&sm.vt[d][16 + 4 * j]);   // rows 16+4j..
+            // byte k of lo / hi: the code of row 4j + k / 16 + 4j + k
+            auto byte = [](uint32_t w, int k) { return (w >> (8 * k)) & 0xFFu; };
+            if (CB == 4) {
+                // k-slot e (rows 4j+e, then 16+4j+e-4) at code_shift(4, e): even slots
+                // at 0, 4, 8, 12, odd ones at 16, 20, 24, 28
+                vsec[w] = byte(lo, 0) | (byte(lo, 2) << 4) | (byte(hi, 0) << 8) | (byte(hi, 2) << 12) |
+                          (byte(lo, 1) << 16) | (byte(lo, 3) << 20) | (byte(hi, 1) << 24) | (byte(hi, 3) << 28);
+            } else {
+                // slot q of each 4-row half at code_shift(8, q): q = 0, 2, 1, 3 in bytes 0..3
+                vsec[2 * w] = byte(lo, 0) | (byte(lo, 2) << 8) | (byte(lo, 1) << 16) | (byte(lo, 3) << 24);
+                vsec[2 * w + 1] = byte(hi, 0) | (byte(hi, 2) << 8) | (byte(hi, 1) << 16) | (byte(hi, 3) << 24);
+            }
         }
-        vsec[pf.cb == 4 ? base : base * 2 + half] = w;
-    }
     }
 }
 
@@ -1040,8 +1281,37 @@ extern "C" int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_
         // each walks its segment's pages while they hold rows
         const int segs = mirror->n_kv_heads * mirror->batch * n_changed;
         const int per_seg = std::min(mirror->cap / PAGE, std::max(1, (4096 + segs - 1) / segs));
-        hipLaunchKernelGGL(drafter_rebuild_page_kernel, dim3(per_seg, mirror->n_kv_heads, mirror->batch * n_changed),
-                           dim3(BLK), 0, as_stream(stream), a);
+        const dim3 grid(per_seg, mirror->n_kv_heads, mirror->batch * n_changed);
+        // the compile-time kernel when every changed layer has the common shape
+        bool fast = full->dtype == DKV_BF16 && full->block_size == 16 && mirror->head_dim == 128;
+        int key = -1;
+        for (int i = 0; i < n_changed && fast; ++i) {
+            const dkv_qcfg_t& c = cfgs[layers[i]];
+            const int k = (c.bits == 8 ? 8 : 0) | (c.group == 16 ? 0 : c.group == 32 ? 1 : c.group == 64 ? 2 : 3) << 1 |
+                          (c.meta_f16 ? 1 : 0);
+            fast = c.bits < 16 && (c.group == 16 || c.group == 32 || c.group == 64 || c.group == 128) &&
+                   (key < 0 || key == k);
+            key = k;
+        }
+        if (fast) {
+#define DKV_RBF(CB, G, MF) hipLaunchKernelGGL((drafter_rebuild_fast_kernel<CB, G, MF>), grid, dim3(BLK), 0, \
+                                              as_stream(stream), a)
+            switch (key) {
+                case 0: DKV_RBF(4, 16, 0); break;   case 1: DKV_RBF(4, 16, 1); break;
+                case 2: DKV_RBF(4, 32, 0); break;   case 3: DKV_RBF(4, 32, 1); break;
+                case 4: DKV_RBF(4, 64, 0); break;   case 5: DKV_RBF(4, 64, 1); break;
+                case 6: DKV_RBF(4, 128, 0); break;  case 7: DKV_RBF(4, 128, 1); break;
+                case 8: DKV_RBF(8, 16, 0); break;   case 9: DKV_RBF(8, 16, 1); break;
+                case 10: DKV_RBF(8, 32, 0); break;  case 11: DKV_RBF(8, 32, 1); break;
+                case 12: DKV_RBF(8, 64, 0); break;  case 13: DKV_RBF(8, 64, 1); break;
+                case 14: DKV_RBF(8, 128, 0); break; default: DKV_RBF(8, 128, 1); break;
+            }
+#undef DKV_RBF
+        } else if (full->dtype == DKV_BF16) {
+            hipLaunchKernelGGL(drafter_rebuild_page_kernel<true>, grid, dim3(BLK), 0, as_stream(stream), a);
+        } else {
+            hipLaunchKernelGGL(drafter_rebuild_page_kernel<false>, grid, dim3(BLK), 0, as_stream(stream), a);
+        }
     } else {
         hipLaunchKernelGGL(drafter_rebuild_kernel, dim3(mirror->cap / PAGE, mirror->batch, n_changed), dim3(BLK), 0,
                            as_stream(stream), a);
