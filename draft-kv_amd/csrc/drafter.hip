@@ -924,9 +924,10 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
 // one channel of one row each (channels tid / 32 + 8x), so all 16 share one
 // base address and differ by immediate offsets. V codes are staged by
 // channel (vt[d][row]), so a V code word is two 4-byte LDS reads.
-constexpr int RF_VT = PAGE + 4;   // bytes per channel of staged V codes
+constexpr int RF_VT = PAGE + 4;         // bytes per channel of staged V codes
+constexpr int RF_ROW = RB_MAXD + 8;     // bf16 per staged row (16-byte aligned rows)
 struct RebuildFastSmem {
-    float x[2][PAGE][RB_ROW];
+    uint16_t x[2][PAGE][RF_ROW];        // the page's K and V rows as loaded (bf16)
     uint8_t vt[RB_MAXD][RF_VT];
     int64_t kb[2][PAGE], vb[2][PAGE];   // element offsets of each row's K and V channel 0 (two pages)
 };
@@ -985,22 +986,15 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
             for (int x = 0; x < 16; ++x) rv[x] = p[8 * BS * x];
         }
     };
+    // rows past the page's live count stage as zeros (their codes are those of 0)
     auto stage = [&](int rows) {
 #pragma unroll
         for (int x = 0; x < 2; ++x) {
             const int i = kr + 16 * x;
-            float kv[8];
-            const uint32_t ww[4] = {rk[x].x, rk[x].y, rk[x].z, rk[x].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kv[2 * e] = i < rows ? bf16_to_f32(ww[e] & 0xffffu) : 0.0f;
-                kv[2 * e + 1] = i < rows ? bf16_to_f32(ww[e] >> 16) : 0.0f;
-            }
-            *reinterpret_cast<float4*>(&sm.x[0][i][8 * oct]) = make_float4(kv[0], kv[1], kv[2], kv[3]);
-            *reinterpret_cast<float4*>(&sm.x[0][i][8 * oct + 4]) = make_float4(kv[4], kv[5], kv[6], kv[7]);
+            *reinterpret_cast<uint4*>(&sm.x[0][i][8 * oct]) = i < rows ? rk[x] : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
-        for (int x = 0; x < 16; ++x) sm.x[1][vi][vd + 8 * x] = vi < rows ? bf16_to_f32(rv[x]) : 0.0f;
+        for (int x = 0; x < 16; ++x) sm.x[1][vi][vd + 8 * x] = vi < rows ? rv[x] : uint16_t(0);
     };
 
     const int step = gridDim.x;
@@ -1025,9 +1019,14 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
             const int t = x >> 1, i = kr + 16 * (x & 1);
-            const float4 a0 = *reinterpret_cast<const float4*>(&sm.x[t][i][8 * oct]);
-            const float4 a1 = *reinterpret_cast<const float4*>(&sm.x[t][i][8 * oct + 4]);
-            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const uint4 raw8 = *reinterpret_cast<const uint4*>(&sm.x[t][i][8 * oct]);
+            const uint32_t ww[4] = {raw8.x, raw8.y, raw8.z, raw8.w};
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = __uint_as_float(ww[e] << 16);
+                v[2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+            }
             float mn = v[0], mx = v[0];
 #pragma unroll
             for (int e = 1; e < 8; ++e) {
