@@ -19,6 +19,7 @@ namespace dkv {
 
 constexpr int VCH = 4096;
 constexpr int ABLK = 256;
+static_assert(VCH % ABLK == 0, "pick: every thread owns VCH / ABLK elements");
 
 struct ChunkStat {
     float mx;
@@ -39,93 +40,137 @@ __device__ __forceinline__ const float* row_ptr(const float* target, const float
     return draft + ((int64_t)s * gamma + (row - gamma - 1)) * vocab;
 }
 
+// One read of the chunk, held in registers: the block's max (first index on
+// ties), then the float64 sum of exp(x/T - max/T) (x/T as x * (1/T): a
+// normaliser needs no correctly rounded quotient).
 __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ target, const float* __restrict__ draft,
                                                      int gamma, int vocab, float T, int n_chunks,
                                                      ChunkStat* __restrict__ stats) {
+    constexpr int PER = VCH / ABLK;
     const int chunk = blockIdx.x, row = blockIdx.y, s = blockIdx.z;
-    const int n_rows = T > 0.0f ? 2 * gamma + 1 : gamma + 1;
+    const bool samp = T > 0.0f;
+    const int n_rows = samp ? 2 * gamma + 1 : gamma + 1;
     if (row >= n_rows) return;
     const float* x = row_ptr(target, draft, s, row, gamma, vocab);
     const int i0 = chunk * VCH, i1 = min(vocab, i0 + VCH);
     __shared__ float smx[ABLK / WAVE];
     __shared__ int sarg[ABLK / WAVE];
     __shared__ double ssum[ABLK / WAVE];
-    __shared__ float bmx;
+    float xv[PER];
     float mx = -INFINITY;
     int arg = INT_MAX;
-    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) {
-        const float v = x[i];
-        if (v > mx || (v == mx && i < arg)) { mx = v; arg = i; }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = i0 + threadIdx.x + k * ABLK;
+        xv[k] = i < i1 ? x[i] : -INFINITY;
     }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)   // a thread's indices rise with k: its first maximum is kept
+        if (xv[k] > mx) {
+            mx = xv[k];
+            arg = i0 + threadIdx.x + k * ABLK;
+        }
     for (int o = 32; o > 0; o >>= 1) {
         const float om = __shfl_xor(mx, o);
         const int oa = __shfl_xor(arg, o);
-        if (om > mx || (om == mx && oa < arg)) { mx = om; arg = oa; }
+        if (om > mx || (om == mx && oa < arg)) {
+            mx = om;
+            arg = oa;
+        }
     }
     const int w = threadIdx.x / WAVE;
-    if (threadIdx.x % WAVE == 0) { smx[w] = mx; sarg[w] = arg; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = smx[0];
-        int a = sarg[0];
-        for (int i = 1; i < ABLK / WAVE; ++i)
-            if (smx[i] > m || (smx[i] == m && sarg[i] < a)) { m = smx[i]; a = sarg[i]; }
-        bmx = m;
-        ChunkStat& cs = stats[((int64_t)s * (2 * gamma + 1) + row) * n_chunks + chunk];
-        cs.mx = m;
-        cs.arg = a;
-        cs.sum = 0.0;
+    if (threadIdx.x % WAVE == 0) {
+        smx[w] = mx;
+        sarg[w] = arg;
     }
     __syncthreads();
-    if (T <= 0.0f) return;
-    const double mT = (double)bmx / (double)T;
+    mx = smx[0];
+    arg = sarg[0];
+    for (int i = 1; i < ABLK / WAVE; ++i)
+        if (smx[i] > mx || (smx[i] == mx && sarg[i] < arg)) {
+            mx = smx[i];
+            arg = sarg[i];
+        }
     double sum = 0.0;
-    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) sum += exp((double)x[i] / (double)T - mT);
-    sum = wave_sum_d(sum);
-    if (threadIdx.x % WAVE == 0) ssum[w] = sum;
-    __syncthreads();
+    if (samp) {
+        const double iT = 1.0 / (double)T, mT = (double)mx * iT;
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+            if (xv[k] > -INFINITY) sum += exp((double)xv[k] * iT - mT);
+        sum = wave_sum_d(sum);
+        if (threadIdx.x % WAVE == 0) ssum[w] = sum;
+        __syncthreads();
+    }
     if (threadIdx.x == 0) {
         double t = 0.0;
-        for (int i = 0; i < ABLK / WAVE; ++i) t += ssum[i];
-        stats[((int64_t)s * (2 * gamma + 1) + row) * n_chunks + chunk].sum = t;
+        if (samp)
+            for (int i = 0; i < ABLK / WAVE; ++i) t += ssum[i];
+        ChunkStat& cs = stats[((int64_t)s * (2 * gamma + 1) + row) * n_chunks + chunk];
+        cs.mx = mx;
+        cs.arg = arg;
+        cs.sum = t;
     }
 }
 
 struct RowNorm {
     double m;   // max(x)/T
     double S;   // sum exp(x/T - m)
+    double iS;  // 1 / S
     int arg;
 };
 
-__device__ RowNorm merge_row(const ChunkStat* st, int n_chunks, float T) {
-    float mx = -INFINITY;
-    int arg = INT_MAX;
-    for (int c = 0; c < n_chunks; ++c)
-        if (st[c].mx > mx || (st[c].mx == mx && st[c].arg < arg)) { mx = st[c].mx; arg = st[c].arg; }
-    RowNorm r{0.0, 0.0, arg};
-    if (T > 0.0f) {
-        r.m = (double)mx / (double)T;
-        for (int c = 0; c < n_chunks; ++c) r.S += st[c].sum * exp((double)st[c].mx / (double)T - r.m);
-    }
-    return r;
-}
-
+// p(x) = exp(x/T - m) / S with x/T as x * (1/T) and the division by S as a
+// product with its reciprocal (each within an ulp of the quotient)
 __device__ __forceinline__ double prob(float x, const RowNorm& r, float T) {
-    return exp((double)x / (double)T - r.m) / r.S;
+    return exp((double)x * (1.0 / (double)T) - r.m) * r.iS;
 }
 
-__global__ void decide_kernel(const float* __restrict__ target, const float* __restrict__ draft,
-                              const int32_t* __restrict__ draft_tokens, int gamma, int vocab, float T,
-                              const double* __restrict__ u, int n_chunks, const ChunkStat* __restrict__ stats,
-                              RowNorm* __restrict__ norms, SeqState* __restrict__ state, int32_t* accepted,
-                              int32_t* next_token, int32_t* n_uniforms) {
-    const int s = blockIdx.x;
-    if (threadIdx.x != 0) return;
+// One wave per sequence: the lanes merge each row's chunk statistics, then
+// lane 0 runs the accept tests (a handful of reads) and picks the final
+// distribution.
+__global__ void __launch_bounds__(WAVE) decide_kernel(const float* __restrict__ target,
+                                                      const float* __restrict__ draft,
+                                                      const int32_t* __restrict__ draft_tokens, int gamma, int vocab,
+                                                      float T, const double* __restrict__ u, int n_chunks,
+                                                      const ChunkStat* __restrict__ stats,
+                                                      RowNorm* __restrict__ norms, SeqState* __restrict__ state,
+                                                      int32_t* accepted, int32_t* next_token,
+                                                      int32_t* n_uniforms) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    const bool samp = T > 0.0f;
     const int R = 2 * gamma + 1;
     const ChunkStat* st = stats + (int64_t)s * R * n_chunks;
-    const int n_rows = T > 0.0f ? R : gamma + 1;
+    const int n_rows = samp ? R : gamma + 1;
     RowNorm* nr = norms + (int64_t)s * R;
-    for (int r = 0; r < n_rows; ++r) nr[r] = merge_row(st + (int64_t)r * n_chunks, n_chunks, T);
+    for (int r = 0; r < n_rows; ++r) {
+        const ChunkStat* sr = st + (int64_t)r * n_chunks;
+        float mx = -INFINITY;
+        int arg = INT_MAX;
+        for (int c = lane; c < n_chunks; c += WAVE)
+            if (sr[c].mx > mx || (sr[c].mx == mx && sr[c].arg < arg)) {
+                mx = sr[c].mx;
+                arg = sr[c].arg;
+            }
+        for (int o = WAVE / 2; o > 0; o >>= 1) {
+            const float om = __shfl_xor(mx, o);
+            const int oa = __shfl_xor(arg, o);
+            if (om > mx || (om == mx && oa < arg)) {
+                mx = om;
+                arg = oa;
+            }
+        }
+        RowNorm rn{0.0, 0.0, 0.0, arg};
+        if (samp) {
+            const double iT = 1.0 / (double)T;
+            rn.m = (double)mx * iT;
+            double S = 0.0;
+            for (int c = lane; c < n_chunks; c += WAVE) S += sr[c].sum * exp((double)sr[c].mx * iT - rn.m);
+            rn.S = wave_sum_d(S);
+            rn.iS = 1.0 / rn.S;
+        }
+        if (lane == 0) nr[r] = rn;
+    }
+    if (lane != 0) return;
     int acc = 0, used = 0;
     const double* us = u + (int64_t)s * (gamma + 1);
     for (int i = 0; i < gamma; ++i) {
@@ -220,7 +265,7 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
         if (from_p) mode = 1;
         const RowNorm pn = nr[ss.row];
         auto chunk_mass = [&](int c) -> double {
-            return from_p ? pst[c].sum * exp((double)pst[c].mx / (double)T - pn.m) / pn.S : cs[c];
+            return from_p ? pst[c].sum * exp((double)pst[c].mx * (1.0 / (double)T) - pn.m) * pn.iS : cs[c];
         };
         if (from_p) {
             total = 0.0;
@@ -254,42 +299,49 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
     const int c = s_chunk;
     const int i0 = c * VCH, i1 = min(vocab, i0 + VCH);
     const double tgt = s_target;
-    // block-wide inclusive scan over the chunk, ABLK elements at a time
+    // Thread t owns PER consecutive elements of the chunk: per-thread masses,
+    // one block-wide exclusive scan of them, then the thread whose range
+    // crosses the target walks its own elements.
+    constexpr int PER = VCH / ABLK;
     __shared__ double wsum[ABLK / WAVE];
     __shared__ int found, last_pos;
-    __shared__ double run;
     if (threadIdx.x == 0) {
         found = INT_MAX;
         last_pos = -1;
-        run = s_before;
     }
-    __syncthreads();
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
-    for (int base = i0; base < i1; base += ABLK) {
-        const int i = base + threadIdx.x;
-        const double v = i < i1 ? final_mass(pr, qr, pn, qn, mode, i, T) : 0.0;
-        double x = v;
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const double y = __shfl_up(x, o);
-            if (lane >= o) x += y;
-        }
-        if (lane == WAVE - 1) wsum[w] = x;
-        __syncthreads();
-        double off = run;
-        for (int k = 0; k < w; ++k) off += wsum[k];
-        if (i < i1 && v > 0.0) {
-            if (off + x > tgt) atomicMin(&found, i);
-            atomicMax(&last_pos, i);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double t = run;
-            for (int k = 0; k < ABLK / WAVE; ++k) t += wsum[k];
-            run = t;
-        }
-        __syncthreads();
-        if (found != INT_MAX) break;
+    const int b0 = i0 + PER * threadIdx.x;
+    double v[PER];
+    double loc = 0.0;
+    int lastp = -1;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = b0 + k;
+        v[k] = i < i1 ? final_mass(pr, qr, pn, qn, mode, i, T) : 0.0;
+        loc += v[k];
+        if (v[k] > 0.0) lastp = i;
     }
+    double x = loc;   // inclusive scan within the wave
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const double y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    if (lane == WAVE - 1) wsum[w] = x;
+    __syncthreads();
+    double off = s_before + (x - loc);
+    for (int k = 0; k < w; ++k) off += wsum[k];
+    int hit = INT_MAX;
+    if (off + loc > tgt) {
+        double run = off;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            run += v[k];
+            if (hit == INT_MAX && v[k] > 0.0 && run > tgt) hit = b0 + k;
+        }
+    }
+    if (hit != INT_MAX) atomicMin(&found, hit);
+    if (lastp >= 0) atomicMax(&last_pos, lastp);
+    __syncthreads();
     if (threadIdx.x == 0) {
         // a draw that rounding pushes past the end of the cdf takes the last
         // index with positive mass (the reference's cdf ends at exactly 1)
@@ -336,7 +388,7 @@ extern "C" int dkv_accept(const float* target, const float* draft, const int32_t
                        temperature, nc, stats);
     int rc = check_launch("dkv_accept(stats)");
     if (rc) return rc;
-    hipLaunchKernelGGL(decide_kernel, dim3(batch), dim3(64), 0, st, target, draft, draft_tokens, gamma, vocab,
+    hipLaunchKernelGGL(decide_kernel, dim3(batch), dim3(WAVE), 0, st, target, draft, draft_tokens, gamma, vocab,
                        temperature, u, nc, stats, norms, state, accepted, next_token, n_uniforms);
     if ((rc = check_launch("dkv_accept(decide)"))) return rc;
     if (temperature <= 0.0f) return DKV_OK;
