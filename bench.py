@@ -22,7 +22,9 @@ mirror, under each arm) and ``cpu_baseline`` (the numpy oracle on a bounded
 sample of the same round).
 
 ``--workload kernels`` times the attention kernels alone at the same shape
-(drafter pass and 9-query verify pass over rotating layers) for profiling.
+(drafter pass and 9-query verify pass over rotating layers) for profiling;
+``--workload requant`` the mirror rebuild of an arm switch; ``--workload
+accept`` one verify decision over the batch.
 """
 
 from __future__ import annotations
@@ -52,7 +54,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--period", type=int, default=64)
     ap.add_argument("--baseline-steps", type=int, default=8)
-    ap.add_argument("--workload", choices=["e2e", "kernels", "copy"], default="e2e")
+    ap.add_argument("--workload", choices=["e2e", "kernels", "copy", "requant", "accept"], default="e2e")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--gamma", type=int, default=16)
@@ -621,6 +623,101 @@ def run_copy(args):
             "config": {"workload": "copy 1 GiB device to device", "bytes_read": n, "bytes_written": n}}
 
 
+def run_requant(args):
+    """Requantize alone (the mirror rebuild on an arm switch) at the
+    Llama-3-8B attention shape: every layer of a batch x ctx mirror rebuilt
+    from the bf16 full cache, alternating int8 group-64 keep 1.0 and
+    int{bits} group-{group} keep {keep} (fp16 scale/zero), each call timed
+    with HIP events on the launch stream. Algorithmic bytes: the kept rows'
+    bf16 K and V read, their codes and scale/zero pairs written, and 12 B of
+    position and score per kept row."""
+    import numpy as np
+    import torch
+    from draftkv import CompressedKVCache, CompressionConfig
+    from draftkv.compress import _budget
+    L, Hkv, D = args.layers, 8, 128
+    b, ctx = args.batch, args.ctx
+    log(f"synthetic full cache: batch {b}, ctx {ctx}, {L} layers")
+    full = shuffled_full_cache(L, Hkv, D, b, ctx, 16, torch.bfloat16)
+    arms = [CompressionConfig(8, 1.0, group=64, scale_fp16=True),
+            CompressionConfig(args.bits, args.keep, group=args.group, scale_fp16=True)]
+    comp = CompressedKVCache(L, arms[0], batch=b, cap=ctx + 64, reserve_cfgs=arms)
+    comp.sync_from(full, 0)
+    t = EventTimer(comp, "rebuild_layers")
+    for i in range(args.warmup):
+        comp.rebuild_layers(full, list(range(L)), [arms[(i + 1) % 2]] * L)
+    torch.cuda.synchronize()
+    t.on = True
+    tags = []
+    for i in range(2 * args.steps):
+        arm = arms[(args.warmup + i + 1) % 2]
+        comp.rebuild_layers(full, list(range(L)), [arm] * L)
+        tags.append(arm)
+    torch.cuda.synchronize()
+    t.restore()
+    n = full.lengths()
+    out_k = {}
+    for arm, ms in zip(tags, t.times_ms()):
+        kept = np.array([min(int(x), _budget(arm, int(x))) for x in n], np.float64)
+        ng = -(-D // arm.group)
+        per_row = Hkv * 2 * (D * 2 + D * arm.bits / 8 + ng * 4)
+        nbytes = L * float(kept.sum()) * (per_row + 12)
+        c = out_k.setdefault(f"{arm.label()} g{arm.group}", [0.0, 0.0, 0])
+        c[0] += nbytes
+        c[1] += ms * 1e3
+        c[2] += 1
+    kern = {k: {"us_per_call": v[1] / v[2], "bytes_per_call": v[0] / v[2], "GB/s": v[0] / (v[1] * 1e-6) / 1e9,
+                "calls": v[2]} for k, v in out_k.items()}
+    main = kern[f"{arms[1].label()} g{arms[1].group}"]
+    return {"metric": f"requantize (mirror rebuild of {L} layers) GB/s, b={b} ctx={ctx}", "value": main["GB/s"],
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": main["us_per_call"] / 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16->int", "data": "synthetic",
+            "config": {"workload": f"requantize {L} layers, batch {b}, ctx {ctx}, alternating arms"},
+            "roofline": {"bound": "hbm", "achieved": main["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": main["GB/s"] / HBM_PEAK_GBS, "traffic": None},
+            "kernels": kern, "cpu_baseline": None}
+
+
+def run_accept(args):
+    """Acceptance alone: one verify decision over the batch (target logits
+    [batch, gamma+1, vocab] and draft logits [batch, gamma, vocab], float32
+    N(0, 2^2), temperature rejection sampling), timed per call with HIP
+    events. Algorithmic bytes: every logit read once."""
+    import torch
+    from draftkv import ops
+    b, g, V = args.batch, args.gamma, 128256
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    target = 2.0 * torch.randn((b, g + 1, V), generator=gen, device=dev)
+    draft = 2.0 * torch.randn((b, g, V), generator=gen, device=dev)
+    tok = torch.randint(0, V, (b, g), generator=gen, device=dev, dtype=torch.int32)
+    u = torch.rand((b, g + 1), generator=gen, device=dev, dtype=torch.float64)
+    T = args.temperature
+    for _ in range(args.warmup):
+        ops.accept(target, draft, tok, T, u)
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(args.steps):
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        ops.accept(target, draft, tok, T, u)
+        e_ev.record()
+        evs.append((s_ev, e_ev))
+    torch.cuda.synchronize()
+    us = 1e3 * sum(a.elapsed_time(c) for a, c in evs) / len(evs)
+    nbytes = 4.0 * b * (2 * g + 1) * V
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"metric": f"accept (verify decision) GB/s, b={b} gamma={g} vocab={V}", "value": gbs, "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": us / 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32/f64",
+            "data": "synthetic", "config": {"workload": f"accept b={b} gamma={g} T={T}"},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_call": nbytes, "us_per_call": us},
+            "cpu_baseline": None}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -631,7 +728,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    out = {"e2e": run_e2e, "kernels": run_kernels, "copy": run_copy}[args.workload](args)
+    out = {"e2e": run_e2e, "kernels": run_kernels, "copy": run_copy, "requant": run_requant,
+           "accept": run_accept}[args.workload](args)
     print(json.dumps(out), flush=True)
 
 
