@@ -180,13 +180,24 @@ class EventTimer:
 
 
 # ---------------------------------------------------------------- CPU baseline
+def splitk_bytes(rows_per_seq, n_kv_heads, d, bits, group, q_heads):
+    """Algorithmic bytes of the drafter's split-K kernel: codes + fp16
+    scale/zero of every kept row and KV head, and the fp32 query (the mass
+    and the output belong to the two passes after it)."""
+    per_row = n_kv_heads * 2 * (d * bits / 8 + 4 * math.ceil(d / group))
+    return float(sum(rows_per_seq)) * per_row + len(rows_per_seq) * q_heads * d * 4
+
+
 def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
-    """Drafter attention calls timed with HIP events on the launch stream, on
-    the decode run's own mirror rebuilt under each arm in turn: every layer,
-    ``reps`` times, with N(0,1) queries and the attention mass on (as in the
-    draft steps). Returns {arm: [algorithmic bytes, us, calls]}."""
+    """Drafter attention timed on the decode run's own mirror, rebuilt under
+    each arm in turn: every layer, ``reps`` times, with N(0,1) queries and the
+    attention mass on (as in the draft steps). HIP events on the launch
+    stream time each whole call and, through the library's timing hook, its
+    split-K kernel alone. Returns {arm: {"call": [bytes, us, calls],
+    "splitk": [bytes, us, calls]}}."""
     import numpy as np
     import torch
+    from draftkv import ops
     L, b = comp.n_layers, comp.batch
     g = torch.Generator(device=comp.device)
     g.manual_seed(7)
@@ -197,6 +208,14 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
             comp.rebuild_layers(full, list(range(L)), [arm] * L)
         comp.attend(0, q)
         torch.cuda.synchronize()
+        rows = comp.rows()
+        cb = kb = 0.0
+        for layer in range(L):
+            r = rows[:, layer].astype(np.float64)
+            cb += reps * drafter_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
+            kb += reps * splitk_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
+        # whole calls back to back, then the split-K kernel of each call (its
+        # event pair read after the call, so those calls do not overlap)
         t = EventTimer(comp, "attend")
         t.on = True
         for _ in range(reps):
@@ -204,10 +223,16 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
                 comp.attend(layer, q)
         torch.cuda.synchronize()
         t.restore()
-        rows = comp.rows()
-        nbytes = reps * sum(drafter_bytes(rows[:, layer].astype(np.float64), comp.n_kv_heads, comp.d_head,
-                                          arm.bits, arm.group, n_q_heads) for layer in range(L))
-        out[arm] = [nbytes, sum(t.times_ms()) * 1e3, len(t.pairs)]
+        ops.drafter_kernel_timing(True)
+        k_ms = []
+        for _ in range(reps):
+            for layer in range(L):
+                comp.attend(layer, q)
+                k_ms.append(ops.drafter_kernel_last_ms())
+        ops.drafter_kernel_timing(False)
+        torch.cuda.synchronize()
+        out[arm] = {"call": [cb, sum(t.times_ms()) * 1e3, len(t.pairs)],
+                    "splitk": [kb, sum(k_ms) * 1e3, len(k_ms)]}
     return out
 
 
@@ -424,25 +449,26 @@ def run_e2e(args):
             st[0] += x.accepted
             st[1] += x.gamma
             st[2] += 1
-    # drafter attention: bytes of each timed call from the rows the mirror held
-    arm_calls = {}
+    # drafter attention during the rounds (eager steps only): bytes of each
+    # timed call from the rows the mirror held
+    live_calls = {}
     if live:
         for (s_ev, e_ev), (cfg, seen) in zip(t_draft.pairs, t_draft.tags):
             rows = [min(int(n), _budget(cfg, int(n))) for n in seen]
             nbytes = drafter_bytes(rows, Hkv, D, cfg.bits, cfg.group, Hq)
-            c = arm_calls.setdefault(cfg, [0.0, 0.0, 0])
+            c = live_calls.setdefault(cfg, [0.0, 0.0, 0])
             c[0] += nbytes
             c[1] += s_ev.elapsed_time(e_ev) * 1e3
             c[2] += 1
-    else:
-        log("drafter attention timed per call on the run's mirror, under each arm")
-        arm_calls = time_drafter(comp, full, arms, Hq)
+    log("drafter attention and its split-K kernel timed on the run's mirror, under each arm")
+    timed = time_drafter(comp, full, arms, Hq)
     main_arm = arms[1]
-    mb, mus, mn = arm_calls.get(main_arm, [float("nan"), float("nan"), 0])
-    achieved = mb / (mus * 1e-6) / 1e9 if mn else float("nan")
+    mb, mus, mn = timed[main_arm]["call"]
+    kbytes, kus, kn = timed[main_arm]["splitk"]
+    achieved = kbytes / (kus * 1e-6) / 1e9
     traffic = None
     if (b, ctx, main_arm.bits, main_arm.group, main_arm.keep_frac) == (32, 32768, 4, 32, 0.25):
-        traffic = measured_traffic("drafter_attention_int4_g32_keep0.25_b32_ctx32k")
+        traffic = measured_traffic("drafter_splitk_int4_g32_keep0.25_b32_ctx32k")
     v_us = t_ver.mean_us()
     v_bytes = verify_bytes(full.lengths().astype(np.float64) + gmax / 2, Hkv, D, gmax + 1, Hq)
     # plain full-KV decoding on the same cache (one token per sequence per step)
@@ -510,14 +536,22 @@ def run_e2e(args):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": "profiles/attention_hbm_traffic_b32_ctx32k.md (FETCH_SIZE x 2.0 + "
                                        "WRITE_SIZE, copy-kernel calibrated)" if traffic else None,
-                     "kernel": f"drafter attention, {main_arm.label()} g{main_arm.group} (dkv_drafter_attention: "
-                               "split-K pass + combine + mass)",
-                     "bytes_per_call": mb / max(mn, 1), "us_per_call": mus / max(mn, 1), "calls": mn},
+                     "kernel": f"drafter attention split-K kernel, {main_arm.label()} g{main_arm.group} "
+                               "(the dominant kernel of dkv_drafter_attention)",
+                     "bytes_per_launch": kbytes / max(kn, 1), "us_per_launch": kus / max(kn, 1), "launches": kn,
+                     "call": {"what": "split-K + combine + mass", "bytes_per_call": mb / max(mn, 1),
+                              "us_per_call": mus / max(mn, 1), "GB/s": mb / (mus * 1e-6) / 1e9,
+                              "frac": mb / (mus * 1e-6) / 1e9 / HBM_PEAK_GBS, "calls": mn}},
         "kernels": {"verify_attention": {"us_per_call": v_us, "bytes_per_call": v_bytes,
                                          "GB/s": v_bytes / (v_us * 1e-6) / 1e9, "calls": len(t_ver.pairs)}},
     }
-    for cfg, (nb, us, n) in arm_calls.items():
+    for cfg, d in timed.items():
+        (nb, us, n), (kb_, kus_, kn_) = d["call"], d["splitk"]
         out["kernels"][f"drafter_attention {cfg.label()} g{cfg.group}"] = {
+            "us_per_call": us / n, "bytes_per_call": nb / n, "GB/s": nb / (us * 1e-6) / 1e9, "calls": n,
+            "splitk_us": kus_ / kn_, "splitk_GB/s": kb_ / (kus_ * 1e-6) / 1e9}
+    for cfg, (nb, us, n) in live_calls.items():
+        out["kernels"][f"drafter_attention {cfg.label()} g{cfg.group} (live, in the rounds)"] = {
             "us_per_call": us / n, "bytes_per_call": nb / n, "GB/s": nb / (us * 1e-6) / 1e9, "calls": n}
     log(f"{emitted} tokens in {dt:.3f} s ({value:.1f} tok/s); full-KV decode {base_tps:.1f} tok/s; "
         f"acceptance {alpha}")

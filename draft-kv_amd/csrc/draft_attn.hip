@@ -908,6 +908,28 @@ static DraftWork draft_work(const dkv_drafter_t& m, int n_q_heads, int want_mass
     return w;
 }
 
+// Measurement hook: when on, dkv_drafter_attention records a pair of HIP
+// events around its split-K kernel on the launch stream.
+static bool g_time_splitk = false;
+static hipEvent_t g_splitk_ev[2] = {nullptr, nullptr};
+
+extern "C" int dkv_drafter_kernel_timing(int32_t on) {
+    if (on && !g_splitk_ev[0]) {
+        if (hipEventCreate(&g_splitk_ev[0]) != hipSuccess || hipEventCreate(&g_splitk_ev[1]) != hipSuccess)
+            return fail(DKV_ELAUNCH, "dkv_drafter_kernel_timing: cannot create events");
+    }
+    g_time_splitk = on != 0;
+    return DKV_OK;
+}
+
+extern "C" float dkv_drafter_kernel_last_ms(void) {
+    float ms = -1.0f;
+    if (!g_splitk_ev[1] || hipEventSynchronize(g_splitk_ev[1]) != hipSuccess ||
+        hipEventElapsedTime(&ms, g_splitk_ev[0], g_splitk_ev[1]) != hipSuccess)
+        return -1.0f;
+    return ms;
+}
+
 extern "C" size_t dkv_drafter_attention_workspace(const dkv_drafter_t* mirror, int32_t n_q_heads,
                                                   int32_t want_mass) {
     if (!mirror || n_q_heads <= 0) return 0;
@@ -939,6 +961,7 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
+    if (g_time_splitk) hipEventRecord(g_splitk_ev[0], st);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
         // blocks of 4 waves; each wave walks splits blockIdx.x*4 + wave, +
@@ -1003,6 +1026,7 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
                            m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
     }
+    if (g_time_splitk) hipEventRecord(g_splitk_ev[1], st);
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
     // one wave of the combine per 8 partials, up to 16 waves

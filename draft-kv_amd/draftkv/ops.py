@@ -228,6 +228,16 @@ def drafter_attention(desc: Drafter, layer: int, cfg: QCfg, q: torch.Tensor, wan
     return out
 
 
+def drafter_kernel_timing(on: bool) -> None:
+    """Record HIP events around the split-K kernel of every drafter_attention
+    call (a benchmark hook; drafter_kernel_last_ms reads the last pair)."""
+    check(lib().dkv_drafter_kernel_timing(int(bool(on))), "dkv_drafter_kernel_timing")
+
+
+def drafter_kernel_last_ms() -> float:
+    return float(lib().dkv_drafter_kernel_last_ms())
+
+
 def drafter_gather(desc: Drafter, seq: int, layer: int, cfg: QCfg, rows: int, device) -> dict:
     H, D = desc.n_kv_heads, desc.head_dim
     ng = 0 if cfg.bits >= 16 else -(-D // cfg.group)

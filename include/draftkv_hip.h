@@ -164,6 +164,14 @@ int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t
                           const float* q, int32_t n_q_heads, int32_t want_mass, float* out,
                           void* work, size_t work_bytes, dkv_stream_t stream);
 
+/* Measurement hook (no counterpart in the reference; for benchmarks that
+ * time the dominant kernel alone): when on, dkv_drafter_attention records
+ * a pair of HIP events around its split-K kernel on its launch stream;
+ * dkv_drafter_kernel_last_ms waits for the last pair and returns the
+ * elapsed milliseconds (-1 when there is none). Not for concurrent callers. */
+int dkv_drafter_kernel_timing(int32_t on);
+float dkv_drafter_kernel_last_ms(void);
+
 /* Unpack one layer of one sequence to plain arrays (debug/parity `read`,
  * compress.py:135-142): codes u8 [rows][Hkv][D], scale/lo f32
  * [rows][Hkv][groups], deq f32 [rows][Hkv][D] for K and V, pos int32 [rows].

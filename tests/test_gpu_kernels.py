@@ -277,6 +277,30 @@ def test_drafter_attention_and_mass(dev, arm, Hq, Hkv, D):
     assert mass.shape == (nr,)
 
 
+def test_splitk_timing_hook_times_each_call(dev):
+    """The benchmark hook records events around the split-K kernel only: its
+    time is positive and below the whole call's, and off means no events."""
+    draftkv, _ = _dk()
+    from draftkv import ops
+    rng = np.random.default_rng(5)
+    _, full_d, _, _ = _full_pair(1, 8, 128, 3000, rng, dev)
+    md = draftkv.CompressedKVCache(1, [_dcfg(Cfg(4, 0.25, group=32, meta="f16"))])
+    md.sync_from(full_d, 0)
+    q = torch.from_numpy(rng.standard_normal((1, 32, 128)).astype(np.float32)).to(dev)
+    ops.drafter_kernel_timing(True)
+    try:
+        for _ in range(3):
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_ev.record()
+            md.attend(0, q, want_mass=True)
+            e_ev.record()
+            k_ms = ops.drafter_kernel_last_ms()
+            torch.cuda.synchronize()
+            assert 0.0 < k_ms <= s_ev.elapsed_time(e_ev) + 1e-3
+    finally:
+        ops.drafter_kernel_timing(False)
+
+
 # ------------------------------------------------------------------ (a10, a11)
 @pytest.mark.parametrize("V", [128, 50257, 128256])
 @pytest.mark.parametrize("T", [0.0, 0.8, 1.0])
