@@ -656,25 +656,24 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     const int h = blockIdx.y, s = blockIdx.z;
     const int G = Hq / m.n_kv_heads;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    // This wave's splits are split0, split0 + stride, ... while they hold rows;
-    // their pages form one stream g = 0..T-1 (split j = g / PPS, page g % PPS),
-    // so the ring stays full across split boundaries. Only the segment's last
-    // split can be partial, and it is the wave's last.
-    const int PPS = rps / PAGE;
-    const int split0 = blockIdx.x * 4 + wave, stride = 4 * gridDim.x;
-    const int nsplit = min((n + rps - 1) / rps, n_splits);
-    if (split0 >= nsplit) return;
-    const int J = (nsplit - 1 - split0) / stride + 1;
-    const int last_rows = n - (split0 + (J - 1) * stride) * rps;   // rows of the wave's last split
-    const int T = (J - 1) * PPS + (min(last_rows, rps) + PAGE - 1) / PAGE;
-    const bool tail = last_rows < rps && last_rows % PAGE != 0;   // the stream's last page is partial
+    // The segment's live pages are dealt in contiguous, balanced runs to its
+    // A = min(waves, pages) active waves: wave w streams pages
+    // [w*np/A, (w+1)*np/A) as one run g = 0..T-1 and writes partial slot w.
+    // Only the segment's last page can be partial, and it is the last wave's last.
+    const int wid = blockIdx.x * 4 + wave;
+    const int np = (n + PAGE - 1) / PAGE;
+    const int A = min(min(4 * (int)gridDim.x, n_splits), np);
+    if (wid >= A) return;
+    const int pg0 = (int)(((int64_t)wid * np) / A);
+    const int T = (int)(((int64_t)(wid + 1) * np) / A) - pg0;
+    const bool tail = wid == A - 1 && n % PAGE != 0;   // the stream's last page is partial
     const PageFmt f = page_fmt(cfg, D);
     const uint32_t kmb = (uint32_t)(f.vc - f.km);   // K meta bytes (= V meta bytes)
 
     extern __shared__ __align__(16) char dma_smem[];
     char* ring = dma_smem + (size_t)wave * S * SLOT;
     int slot_in = 0, slot_out = 0;   // byte offsets of the next slot to fill / to read
-    auto page_of = [&](int g) { return (split0 + (g / PPS) * stride) * PPS + g % PPS; };
+    auto page_of = [&](int g) { return pg0 + g; };
     // source offset of each 1 KB load (the same for every page); the V code
     // loads gather into lane order and need the lane's column
     const int col = lane % 16, jj = lane / 16;
@@ -705,8 +704,8 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     for (int j = 0; j < S - 1; ++j)
         if (j < T) issue(j);
 
-    // one softmax state across the wave's whole stream: a single partial, in
-    // slot split0
+    // one softmax state across the wave's whole run: a single partial, in
+    // slot wid
     Core c;
     c.init(q, s, h, Hq, G, cfg.group, lane, scale);
     c.reset();
@@ -759,22 +758,23 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     for (int g = 0; g < gfull; ++g) {
         wait_page(g);
         if (g + S - 1 < T) issue(g + S - 1);
-        const int j = g / PPS, k = g % PPS, split = split0 + j * stride;
         operands(cur);
-        c.template page<false>(cur, split * rps + k * PAGE, n, store);
+        c.template page<false>(cur, (pg0 + g) * PAGE, n, store);
     }
     if (tail) {
-        const int g = T - 1, j = g / PPS, k = g % PPS, split = split0 + j * stride;
+        const int g = T - 1;
         wait_page(g);
         operands(cur);
-        c.template page<true>(cur, split * rps + k * PAGE, n, store);
+        c.template page<true>(cur, (pg0 + g) * PAGE, n, store);
     }
-    c.finish(part, s, h, Hq, G, n_splits, split0);
+    c.finish(part, s, h, Hq, G, n_splits, wid);
 }
 
 // ---------------------------------------------------------------- combine + mass
 // Merge the partials of (seq, query head) and record the final (max, sum).
-// Partial slots [0, min(live splits, n_parts)) hold data. The global max
+// Partial slots [0, min(live units, n_splits, n_parts)) hold data, a unit
+// being a split (register-staged and generic kernels) or a page (the
+// LDS-staged kernel, whose waves take contiguous runs of pages). The global max
 // comes first, so the weighted sums over the partials are independent terms:
 // wave w of the block takes partials w, w + nw, ... (lane: channels lane and
 // lane + 64), 8 of them in flight, and the waves' sums meet in LDS in a
@@ -782,13 +782,13 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
 constexpr int COMB_WAVES = 16;
 __global__ void __launch_bounds__(64 * COMB_WAVES) draft_combine_kernel(dkv_drafter_t m, int layer,
                                                                         const float* __restrict__ part, int Hq,
-                                                                        int rps, int n_splits, int n_parts,
+                                                                        int unit, int n_splits, int n_parts,
                                                                         float* __restrict__ out,
                                                                         float* __restrict__ stats) {
     const int hq = blockIdx.x, s = blockIdx.y;
     const int D = m.head_dim, PD = D + 2;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int ns = min(min((n + rps - 1) / rps, n_splits), n_parts);
+    const int ns = min(min((n + unit - 1) / unit, n_splits), n_parts);
     const float* p = part + ((int64_t)s * Hq + hq) * n_splits * PD;
     const int nw = blockDim.x / WAVE, w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     __shared__ float smax[COMB_WAVES], sl[COMB_WAVES];
@@ -961,6 +961,7 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
+    int unit = rps;     // rows per unit of work that owns a partial slot
     if (g_time_splitk) hipEventRecord(g_splitk_ev[0], st);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
@@ -973,6 +974,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         const dim3 grid(std::min((ns + 3) / 4, per_seg), m.n_kv_heads, m.batch);
         n_parts = 4 * (int)grid.x;   // one partial per wave
         if (dma) {
+            n_parts = std::min(n_parts, ns);   // the waves past the partial slots stay idle
+            unit = PAGE;
             // 4-bit codes: pages streamed through an LDS ring, S-1 ahead; the
             // kernel is instantiated per loads-per-page count, which fixes its
             // slot size and ring depth (and so the LDS it is given)
@@ -1032,7 +1035,7 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     // one wave of the combine per 8 partials, up to 16 waves
     const int comb_waves = std::min(COMB_WAVES, std::max(1, (std::min(n_parts, ns) + 7) / 8));
     hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(WAVE * comb_waves), 0, st, m, layer,
-                       part, n_q_heads, rps, ns, n_parts, out, stats);
+                       part, n_q_heads, unit, ns, n_parts, out, stats);
     if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
     if (want_mass) {
         const int per_block = 256 * MASS_ROWS;

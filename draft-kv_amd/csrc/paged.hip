@@ -277,8 +277,11 @@ __global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, 
     // wave index through readfirstlane: the q-tile and everything derived
     // from it are then wave-uniform (scalar registers and branches)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
-    const int qg = blockIdx.x % n_qgroups, chunk = blockIdx.x / n_qgroups;
-    const int h = blockIdx.y, s = blockIdx.z;
+    // grid (q-group, head x sequence, chunk): the chunk is the slowest index, so
+    // the workgroups of the full chunks are dispatched first and the short
+    // last chunk fills the tail instead of splitting a round
+    const int qg = blockIdx.x, chunk = blockIdx.z;
+    const int h = blockIdx.y % c.n_kv_heads, s = blockIdx.y / c.n_kv_heads;
     const int G = Hq / c.n_kv_heads;
     const int s0 = start[s];
     const int len = s0 + T;
@@ -562,7 +565,9 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
         const size_t lds = dkv::VERIFY_STAGES * stage + (((size_t)chunk_keys / 16 * 4 + 15) & ~size_t(15));
         // gfx950 gives a workgroup up to 160 KB of LDS
         DKV_REQUIRE(lds <= 160 * 1024, "dkv_paged_attention: chunk_keys too large for the bf16 kernel");
-        const dim3 grid(n_chunks * n_qgroups, c.n_kv_heads, c.batch), blk(64 * W);
+        DKV_REQUIRE((int64_t)c.n_kv_heads * c.batch <= 65535 && n_chunks <= 65535,
+                    "dkv_paged_attention: batch x heads or chunk count too large for the grid");
+        const dim3 grid(n_qgroups, c.n_kv_heads * c.batch, n_chunks), blk(64 * W);
         float* part = static_cast<float*>(work);
 #define DKV_VERIFY(DD, WW)                                                                                         \
     do {                                                                                                           \
