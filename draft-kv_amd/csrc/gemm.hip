@@ -1,0 +1,356 @@
+// bf16 projection GEMM of the model forwards: y[M, N] = x[M, K] . W[N, K]^T
+// with float32 accumulation and one rounding to bf16 (or a float32 result).
+// Reference: the `x @ W` projections, MLP and LM head of model.py:113-133,
+// gpt2.py:191-213, llama.py:187-225 (numpy float32 there).
+//
+// At decode sizes (M = batch rows, or batch * (gamma + 1) in verify) the
+// product is bound by the weight stream: W is read once from HBM, x (a few
+// hundred KB) from L2. K is cut into S chunks, S a function of (N, K) only.
+// Every output is, per chunk, one in-order chain of
+// v_mfma_f32_16x16x32_bf16 over the chunk's 128-k blocks (block step j,
+// lane group q: k = 32j + 8q .. +8, the same for W and x), and the chunk
+// sums are added in chunk order, either inside the workgroup or by the
+// reduce kernel from per-chunk partials -- the same float additions in the
+// same order. So an output's arithmetic depends neither on M, nor on the
+// launch shape chosen for M, nor on the row's place in the batch: a verify
+// row equals the one-token decode row bit for bit.
+#include "dkv_common.h"
+
+namespace dkv {
+
+typedef __bf16 gbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float gf32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t gu32x4_t __attribute__((ext_vector_type(4)));   // a native vector: copies stay in registers
+
+constexpr int GKB = 128;            // k per block: four 32-k MFMA steps
+constexpr int GX_ROW = GKB + 8;     // LDS row of a staged x block (bf16), padded against bank conflicts
+
+__device__ __forceinline__ gbf16x8_t as_bf16x8(gu32x4_t v) { return __builtin_bit_cast(gbf16x8_t, v); }
+
+__device__ __forceinline__ float4 bias4(const uint16_t* b, int64_t n) {
+    if (!b) return make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint2 v = *reinterpret_cast<const uint2*>(b + n);
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                       __uint_as_float(v.y & 0xffff0000u));
+}
+
+__device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
+    const __bf16 a = (__bf16)lo, b = (__bf16)hi;   // v_cvt_pk_bf16_f32: round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+struct GemmArgs {
+    const uint16_t* x;   // [M, K]
+    const uint16_t* w;   // [N, K]
+    const uint16_t* bias;   // [N] bf16 or null, added after the chunk sums
+    int M, N, K;
+    int KC;              // chunk length: K = S * KC, KC % 32 == 0
+    int S;               // chunks
+    int c_per;           // chunks per workgroup: S (summed in order here) or 1 (one partial per chunk)
+    int units;           // n_tiles * (S / c_per)
+    int m_tiles;
+    float* part;         // [S][M][N] float32 partials when c_per == 1 < S
+    void* y;
+    int y_f32;
+};
+
+// One workgroup: 64*NW rows of W (16*NW per wave) against a tile of 16*MB
+// rows of x, over c_per consecutive K chunks. Per 128-k block the tile's x
+// is staged once in LDS (shared by the four waves); each lane streams its W
+// rows straight into registers two blocks ahead (three register sets in
+// rotation). MULTI: the chunks' sums are added in chunk order here (the same
+// additions, in the same order, as the reduce kernel applies to partials).
+// PARTIAL: chunks may end in a block of fewer than four 32-k steps (K not a
+// multiple of 128); otherwise every block is whole.
+template <int NW, int MB, bool MULTI, bool PARTIAL>
+__global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
+    constexpr int TM = 16 * MB;
+    __shared__ __align__(16) uint16_t xs[2][TM][GX_ROW];
+    // XCD-aware order: workgroup g runs on XCD g % 8; the m tiles of one unit
+    // (a W row block and chunk range) take consecutive slots of one XCD, so
+    // its W rows are fetched from HBM once and reread from that XCD's L2.
+    const int g = blockIdx.x, slot = g >> 3;
+    const int u = (slot / a.m_tiles) * 8 + (g & 7), mt = slot % a.m_tiles;
+    if (u >= a.units) return;   // whole workgroup
+    const int splits = a.S / a.c_per;
+    const int nt = u / splits, c0 = (u % splits) * a.c_per;
+    const int m0 = mt * TM, mrows = min(TM, a.M - m0);
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int col = lane % 16, q = lane / 16;
+    const int n0 = nt * 64 * NW + 16 * NW * wave;
+    const bool live = n0 < a.N;   // wave-uniform; NW == 2 only where N % 32 == 0
+    const int K = a.K, KC = a.KC;
+    const int nb = (KC + GKB - 1) / GKB, G = nb * a.c_per;
+    const uint16_t* wrow[NW];
+#pragma unroll
+    for (int f = 0; f < NW; ++f) wrow[f] = a.w + (int64_t)(live ? n0 + 16 * f + col : col) * K + 8 * q;
+    // x piece i of this thread: tile row xr_row[i], k offset 8 xr_c[i] in the block. Tile rows past M
+    // reread row M-1 (their outputs are dropped), so every load and LDS write is unconditional.
+    const uint16_t* xsrc[MB];
+    uint32_t xdst[MB];
+    int xc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int p = tid + 256 * i, r = p / 16;
+        xc[i] = p % 16;
+        xsrc[i] = a.x + (int64_t)(m0 + min(r, mrows - 1)) * K;
+        xdst[i] = (uint32_t)(r * GX_ROW);
+    }
+
+    // block gb of this workgroup: k start and number of 32-k steps
+    auto blk_k = [&](int gb) {
+        const int cl = gb / nb;
+        return (c0 + cl) * KC + (gb - cl * nb) * GKB;
+    };
+    auto blk_steps = [&](int gb) {
+        if constexpr (!PARTIAL) return 4;
+        const int cl = gb / nb;
+        return min(4, (KC - (gb - cl * nb) * GKB) / 32);
+    };
+
+    // Every load below is unconditional (addresses clamped into the operands), so that the compiler's
+    // wait counts see the same sequence of loads on every path and keep two blocks in flight.
+#define DKV_LOAD_W(DST, GB)                                                                                     \
+    do {                                                                                                        \
+        const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
+        _Pragma("unroll") for (int f = 0; f < NW; ++f) _Pragma("unroll") for (int j = 0; j < 4; ++j) DST[f][j] = \
+            *reinterpret_cast<const gu32x4_t*>(wrow[f] + k_ + 32 * (PARTIAL ? min(j, st_ - 1) : j));            \
+    } while (0)
+#define DKV_LOAD_X(GB)                                                                                          \
+    do {                                                                                                        \
+        const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
+        _Pragma("unroll") for (int i = 0; i < MB; ++i) xr[i] =                                                 \
+            *reinterpret_cast<const gu32x4_t*>(xsrc[i] + k_ + 8 * (PARTIAL ? min(xc[i], 4 * st_ - 1) : xc[i]));   \
+    } while (0)
+#define DKV_STORE_X(BUF)                                                                                        \
+    do {                                                                                                        \
+        _Pragma("unroll") for (int i = 0; i < MB; ++i) *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i] +    \
+                                                                                 8 * xc[i]) = xr[i];            \
+    } while (0)
+
+    gf32x4_t acc[NW][MB], tot[MULTI ? NW : 1][MULTI ? MB : 1];
+#pragma unroll
+    for (int f = 0; f < NW; ++f)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[f][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    gu32x4_t w0[NW][4], w1[NW][4], w2[NW][4], xr[MB];
+    DKV_LOAD_X(0);
+    DKV_STORE_X(0);
+    DKV_LOAD_W(w0, 0);
+    DKV_LOAD_X(min(1, G - 1));
+    DKV_LOAD_W(w1, min(1, G - 1));
+    __syncthreads();
+
+    // one block: stage x(gb+1), prefetch block gb+2 into NXT (the last block again past the end),
+    // multiply block gb from CUR
+#define DKV_BLOCK(CUR, NXT)                                                                                     \
+    do {                                                                                                        \
+        const int gb = g0 + v_;                                                                                 \
+        if (gb + 1 < G) DKV_STORE_X((gb + 1) & 1);                                                              \
+        DKV_LOAD_X(min(gb + 2, G - 1));                                                                         \
+        DKV_LOAD_W(NXT, min(gb + 2, G - 1));                                                                    \
+        const int st = blk_steps(min(gb, G - 1));                                                               \
+        if (live && gb < G) {                                                                                   \
+            const uint16_t* xb = &xs[gb & 1][0][0] + col * GX_ROW + 8 * q;                                      \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                     \
+                if (!PARTIAL || j < st) {                                                                       \
+                    gbf16x8_t bx[MB];                                                                           \
+                    _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) bx[mb] =                                  \
+                        as_bf16x8(*reinterpret_cast<const gu32x4_t*>(xb + 16 * mb * GX_ROW + 32 * j));             \
+                    _Pragma("unroll") for (int f = 0; f < NW; ++f) _Pragma("unroll") for (int mb = 0; mb < MB;  \
+                                                                                          ++mb) acc[f][mb] =    \
+                        __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(CUR[f][j]), bx[mb], acc[f][mb], 0, 0, 0); \
+                }                                                                                               \
+            }                                                                                                   \
+        }                                                                                                       \
+        if constexpr (MULTI) {                                                                                  \
+            if (gb < G && (gb + 1) % nb == 0) { /* a chunk ends: add its sum in chunk order */                 \
+                _Pragma("unroll") for (int f = 0; f < NW; ++f) _Pragma("unroll") for (int mb = 0; mb < MB;      \
+                                                                                      ++mb) {                   \
+                    if (gb + 1 == nb) tot[f][mb] = acc[f][mb];                                                  \
+                    else                                                                                        \
+                        _Pragma("unroll") for (int e = 0; e < 4; ++e) tot[f][mb][e] =                           \
+                            tot[f][mb][e] + acc[f][mb][e];                                                      \
+                    acc[f][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};                                                  \
+                }                                                                                               \
+            }                                                                                                   \
+        }                                                                                                       \
+        __syncthreads();                                                                                        \
+    } while (0)
+
+    for (int g0 = 0; g0 < G; g0 += 3) {
+        {
+            constexpr int v_ = 0;
+            DKV_BLOCK(w0, w2);
+        }
+        {
+            constexpr int v_ = 1;
+            DKV_BLOCK(w1, w0);
+        }
+        {
+            constexpr int v_ = 2;
+            DKV_BLOCK(w2, w1);
+        }
+    }
+#undef DKV_BLOCK
+#undef DKV_STORE_X
+#undef DKV_LOAD_X
+#undef DKV_LOAD_W
+    if (!live) return;
+    // lane holds C[4q + r][col]: outputs (m, n + 4q .. 4q + 3), m = m0 + 16 mb + col
+    const bool to_part = !MULTI && a.S > 1;
+#pragma unroll
+    for (int f = 0; f < NW; ++f)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int m = m0 + 16 * mb + col;
+            if (m >= a.M) continue;
+            gf32x4_t t;
+            if constexpr (MULTI) t = tot[f][mb];
+            else t = acc[f][mb];
+            const int n = n0 + 16 * f + 4 * q;
+            const int64_t o = (int64_t)m * a.N + n;
+            if (!to_part && a.bias) {
+                const float4 bv = bias4(a.bias, n);
+                t[0] = t[0] + bv.x;
+                t[1] = t[1] + bv.y;
+                t[2] = t[2] + bv.z;
+                t[3] = t[3] + bv.w;
+            }
+            if (to_part) {
+                *reinterpret_cast<float4*>(a.part + (int64_t)c0 * a.M * a.N + o) = make_float4(t[0], t[1], t[2], t[3]);
+            } else if (a.y_f32) {
+                *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
+            } else {
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + o) =
+                    make_uint2(bf16_pair_rne(t[0], t[1]), bf16_pair_rne(t[2], t[3]));
+            }
+        }
+}
+
+// y = sum of the K chunks' partials, in chunk order, then the bias; 4 outputs per thread
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, int64_t MN, int S, int N,
+                                                          const uint16_t* __restrict__ bias, void* __restrict__ y,
+                                                          int y_f32) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= MN) return;
+    float4 t = *reinterpret_cast<const float4*>(part + i);
+    for (int s = 1; s < S; ++s) {
+        const float4 u = *reinterpret_cast<const float4*>(part + (int64_t)s * MN + i);
+        t.x += u.x;
+        t.y += u.y;
+        t.z += u.z;
+        t.w += u.w;
+    }
+    if (bias) {   // the four outputs share a row (N % 16 == 0)
+        const float4 bv = bias4(bias, i % N);
+        t.x += bv.x;
+        t.y += bv.y;
+        t.z += bv.z;
+        t.w += bv.w;
+    }
+    if (y_f32) *reinterpret_cast<float4*>(static_cast<float*>(y) + i) = t;
+    else *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + i) = make_uint2(bf16_pair_rne(t.x, t.y),
+                                                                               bf16_pair_rne(t.z, t.w));
+}
+
+// K chunks: a function of (N, K) only, never of M, so that an output's
+// additions are the same for every batch. Enough chunks for about 512
+// workgroups of 64 W rows when M is small, each chunk a whole number of
+// 128-k blocks and at least 512 long.
+static int gemm_chunks(int N, int K) {
+    const int64_t wgs = (N + 63) / 64;
+    int S = 1;
+    while (wgs * S < 512 && K % (2 * S * GKB) == 0 && K / (2 * S) >= 512) S *= 2;
+    return S;
+}
+
+// Launch shape, free to depend on M (the arithmetic does not): W rows per
+// wave, x rows per tile, and whether the chunks are split across workgroups.
+struct GemmPlan {
+    int nw, mb, m_tiles, n_tiles, c_per;
+};
+
+static GemmPlan gemm_plan(int M, int N, int K) {
+    GemmPlan p;
+    const int S = gemm_chunks(N, K);
+    // from M = 33 on, two W fragments per wave (each x fragment read from LDS feeds two MFMAs) wherever
+    // whole 32-row fragments and 128-k blocks allow; the x tile just covers M up to 128 rows (measured
+    // on the Llama-3-8B projection and head shapes, weights streamed cold from HBM)
+    p.nw = (N % 32 == 0 && K % GKB == 0 && M > 32) ? 2 : 1;
+    p.mb = M <= 16 ? 1 : M <= 32 ? 2 : (M <= 64 || p.nw == 1) ? 4 : 8;
+    p.m_tiles = (M + 16 * p.mb - 1) / (16 * p.mb);
+    p.n_tiles = (N + 64 * p.nw - 1) / (64 * p.nw);
+    // split the chunks over workgroups only when the tiles alone leave most of the chip idle
+    p.c_per = (S > 1 && (int64_t)p.n_tiles * p.m_tiles < 128) ? 1 : S;
+    return p;
+}
+
+}  // namespace dkv
+
+using namespace dkv;
+
+extern "C" size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int S = gemm_chunks(N, K);
+    const GemmPlan p = gemm_plan(M, N, K);
+    return p.c_per == 1 && S > 1 ? sizeof(float) * (size_t)S * M * N : 0;
+}
+
+template <int NW, int MB, bool PARTIAL>
+static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
+    if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL>), grid, dim3(256), 0, st, a);
+}
+
+template <int NW, int MB>
+static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
+    if (a.KC % GKB == 0) launch_gemm<NW, MB, false>(a, grid, st);
+    else launch_gemm<NW, MB, true>(a, grid, st);
+}
+
+extern "C" int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int32_t M, int32_t N, int32_t K, void* y,
+                             int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream) {
+    DKV_REQUIRE(x && w && y, "dkv_gemm_bf16: NULL argument");
+    DKV_REQUIRE(M >= 0 && N > 0 && K > 0, "dkv_gemm_bf16: bad sizes");
+    DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
+    DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
+    DKV_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(y) % 16 == 0,
+                "dkv_gemm_bf16: x, w and y must be 16-byte aligned");
+    DKV_REQUIRE(reinterpret_cast<uintptr_t>(bias) % 8 == 0, "dkv_gemm_bf16: bias must be 8-byte aligned");
+    if (M == 0) return DKV_OK;
+    const int S = gemm_chunks(N, K);
+    const GemmPlan p = gemm_plan(M, N, K);
+    const size_t need = dkv_gemm_bf16_workspace(M, N, K);
+    if (need && (!work || work_bytes < need))
+        return fail(DKV_EWORKSPACE, "dkv_gemm_bf16: workspace too small (need " + std::to_string(need) + ")");
+    DKV_REQUIRE(reinterpret_cast<uintptr_t>(work) % 16 == 0, "dkv_gemm_bf16: workspace must be 16-byte aligned");
+    GemmArgs a;
+    a.x = static_cast<const uint16_t*>(x);
+    a.w = static_cast<const uint16_t*>(w);
+    a.bias = static_cast<const uint16_t*>(bias);
+    a.M = M, a.N = N, a.K = K, a.S = S, a.KC = K / S, a.c_per = p.c_per;
+    a.units = p.n_tiles * (S / p.c_per);
+    a.m_tiles = p.m_tiles;
+    a.part = need ? static_cast<float*>(work) : nullptr;
+    a.y = y;
+    a.y_f32 = y_dtype == DKV_F32;
+    const int64_t nwg = (int64_t)(a.units + 7) / 8 * 8 * p.m_tiles;
+    DKV_REQUIRE(nwg < (int64_t)1 << 31, "dkv_gemm_bf16: too many workgroups");
+    const dim3 grid((unsigned)nwg);
+    hipStream_t st = as_stream(stream);
+    if (p.nw == 2 && p.mb == 4) launch_gemm<2, 4, false>(a, grid, st);   // K % 128 == 0 with two fragments
+    else if (p.nw == 2) launch_gemm<2, 8, false>(a, grid, st);
+    else if (p.mb == 1) launch_gemm<1, 1>(a, grid, st);
+    else if (p.mb == 2) launch_gemm<1, 2>(a, grid, st);
+    else launch_gemm<1, 4>(a, grid, st);
+    int rc = check_launch("dkv_gemm_bf16");
+    if (rc || !need) return rc;
+    const int64_t MN = (int64_t)M * N;   // a multiple of 16
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, a.part, MN, S, N,
+                       a.bias, y, a.y_f32);
+    return check_launch("dkv_gemm_bf16(reduce)");
+}

@@ -42,20 +42,23 @@ __global__ void __launch_bounds__(256) paged_append_kernel(dkv_paged_t c, int la
 // tile max/sum order, rescale sequence) depends only on absolute key indices,
 // never on T or on how many rows share the block, so a row's partial is
 // bit-identical whether it is computed in a verify pass (T = gamma+1) or in a
-// one-token decode step. Masked keys contribute exact zeros.
+// one-token decode step. Masked keys contribute exact zeros. The cache ends
+// at start + count (count null: all T rows were appended); positions past it
+// are never read as keys -- their pages may hold stale bytes, and 0 * NaN is
+// NaN -- and a padding row (t >= count) attends over the whole cache.
 constexpr int QB = 16;
 constexpr int KT = 32;
 constexpr int MAXD = 128;   // LDS tiles stay under 64 KB
 
 __global__ void __launch_bounds__(256) paged_attn_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
                                                          int T, int Hq, const int32_t* __restrict__ start,
-                                                         int CH, int n_chunks, int n_qtiles, float scale,
-                                                         float* __restrict__ part) {
+                                                         const int32_t* __restrict__ count, int CH, int n_chunks,
+                                                         int n_qtiles, float scale, float* __restrict__ part) {
     const int chunk = blockIdx.x / n_qtiles, qtile = blockIdx.x % n_qtiles;
     const int h = blockIdx.y, s = blockIdx.z;
     const int D = c.head_dim, G = Hq / c.n_kv_heads;
     const int s0 = start[s];
-    const int len = s0 + T;                       // cache holds positions 0..len-1
+    const int len = s0 + (count ? count[s] : T);  // cache holds positions 0..len-1
     const int k_begin = chunk * CH;
     if (k_begin >= len) return;
     const int k_end = min(k_begin + CH, len);
@@ -264,7 +267,8 @@ __device__ __forceinline__ uint64_t key_mask4(int nv) {
 template <int D, int W>
 __global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, int layer, const float* __restrict__ q,
                                                                  int T, int Hq, const int32_t* __restrict__ start,
-                                                                 int CH, int n_qgroups, int n_chunks, int n_qtiles,
+                                                                 const int32_t* __restrict__ count, int CH,
+                                                                 int n_qgroups, int n_chunks, int n_qtiles,
                                                                  float scale, float* __restrict__ part) {
 #pragma clang fp contract(off)
     using St = VerifyStage<D>;
@@ -284,7 +288,7 @@ __global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, 
     const int h = blockIdx.y % c.n_kv_heads, s = blockIdx.y / c.n_kv_heads;
     const int G = Hq / c.n_kv_heads;
     const int s0 = start[s];
-    const int len = s0 + T;
+    const int len = s0 + (count ? count[s] : T);
     const int k_begin = chunk * CH;
     const int n_rows = T * G;
     // the group's last row bounds the keys any of its rows may see
@@ -456,11 +460,19 @@ __global__ void __launch_bounds__(64 * W) paged_attn_mfma_kernel(dkv_paged_t c, 
 constexpr int PCOMB_WAVES = 4;
 __global__ void __launch_bounds__(64 * PCOMB_WAVES) paged_combine_kernel(const float* __restrict__ part, int T,
                                                                          int Hq, int D,
-                                                                         const int32_t* __restrict__ start, int CH,
+                                                                         const int32_t* __restrict__ start,
+                                                                         const int32_t* __restrict__ count, int CH,
                                                                          int n_chunks, float* __restrict__ out) {
     const int hq = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
-    const int qpos = start[s] + t;
-    const int nc = min(qpos / CH + 1, n_chunks);   // never past the workspace
+    // the last key the row saw: its own position, or the cache end for a
+    // padding row (t >= count[s]), which attends over the whole cache
+    const int len = start[s] + (count ? count[s] : T);
+    const int last = min(start[s] + t, len - 1);
+    if (last < 0) {   // an empty cache (count 0 at start 0): nothing to attend to
+        for (int d = threadIdx.x; d < D; d += blockDim.x) out[(((int64_t)s * T + t) * Hq + hq) * D + d] = 0.0f;
+        return;
+    }
+    const int nc = min(last / CH + 1, n_chunks);   // never past the workspace
     const int PD = D + 2;
     const float* p = part + (((int64_t)s * T + t) * Hq + hq) * n_chunks * PD;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -532,8 +544,9 @@ extern "C" size_t dkv_paged_attention_workspace(const dkv_paged_t* cache, int32_
 }
 
 extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, const float* q, int32_t T,
-                                   int32_t n_q_heads, const int32_t* start, int32_t max_len, int32_t chunk_keys,
-                                   float* out, void* work, size_t work_bytes, dkv_stream_t stream) {
+                                   int32_t n_q_heads, const int32_t* start, const int32_t* count, int32_t max_len,
+                                   int32_t chunk_keys, float* out, void* work, size_t work_bytes,
+                                   dkv_stream_t stream) {
     DKV_REQUIRE(cache && q && start && out, "dkv_paged_attention: NULL argument");
     const dkv_paged_t c = *cache;
     DKV_REQUIRE(layer >= 0 && layer < c.n_layers, "dkv_paged_attention: layer out of range");
@@ -575,8 +588,8 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
         if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),                             \
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
             return dkv::fail(DKV_ELAUNCH, "dkv_paged_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
-        hipLaunchKernelGGL(kfn, grid, blk, lds, st, c, layer, q, T, n_q_heads, start, chunk_keys, n_qgroups,       \
-                           n_chunks, n_qtiles, scale, part);                                                       \
+        hipLaunchKernelGGL(kfn, grid, blk, lds, st, c, layer, q, T, n_q_heads, start, count, chunk_keys,          \
+                           n_qgroups, n_chunks, n_qtiles, scale, part);                                            \
     } while (0)
         if (c.head_dim == 128) {
             switch (W) {
@@ -596,12 +609,13 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
 #undef DKV_VERIFY
     } else {
         hipLaunchKernelGGL(dkv::paged_attn_kernel, dim3(n_chunks * n_qtiles, c.n_kv_heads, c.batch), dim3(256),
-                           dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, chunk_keys, n_chunks,
-                           n_qtiles, scale, static_cast<float*>(work));
+                           dkv::attn_smem(c.head_dim), st, c, layer, q, T, n_q_heads, start, count, chunk_keys,
+                           n_chunks, n_qtiles, scale, static_cast<float*>(work));
     }
     int rc = dkv::check_launch("dkv_paged_attention");
     if (rc) return rc;
     hipLaunchKernelGGL(dkv::paged_combine_kernel, dim3(n_q_heads, T, c.batch), dim3(dkv::WAVE * dkv::PCOMB_WAVES), 0, st,
-                       static_cast<const float*>(work), T, n_q_heads, c.head_dim, start, chunk_keys, n_chunks, out);
+                       static_cast<const float*>(work), T, n_q_heads, c.head_dim, start, count, chunk_keys, n_chunks,
+                       out);
     return dkv::check_launch("dkv_paged_attention(combine)");
 }

@@ -42,7 +42,7 @@ _SIGS = {
     "dkv_quantize": (C.c_int, [P, I64, I32, I32, I32, I32, P, P, P, P, P]),
     "dkv_paged_append": (C.c_int, [PPaged, I32, P, P, I32, I32, P, P, P]),
     "dkv_paged_attention_workspace": (SZ, [PPaged, I32, I32, I32, I32]),
-    "dkv_paged_attention": (C.c_int, [PPaged, I32, P, I32, I32, P, I32, I32, P, P, SZ, P]),
+    "dkv_paged_attention": (C.c_int, [PPaged, I32, P, I32, I32, P, P, I32, I32, P, P, SZ, P]),
     "dkv_page_bytes": (I64, [I32, I32, I32, I32]),
     "dkv_drafter_append": (C.c_int, [PDrafter, I32, QCfg, P, P, I32, I32, P, P, P, P]),
     "dkv_drafter_truncate": (C.c_int, [PDrafter, PQCfg, P, P]),
@@ -68,6 +68,8 @@ _SIGS = {
     "dkv_relu": (C.c_int, [P, I32, I32, I32, P, I32, P]),
     "dkv_add": (C.c_int, [P, P, I32, P, I32, I32, I32, P]),
     "dkv_gemm_f32": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P]),
+    "dkv_gemm_bf16_workspace": (SZ, [I32, I32, I32]),
+    "dkv_gemm_bf16": (C.c_int, [P, P, P, I32, I32, I32, P, I32, P, SZ, P]),
     "dkv_last_error": (C.c_char_p, []),
     "dkv_version": (I32, []),
 }

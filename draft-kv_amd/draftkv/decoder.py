@@ -116,7 +116,16 @@ class Decoder:
         """x @ W (+ bias); float32 out for float32 models, bf16 out for bf16 models."""
         if self.wdtype == torch.float32:
             return ops.gemm_f32(x, w, self.layout, bias)
-        return F.linear(x, w, bias)
+        return self._linear(x, w, bias)
+
+    @staticmethod
+    def _linear(x: torch.Tensor, w: torch.Tensor, bias=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+        """bf16 x @ W^T (+ b) (W as [N, K]): the library's batch-invariant
+        GEMM when it takes the shapes, else torch's."""
+        if ops.gemm_bf16_ok(x, w, bias):
+            return ops.gemm_bf16(x, w, bias, out_dtype)
+        y = F.linear(x, w, bias)
+        return y if out_dtype == torch.bfloat16 else y.to(out_dtype)
 
     def _residual(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias, nw, nb) -> torch.Tensor:
         """h += x @ W (+ bias), then return the next norm of h (weights nw, nb).
@@ -124,7 +133,7 @@ class Decoder:
         if self.wdtype == torch.float32:
             ops.gemm_f32(x, w, self.layout, bias, out=h, accumulate=True)
             return self._norm(h, nw, nb)
-        return ops.add_norm(h, F.linear(x, w), bias, nw, nb, self.eps, self.norm == "layer", self.act_dtype)
+        return ops.add_norm(h, self._linear(x, w), bias, nw, nb, self.eps, self.norm == "layer", self.act_dtype)
 
     def _mlp_inner(self, x: torch.Tensor, p: Layer) -> torch.Tensor:
         if self.mlp == "swiglu":
@@ -136,7 +145,7 @@ class Decoder:
     def _head(self, x: torch.Tensor) -> torch.Tensor:
         if self.wdtype == torch.float32:
             return ops.gemm_f32(x, self.head, self.head_layout)
-        return F.linear(x, self.head).float()
+        return self._linear(x, self.head, out_dtype=torch.float32)
 
     # ------------------------------------------------------------ forward
     def forward_batch(self, tokens: torch.Tensor, cache, start: Sequence[int],
@@ -218,7 +227,7 @@ class Decoder:
 
         def attn(L, q, k, v):
             cache.append_layer(L, k, v, start_d, count_d)
-            return cache.attend(L, q, start_d, max_pos)
+            return cache.attend(L, q, start_d, max_pos, count=count_d)
 
         attn.finish = lambda: cache.commit(ct)
         return attn

@@ -154,9 +154,15 @@ def paged_append(desc: Paged, layer: int, k: torch.Tensor, v: torch.Tensor, star
 
 
 def paged_attention(desc: Paged, layer: int, q: torch.Tensor, start: torch.Tensor, max_len: int,
-                    chunk_keys: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    chunk_keys: int, out: Optional[torch.Tensor] = None,
+                    count: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of q [batch, T, Hq, D] over the paged cache; count
+    (int32 [batch], optional): the rows each sequence appended this forward
+    (the cache ends at start + count; padding rows see the whole cache)."""
     _need(q, "q", torch.float32, 4)
     _need(start, "start", torch.int32)
+    if count is not None:
+        _need(count, "count", torch.int32)
     b, T, Hq, D = q.shape
     if b != desc.batch or D != desc.head_dim:
         raise ValueError(f"q shape {tuple(q.shape)} does not match the cache")
@@ -164,8 +170,8 @@ def paged_attention(desc: Paged, layer: int, q: torch.Tensor, start: torch.Tenso
         out = torch.empty_like(q)
     nbytes = lib().dkv_paged_attention_workspace(C.byref(desc), T, Hq, max_len, chunk_keys)
     ws = _WS.get(q.device, nbytes)
-    check(lib().dkv_paged_attention(C.byref(desc), layer, q.data_ptr(), T, Hq, start.data_ptr(), max_len,
-                                    chunk_keys, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream()),
+    check(lib().dkv_paged_attention(C.byref(desc), layer, q.data_ptr(), T, Hq, start.data_ptr(), _ptr(count),
+                                    max_len, chunk_keys, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream()),
           "dkv_paged_attention")
     return out
 
@@ -424,4 +430,35 @@ def gemm_f32(x: torch.Tensor, w: torch.Tensor, w_layout: int, bias: Optional[tor
     bp, bd = _bias(bias)
     check(lib().dkv_gemm_f32(x.data_ptr(), w.data_ptr(), w_layout, M, N, K, bp, bd, out.data_ptr(), int(accumulate),
                              _stream()), "dkv_gemm_f32")
+    return out
+
+
+def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None) -> bool:
+    """Whether dkv_gemm_bf16 takes this product (bf16 contiguous x [M, K] and
+    w [N, K], N % 16 == 0, K % 32 == 0, 16-byte aligned; bias None or bf16
+    contiguous [N], 8-byte aligned)."""
+    ok = (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2
+          and x.is_cuda and w.is_cuda and x.is_contiguous() and w.is_contiguous()
+          and x.shape[1] == w.shape[1] and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0
+          and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+    if ok and bias is not None:
+        ok = (bias.dtype == torch.bfloat16 and bias.is_cuda and bias.dim() == 1 and bias.is_contiguous()
+              and bias.shape[0] == w.shape[0] and bias.data_ptr() % 8 == 0)
+    return ok
+
+
+def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+              out_dtype=torch.bfloat16) -> torch.Tensor:
+    """x [M, K] @ w[N, K]^T (+ bias), bf16 in, float32 accumulation, bf16 (or
+    float32) out; a row's result is the same for any M."""
+    if not gemm_bf16_ok(x, w, bias):
+        raise ValueError(f"gemm_bf16: unsupported operands x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}"
+                         + ("" if bias is None else f", bias {tuple(bias.shape)} {bias.dtype}"))
+    M, K = x.shape
+    N = w.shape[0]
+    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)
+    ws = _WS.get(x.device, nbytes) if nbytes else None
+    check(lib().dkv_gemm_bf16(x.data_ptr(), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(), _odt(out_dtype),
+                              _ptr(ws), 0 if ws is None else ws.numel(), _stream()), "dkv_gemm_bf16")
     return out

@@ -192,8 +192,10 @@ class PagedKVCache:
         ops.paged_append(self.desc(), layer, k, v, start, count)
 
     def attend(self, layer: int, q: torch.Tensor, start: torch.Tensor, max_len: int,
-               out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        return ops.paged_attention(self.desc(), layer, q, start, max_len, self.chunk_keys, out)
+               out: Optional[torch.Tensor] = None, count: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Causal attention of q [batch, T, heads, d_head] at positions start[s]..;
+        count: the rows appended this forward when not all T (see append_layer)."""
+        return ops.paged_attention(self.desc(), layer, q, start, max_len, self.chunk_keys, out, count)
 
     def commit(self, counts: Sequence[int]) -> None:
         """Record that ``counts[s]`` rows were appended to every layer."""

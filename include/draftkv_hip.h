@@ -99,16 +99,20 @@ int dkv_paged_append(const dkv_paged_t* cache, int32_t layer, const void* k, con
  * softmax of draftkv/llama.py:202-218 / gpt2.py:197-206 / model.py:117-127
  * against FullKVCache/PagedKVCache. q: f32 [batch][T][Hq][D]; query t of
  * sequence s sits at position start[s]+t and sees positions <= its own.
- * out: f32 [batch][T][Hq][D]. Keys are split in fixed chunks of
+ * count: NULL (every sequence appended all T rows) or int32 [batch], the
+ * rows sequence s appended (dkv_paged_append's count); the cache of s then
+ * ends at start[s]+count[s], positions past it are never read, and a
+ * padding row t >= count[s] attends over the whole cache (zeros when it
+ * is empty). out: f32 [batch][T][Hq][D]. Keys are split in fixed chunks of
  * chunk_keys absolute positions and merged in chunk order, so a query's
  * result does not depend on T or on the cache length (batch invariance).
  * work: dkv_paged_attention_workspace() bytes. */
 size_t dkv_paged_attention_workspace(const dkv_paged_t* cache, int32_t T, int32_t n_q_heads,
                                      int32_t max_len, int32_t chunk_keys);
 int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, const float* q, int32_t T,
-                        int32_t n_q_heads, const int32_t* start, int32_t max_len,
-                        int32_t chunk_keys, float* out, void* work, size_t work_bytes,
-                        dkv_stream_t stream);
+                        int32_t n_q_heads, const int32_t* start, const int32_t* count,
+                        int32_t max_len, int32_t chunk_keys, float* out, void* work,
+                        size_t work_bytes, dkv_stream_t stream);
 
 /* ------------------------------------------------------------ (a1,a3,a4) */
 /* Quantize and append T rows per sequence to one layer of the mirror, then
@@ -256,6 +260,19 @@ int dkv_add(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t 
  * one-token decode agree bit for bit)  -- the x @ W products of the model forwards */
 int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, int32_t N, int32_t K,
                  const void* bias, int32_t bias_dtype, float* out, int32_t accumulate, dkv_stream_t stream);
+/* y[M][N] = x[M][K] . w[N][K]^T (+ bias[N]), bf16 inputs, float32
+ * accumulation, y bf16 (rounded once, to nearest even) or float32 (y_dtype
+ * DKV_BF16 / DKV_F32); bias bf16 or NULL. N a multiple of 16, K of 32; x, w,
+ * y 16-byte aligned, bias 8-byte aligned. K is cut into chunks fixed by
+ * (N, K) alone; every output is one in-order chain of MFMA steps per chunk,
+ * the chunk sums are added in chunk order and the bias last, so a row's
+ * result is the same for any M and any launch shape (verify and one-token
+ * decode agree bit for bit). work: dkv_gemm_bf16_workspace() bytes (0: none
+ * needed)  -- the x @ W (+ b) products of the bf16 model forwards
+ * (model.py:113-133, gpt2.py:191-213, llama.py:187-225) */
+size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K);
+int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int32_t M, int32_t N, int32_t K, void* y,
+                  int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream);
 
 /* ---------------------------------------------------------------- misc */
 const char* dkv_last_error(void);

@@ -123,6 +123,40 @@ def test_paged_attention_matches_oracle(dev, dtype, Hq, Hkv, D, chunk):
         np.testing.assert_allclose(out[s], ref, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("dtype,Hq,Hkv,D", [("f32", 4, 2, 16), ("bf16", 8, 2, 128), ("bf16", 4, 4, 64),
+                                            ("f32", 32, 8, 128)])
+def test_paged_attention_ignores_rows_past_count(dev, dtype, Hq, Hkv, D):
+    """A ragged forward (a prefill of prompts of different lengths): sequence
+    s appends count[s] of the T rows, and the positions past start + count
+    hold whatever the pool held before -- here NaN bytes. Valid rows must
+    match the oracle over the appended keys alone (a masked key's V times a
+    zero probability would be NaN), padding rows must stay finite, and a
+    sequence that appended nothing reads zeros."""
+    draftkv, _ = _dk()
+    rng = np.random.default_rng(D + Hq)
+    b, T = 3, 40
+    counts = [40, 23, 0]
+    pc = draftkv.PagedKVCache(1, Hkv, D, 16, 64, dtype="bf16" if dtype == "bf16" else np.float32, batch=b,
+                              chunk_keys=32)
+    pc.store.view(torch.uint8).fill_(0xFF)            # stale NaN in every page
+    pc.reserve(counts)
+    k = rng.standard_normal((b, T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((b, T, Hkv, D)).astype(np.float32)
+    if dtype == "bf16":
+        k, v = _bf16(k), _bf16(v)
+    st0 = torch.zeros(b, dtype=torch.int32, device=dev)
+    cnt = torch.tensor(counts, dtype=torch.int32, device=dev)
+    pc.append_layer(0, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev), st0, cnt)
+    q = rng.standard_normal((b, T, Hq, D)).astype(np.float32)
+    out = pc.attend(0, torch.from_numpy(q).to(dev), st0, max_len=T, count=cnt).cpu().numpy()
+    assert np.isfinite(out).all()
+    for s, m in enumerate(counts):
+        if m:
+            ref, _, _ = attend(q[s, :m], k[s, :m], v[s, :m], np.arange(m), np.arange(m), Hq // Hkv)
+            np.testing.assert_allclose(out[s, :m], ref, rtol=RTOL, atol=ATOL)
+    assert not out[2].any()
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("Hq,Hkv,D,g,n", [(8, 2, 64, 8, 700), (32, 8, 128, 16, 2600), (9, 3, 64, 4, 1030),
                                           (4, 4, 128, 1, 64)])

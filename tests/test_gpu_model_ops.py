@@ -123,6 +123,53 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
     assert torch.equal(one[0], out[r])
 
 
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 64, 128, False), (5, 96, 160, True), (17, 6144, 4096, False),
+                                             (32, 4096, 4096, True), (33, 512, 14336, False),
+                                             (96, 6144, 4096, True), (200, 1024, 2048, False), (64, 272, 96, True),
+                                             (544, 4096, 4096, False)])
+def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
+    """bf16 x @ W^T (+ b) against the float32 product of the same bf16 values
+    (one rounding to bf16 apart), float32 output too, and every row equal to
+    the same row computed alone or in a smaller batch, bit for bit. The
+    shapes take every launch plan: one or two W fragments per wave, x tiles
+    of 16 to 128 rows, several M tiles, K chunks split over workgroups
+    (partials + ordered reduce) or summed inside one, 128-k blocks and the
+    32-k tail."""
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    w = (0.05 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+    bias = torch.randn((N,), generator=g, device=dev).to(torch.bfloat16) if with_bias else None
+    ref = x.float() @ w.float().t()
+    if bias is not None:
+        ref = ref + bias.float()
+    y = ops.gemm_bf16(x, w, bias)
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    # one rounding of a float32 sum: within 2^-8 relative plus the sum's own error
+    torch.testing.assert_close(y.float(), ref, rtol=2 ** -8, atol=1e-3 * math.sqrt(K / 128))
+    y32 = ops.gemm_bf16(x, w, bias, out_dtype=torch.float32)
+    torch.testing.assert_close(y32, ref, rtol=1e-5, atol=2e-4 * math.sqrt(K / 128))
+    assert torch.equal(y32.to(torch.bfloat16), y)
+    for r in sorted({0, M // 2, M - 1}):
+        one = ops.gemm_bf16(x[r:r + 1].contiguous(), w, bias)
+        assert torch.equal(one[0], y[r])
+    if M > 17:
+        part = ops.gemm_bf16(x[3:17].contiguous(), w, bias)
+        assert torch.equal(part, y[3:17])
+
+
+def test_gemm_bf16_rejects_unsupported_operands(dev):
+    ops = _ops()
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(x, torch.zeros((40, 64), dtype=torch.bfloat16, device=dev))    # N % 16
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(x[:, :48].contiguous(), torch.zeros((32, 48), dtype=torch.bfloat16, device=dev))   # K % 32
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(x, torch.zeros((32, 64), dtype=torch.bfloat16, device=dev),
+                      torch.zeros((32,), dtype=torch.float32, device=dev))            # bias dtype
+
+
 def test_embed_with_positions(dev):
     ops = _ops()
     g = torch.Generator(device=dev).manual_seed(3)

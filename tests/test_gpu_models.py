@@ -190,6 +190,40 @@ def test_controller_driven_run_is_lossless(dev, tiny_setup):
     assert r.verify_passes <= r.new_tokens
 
 
+@pytest.mark.parametrize("attn_bias", [False, True])
+def test_bf16_verify_block_equals_decode_rows(dev, attn_bias):
+    """The bf16 forward (MFMA GEMMs with K chunks fixed by the shape, per-row
+    norms, batch-invariant verify attention) is batch-invariant too: T rows
+    in one pass == T one-row passes, bit for bit."""
+    from draftkv.llama import LlamaLike, demo_llama_weights
+    w, c = demo_llama_weights(attn_sharpness=1.0, attn_gain=1.0, attn_bias=attn_bias)
+    g = LlamaLike(w, c, dtype=torch.bfloat16)
+    toks = np.array(_prompt(6, 40, c["vocab_size"]))
+    a, b = g.new_cache(), g.new_cache()
+    g.forward(toks[:31], a, 0)
+    g.forward(toks[:31], b, 0)
+    block = g.forward(toks[31:], a, 31)
+    rows = np.stack([g.forward(toks[31 + i: 32 + i], b, 31 + i)[0] for i in range(9)])
+    assert np.array_equal(block.view(np.uint32), rows.view(np.uint32))
+
+
+@pytest.mark.parametrize("attn_bias", [False, True])
+def test_bf16_greedy_output_identical(dev, attn_bias):
+    """Greedy losslessness with bf16 weights and a bf16 paged cache: the
+    speculative output equals full-KV decoding token for token, for several
+    drafter arms and gammas."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    from draftkv.llama import LlamaLike, demo_llama_weights
+    w, c = demo_llama_weights(attn_sharpness=1.0, attn_gain=1.0, attn_bias=attn_bias)
+    g = LlamaLike(w, c, dtype=torch.bfloat16)
+    prompt = _prompt(7, 150, c["vocab_size"])
+    base = DraftKVEngine(g, seed=0).generate_baseline(prompt, 40, 0.0)
+    for cfg, gamma in ((CompressionConfig(8, 1.0), 3), (CompressionConfig(4, 0.5, group=32, scale_fp16=True), 6),
+                       (CompressionConfig(2, 0.25), 4)):
+        r = DraftKVEngine(g, FixedPolicy(cfg, gamma), seed=0).generate(prompt, 40, 0.0)
+        assert r.tokens == base, f"bf16 {cfg.label()} gamma={gamma} diverged from full-KV decoding"
+
+
 def test_bf16_llama_runs_and_is_self_consistent(dev):
     """bf16 weights + bf16 paged cache (the serving configuration): logits stay
     close to the float32 model and speculative decoding runs end to end."""
