@@ -230,6 +230,124 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
         }
 }
 
+// Small M (x tile of 16*MB rows, M <= 16*MB): a workgroup of RW*CW waves owns
+// RW 16-row fragments of W; the CW waves of a fragment take its chunks
+// cg, cg + CW, ... and stream each chunk's W rows and x straight into
+// registers, PD blocks ahead. Each chunk's sum goes to LDS; the fragment's
+// first wave adds them in chunk order (then the bias) and writes y -- the
+// same additions as the other plans, with no partials in HBM and no second
+// kernel. Requires S % CW == 0 and chunks of whole 128-k blocks.
+template <int RW, int CW, int MB>
+__global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs a) {
+    constexpr int PD = 4;
+    extern __shared__ __align__(16) float red[];   // [S][RW][MB][64 lanes][4]
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int fr = wave % RW, cg = wave / RW;
+    const int col = lane % 16, q = lane / 16;
+    const int n0 = (blockIdx.x * RW + fr) * 16;
+    const bool live = n0 < a.N;   // wave-uniform
+    const int K = a.K, KC = a.KC, S = a.S;
+    const int nb = KC / GKB, G = nb * (S / CW);
+    const uint16_t* wrow = a.w + (int64_t)(live ? n0 + col : col) * K + 8 * q;
+    const uint16_t* xrow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) xrow[mb] = a.x + (int64_t)min(16 * mb + col, a.M - 1) * K + 8 * q;
+    // block gb of this wave: chunk cg + CW * (gb / nb), k start, 32-k steps
+    auto blk_k = [&](int gb) {
+        const int cl = gb / nb;
+        return (cg + CW * cl) * KC + (gb - cl * nb) * GKB;
+    };
+    // unconditional loads (clamped), as in gemm_bf16_kernel
+#define DKV_SLOAD(WD, XD, GB)                                                                                   \
+    do {                                                                                                        \
+        const int k_ = blk_k(GB);                                                                               \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                        \
+            const int kj = k_ + 32 * j;                                                                         \
+            WD[j] = *reinterpret_cast<const gu32x4_t*>(wrow + kj);                                            \
+            _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) XD[mb][j] =                                      \
+                *reinterpret_cast<const gu32x4_t*>(xrow[mb] + kj);                                            \
+        }                                                                                                       \
+    } while (0)
+    gu32x4_t w0[4], w1[4], w2[4], w3[4], x0[MB][4], x1[MB][4], x2[MB][4], x3[MB][4];
+    gf32x4_t acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+    DKV_SLOAD(w0, x0, 0);
+    DKV_SLOAD(w1, x1, min(1, G - 1));
+    DKV_SLOAD(w2, x2, min(2, G - 1));
+#define DKV_SBLOCK(WC, XC, WN, XN)                                                                              \
+    do {                                                                                                        \
+        const int gb = g0 + v_;                                                                                 \
+        DKV_SLOAD(WN, XN, min(gb + PD - 1, G - 1));                                                             \
+        if (gb < G) {                                                                                           \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                     \
+                _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) acc[mb] =                                     \
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(WC[j]), as_bf16x8(XC[mb][j]), acc[mb],    \
+                                                            0, 0, 0);                                           \
+            }                                                                                                   \
+            if ((gb + 1) % nb == 0) { /* a chunk ends: park its sum */                                         \
+                const int c = cg + CW * (gb / nb);                                                              \
+                _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                             \
+                    *reinterpret_cast<gf32x4_t*>(red + ((((int64_t)c * RW + fr) * MB + mb) * WAVE + lane) * 4) = \
+                        acc[mb];                                                                                \
+                    acc[mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};                                                     \
+                }                                                                                               \
+            }                                                                                                   \
+        }                                                                                                       \
+    } while (0)
+    for (int g0 = 0; g0 < G; g0 += PD) {
+        {
+            constexpr int v_ = 0;
+            DKV_SBLOCK(w0, x0, w3, x3);
+        }
+        {
+            constexpr int v_ = 1;
+            DKV_SBLOCK(w1, x1, w0, x0);
+        }
+        {
+            constexpr int v_ = 2;
+            DKV_SBLOCK(w2, x2, w1, x1);
+        }
+        {
+            constexpr int v_ = 3;
+            DKV_SBLOCK(w3, x3, w2, x2);
+        }
+    }
+#undef DKV_SBLOCK
+#undef DKV_SLOAD
+    __syncthreads();
+    if (!live || cg != 0) return;
+    // outputs (m, n0 + 4q .. 4q + 3), m = 16 mb + col: the chunk sums in chunk order, then the bias
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int m = 16 * mb + col;
+        gf32x4_t t = *reinterpret_cast<const gf32x4_t*>(red + (((int64_t)fr * MB + mb) * WAVE + lane) * 4);
+        for (int c = 1; c < S; ++c) {
+            const gf32x4_t u =
+                *reinterpret_cast<const gf32x4_t*>(red + ((((int64_t)c * RW + fr) * MB + mb) * WAVE + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] = t[e] + u[e];
+        }
+        if (m >= a.M) continue;
+        const int n = n0 + 4 * q;
+        if (a.bias) {
+            const float4 bv = bias4(a.bias, n);
+            t[0] = t[0] + bv.x;
+            t[1] = t[1] + bv.y;
+            t[2] = t[2] + bv.z;
+            t[3] = t[3] + bv.w;
+        }
+        const int64_t o = (int64_t)m * a.N + n;
+        if (a.y_f32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
+        } else {
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + o) =
+                make_uint2(bf16_pair_rne(t[0], t[1]), bf16_pair_rne(t[2], t[3]));
+        }
+    }
+}
+
 // y = sum of the K chunks' partials, in chunk order, then the bias; 4 outputs per thread
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, int64_t MN, int S, int N,
                                                           const uint16_t* __restrict__ bias, void* __restrict__ y,
@@ -271,11 +389,19 @@ static int gemm_chunks(int N, int K) {
 // wave, x rows per tile, and whether the chunks are split across workgroups.
 struct GemmPlan {
     int nw, mb, m_tiles, n_tiles, c_per;
+    int small, rw, cw;   // gemm_bf16_small_kernel: RW fragments x CW chunk groups per workgroup
 };
 
 static GemmPlan gemm_plan(int M, int N, int K) {
     GemmPlan p;
     const int S = gemm_chunks(N, K);
+    p.small = 0;
+    if (M <= 8 && S >= 4) {   // a few rows and a chunked K: split K inside the workgroup
+        p.small = 1, p.nw = 1, p.mb = 1, p.m_tiles = 1, p.c_per = S;
+        p.cw = 4, p.rw = 1;
+        p.n_tiles = N / 16;
+        return p;
+    }
     // from M = 33 on, two W fragments per wave (each x fragment read from LDS feeds two MFMAs) wherever
     // whole 32-row fragments and 128-k blocks allow; the x tile just covers M up to 128 rows (measured
     // on the Llama-3-8B projection and head shapes, weights streamed cold from HBM)
@@ -296,7 +422,13 @@ extern "C" size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const int S = gemm_chunks(N, K);
     const GemmPlan p = gemm_plan(M, N, K);
-    return p.c_per == 1 && S > 1 ? sizeof(float) * (size_t)S * M * N : 0;
+    return !p.small && p.c_per == 1 && S > 1 ? sizeof(float) * (size_t)S * M * N : 0;
+}
+
+template <int RW, int CW, int MB>
+static void launch_small(const GemmArgs& a, int n_wg, hipStream_t st) {
+    const size_t lds = sizeof(float) * 4 * WAVE * (size_t)a.S * RW * MB;
+    hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
 }
 
 template <int NW, int MB, bool PARTIAL>
@@ -338,10 +470,15 @@ extern "C" int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int
     a.part = need ? static_cast<float*>(work) : nullptr;
     a.y = y;
     a.y_f32 = y_dtype == DKV_F32;
+    hipStream_t st = as_stream(stream);
+    if (p.small) {
+        DKV_REQUIRE((int64_t)S * p.rw * p.mb * 4 * WAVE * sizeof(float) <= 64 * 1024, "dkv_gemm_bf16: too many K chunks");
+        launch_small<1, 4, 1>(a, p.n_tiles, st);   // S >= 4, a power of two; chunks of whole 128-k blocks
+        return check_launch("dkv_gemm_bf16");
+    }
     const int64_t nwg = (int64_t)(a.units + 7) / 8 * 8 * p.m_tiles;
     DKV_REQUIRE(nwg < (int64_t)1 << 31, "dkv_gemm_bf16: too many workgroups");
     const dim3 grid((unsigned)nwg);
-    hipStream_t st = as_stream(stream);
     if (p.nw == 2 && p.mb == 4) launch_gemm<2, 4, false>(a, grid, st);   // K % 128 == 0 with two fragments
     else if (p.nw == 2) launch_gemm<2, 8, false>(a, grid, st);
     else if (p.mb == 1) launch_gemm<1, 1>(a, grid, st);

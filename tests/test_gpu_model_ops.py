@@ -123,7 +123,8 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
     assert torch.equal(one[0], out[r])
 
 
-@pytest.mark.parametrize("M,N,K,with_bias", [(1, 64, 128, False), (5, 96, 160, True), (17, 6144, 4096, False),
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 64, 128, False), (5, 96, 160, True), (6, 1024, 4096, True),
+                                             (8, 4096, 14336, False), (17, 6144, 4096, False),
                                              (32, 4096, 4096, True), (33, 512, 14336, False),
                                              (96, 6144, 4096, True), (200, 1024, 2048, False), (64, 272, 96, True),
                                              (544, 4096, 4096, False)])
@@ -133,8 +134,9 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     the same row computed alone or in a smaller batch, bit for bit. The
     shapes take every launch plan: one or two W fragments per wave, x tiles
     of 16 to 128 rows, several M tiles, K chunks split over workgroups
-    (partials + ordered reduce) or summed inside one, 128-k blocks and the
-    32-k tail."""
+    (partials + ordered reduce) or summed inside one, the small-M kernel that
+    splits K among the waves of a workgroup, 128-k blocks and the 32-k
+    tail."""
     ops = _ops()
     g = torch.Generator(device=dev).manual_seed(M + N + K)
     x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
