@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--group", type=int, default=32)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-calibrate", action="store_true",
+                    help="choose gamma with the nominal 8 TB/s cost model instead of one fitted to this device")
     ap.add_argument("--eager", action="store_true", help="run the draft steps eagerly (no HIP graphs)")
     return ap.parse_args()
 
@@ -214,8 +216,8 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
             r = rows[:, layer].astype(np.float64)
             cb += reps * drafter_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
             kb += reps * splitk_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
-        # whole calls back to back, then the split-K kernel of each call (its
-        # event pair read after the call, so those calls do not overlap)
+        # whole calls back to back, then the split-K kernel of each call
+        # (again back to back: one event pair per call, summed at the end)
         t = EventTimer(comp, "attend")
         t.on = True
         for _ in range(reps):
@@ -224,15 +226,14 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
         torch.cuda.synchronize()
         t.restore()
         ops.drafter_kernel_timing(True)
-        k_ms = []
         for _ in range(reps):
             for layer in range(L):
                 comp.attend(layer, q)
-                k_ms.append(ops.drafter_kernel_last_ms())
+        k_ms, k_n = ops.drafter_kernel_total_ms()
         ops.drafter_kernel_timing(False)
         torch.cuda.synchronize()
         out[arm] = {"call": [cb, sum(t.times_ms()) * 1e3, len(t.pairs)],
-                    "splitk": [kb, sum(k_ms) * 1e3, len(k_ms)]}
+                    "splitk": [kb, k_ms * 1e3, k_n]}
     return out
 
 
@@ -350,7 +351,9 @@ def blas_threads() -> int:
 class ScheduledArms:
     """Arms switched on a fixed schedule (every ``period`` rounds), gamma chosen
     each round by the cost model from a decayed Beta posterior of the current
-    arm's per-token acceptance (the controller protocol, controller.py:29-33)."""
+    arm's per-token acceptance (the controller protocol, controller.py:29-33).
+    Gamma 0 -- a plain full-KV step -- when no draft length beats it, as the
+    reference's controller declines to draft (controller.py:149-152)."""
 
     def __init__(self, arms, period, cost, ctx, gamma_max=16, decay=0.98):
         from draftkv.throughput import best_gamma
@@ -368,7 +371,7 @@ class ScheduledArms:
         self.round += 1
         self.gammas.append(g)
         self.last_arm = arm
-        return arm, max(1, g)
+        return arm, g
 
     def update(self, cfg, gamma, accepted, ctx, key=None):
         p = self.post[cfg]
@@ -381,6 +384,7 @@ def run_e2e(args):
     import torch
     from draftkv import CompressionConfig, CostModel, DraftKVEngine
     from draftkv import ops
+    from draftkv.calibrate import calibrate
     from draftkv.compress import _budget
     from draftkv.engine import DecodeBatch
     from draftkv.llama import LLAMA3_8B, LlamaLike
@@ -391,7 +395,9 @@ def run_e2e(args):
     b, ctx = args.batch, args.ctx
     gmax = args.gamma
     rounds = args.warmup + args.steps
-    max_new = rounds * (gmax + 1) + args.baseline_steps + 2
+    cal_gammas = (1, min(4, gmax))
+    cal_rounds = 0 if args.no_calibrate else 3 + 2 * (1 + 2 * len(cal_gammas))
+    max_new = rounds * (gmax + 1) + cal_rounds * (max(cal_gammas) + 1) + args.baseline_steps + 2
     log(f"random Llama-3-8B-shape weights ({L} layers, bf16)")
     model = LlamaLike.random(cfgL, seed=0, std=0.02, dtype=torch.bfloat16)
     wbytes = float(sum(t.numel() * t.element_size() for p in model.layers
@@ -413,6 +419,14 @@ def run_e2e(args):
     for _ in range(max(1, args.warmup)):
         batch.step()
     torch.cuda.synchronize()
+    calibrated = None
+    if not args.no_calibrate:
+        # fit the cost model's time terms to this device: full-KV steps, then
+        # each arm at two draft lengths (real decode rounds, before the timed ones)
+        log(f"calibrating the cost model ({cal_rounds} rounds)")
+        calibrated = calibrate(batch, cost, arms, gammas=cal_gammas, reps=2)
+        ctrl.cost = calibrated
+        torch.cuda.synchronize()
     comp = batch.comp
     # drafter calls are timed live when the draft steps run eagerly; replayed
     # draft-step graphs never pass through the Python call, so then the
@@ -493,6 +507,7 @@ def run_e2e(args):
     # ceiling (alpha -> 1, gamma -> inf) and its prediction at the measured
     # acceptance and mean gamma of that arm
     cost_model = {}
+    cost_cal = {}
     for arm, (secs, tok, nr) in arm_time.items():
         st_ = per_arm.get(arm.label(), [0, 0, 0])
         alpha_a = st_[0] / max(st_[1], 1)
@@ -503,6 +518,20 @@ def run_e2e(args):
             "ceiling": cost.ceiling(arm, ctx), "frac_of_ceiling": meas / cost.ceiling(arm, ctx),
             "modeled_speedup": cost.speedup(arm, gam, alpha_a, ctx), "gamma": gam, "alpha": alpha_a,
             "frac_of_modeled": meas / cost.speedup(arm, gam, alpha_a, ctx)}
+        if calibrated is not None:
+            declined = nr - st_[2] // max(b, 1)
+            cost_cal[arm.label()] = {
+                "ceiling": calibrated.ceiling(arm, ctx), "frac_of_ceiling": meas / calibrated.ceiling(arm, ctx),
+                "modeled_speedup": calibrated.speedup(arm, gam, alpha_a, ctx),
+                "frac_of_modeled": meas / calibrated.speedup(arm, gam, alpha_a, ctx),
+                "declined_rounds": declined}
+    if calibrated is not None:
+        cost_cal["params"] = {
+            "bandwidth_GBs": calibrated.bandwidth / 1e9, "full_kv_bandwidth_GBs": calibrated.full_kv_bandwidth / 1e9,
+            "compute_per_token_us": calibrated.compute_per_token * 1e6,
+            "fixed_draft_us": calibrated.fixed_draft * 1e6, "fixed_verify_us": calibrated.fixed_verify * 1e6,
+            "resync_per_token_us": calibrated.resync_per_token * 1e6,
+            "controller_overhead_us": calibrated.controller_overhead * 1e6}
     acc_total = sum(v[0] for v in per_arm.values())
     drafted = sum(v[1] for v in per_arm.values())
     alpha = {k: v[0] / max(v[1], 1) for k, v in per_arm.items()}
@@ -522,7 +551,9 @@ def run_e2e(args):
                 "outlier channels x8 written straight into the paged cache in place of a 32k prefill)",
         "config": {"workload": f"Llama-3-8B-shape decode rounds, batch {b}, ctx {ctx}, drafter arms int8 g64 "
                                f"keep 1.0 / int{args.bits} g{args.group} keep {args.keep} (fp16 scale/zero) "
-                               f"switched every {args.period} rounds, gamma by cost model (max {gmax}), "
+                               f"switched every {args.period} rounds, gamma by cost model (max {gmax}; 0 = a "
+                               f"full-KV step when drafting does not pay; "
+                               f"{'nominal 8 TB/s' if calibrated is None else 'fitted to this device'}), "
                                f"T {args.temperature} rejection sampling, 16-token pages, shuffled block tables",
                    "layers": L, "batch": b, "ctx": ctx, "temperature": args.temperature,
                    "rounds_per_arm": {k: v[2] // b for k, v in per_arm.items()},
@@ -531,7 +562,8 @@ def run_e2e(args):
                    "tokens_per_round": emitted / args.steps / b,
                    "full_kv_decode_tok_s": base_tps, "speedup_vs_full_kv_decode": value / base_tps,
                    "requantize_ms": [round(t, 3) for t in t_req.times_ms()],
-                   "draft_graphs": batch.use_graphs, "cost_model_8tbs": cost_model},
+                   "draft_graphs": batch.use_graphs, "cost_model_8tbs": cost_model,
+                   "cost_model_calibrated": cost_cal if calibrated is not None else None},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": "profiles/attention_hbm_traffic_b32_ctx32k.md (FETCH_SIZE x 2.0 + "

@@ -1,4 +1,4 @@
-// (a10) sampling and (a11) the verify decision.
+// Sampling and the verify decision.
 // Reference: draftkv/engine.py:36-41 (`_probs`), :101-106 (`_sample`),
 // :188-213 (accept loop, bonus token, residual resample).
 //

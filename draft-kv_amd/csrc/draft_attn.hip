@@ -1,4 +1,4 @@
-// (a5, a6) Drafter attention over the compressed mirror.
+// Drafter attention over the compressed mirror.
 // Reference: the read + einsum + softmax + note_attention of the model
 // forwards against CompressedKVCache (draftkv/compress.py:135-151,
 // draftkv/llama.py:202-218, gpt2.py:197-206, model.py:117-127).
@@ -909,25 +909,48 @@ static DraftWork draft_work(const dkv_drafter_t& m, int n_q_heads, int want_mass
 }
 
 // Measurement hook: when on, dkv_drafter_attention records a pair of HIP
-// events around its split-K kernel on the launch stream.
+// events around its split-K kernel on the launch stream, into the next of
+// TIMING_PAIRS slots (the last slot is reused once they run out).
+constexpr int TIMING_PAIRS = 1024;
 static bool g_time_splitk = false;
-static hipEvent_t g_splitk_ev[2] = {nullptr, nullptr};
+static int g_timed = 0;   // pairs recorded since timing was switched on
+static hipEvent_t g_splitk_ev[2][TIMING_PAIRS] = {};
+
+static int timing_slot() { return g_timed < TIMING_PAIRS ? g_timed : TIMING_PAIRS - 1; }
 
 extern "C" int dkv_drafter_kernel_timing(int32_t on) {
-    if (on && !g_splitk_ev[0]) {
-        if (hipEventCreate(&g_splitk_ev[0]) != hipSuccess || hipEventCreate(&g_splitk_ev[1]) != hipSuccess)
-            return fail(DKV_ELAUNCH, "dkv_drafter_kernel_timing: cannot create events");
+    if (on && !g_splitk_ev[0][0]) {
+        for (int i = 0; i < TIMING_PAIRS; ++i)
+            if (hipEventCreate(&g_splitk_ev[0][i]) != hipSuccess || hipEventCreate(&g_splitk_ev[1][i]) != hipSuccess)
+                return fail(DKV_ELAUNCH, "dkv_drafter_kernel_timing: cannot create events");
     }
+    if (on) g_timed = 0;
     g_time_splitk = on != 0;
     return DKV_OK;
 }
 
 extern "C" float dkv_drafter_kernel_last_ms(void) {
     float ms = -1.0f;
-    if (!g_splitk_ev[1] || hipEventSynchronize(g_splitk_ev[1]) != hipSuccess ||
-        hipEventElapsedTime(&ms, g_splitk_ev[0], g_splitk_ev[1]) != hipSuccess)
+    if (g_timed == 0) return -1.0f;
+    const int i = min(g_timed, TIMING_PAIRS) - 1;
+    if (hipEventSynchronize(g_splitk_ev[1][i]) != hipSuccess ||
+        hipEventElapsedTime(&ms, g_splitk_ev[0][i], g_splitk_ev[1][i]) != hipSuccess)
         return -1.0f;
     return ms;
+}
+
+extern "C" float dkv_drafter_kernel_total_ms(int32_t* n_pairs) {
+    const int n = min(g_timed, TIMING_PAIRS);
+    if (n_pairs) *n_pairs = n;
+    if (n == 0) return 0.0f;
+    if (hipEventSynchronize(g_splitk_ev[1][n - 1]) != hipSuccess) return -1.0f;
+    double total = 0.0;
+    for (int i = 0; i < n; ++i) {
+        float ms;
+        if (hipEventElapsedTime(&ms, g_splitk_ev[0][i], g_splitk_ev[1][i]) != hipSuccess) return -1.0f;
+        total += ms;
+    }
+    return static_cast<float>(total);
 }
 
 extern "C" size_t dkv_drafter_attention_workspace(const dkv_drafter_t* mirror, int32_t n_q_heads,
@@ -962,7 +985,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     hipStream_t st = as_stream(stream);
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
     int unit = rps;     // rows per unit of work that owns a partial slot
-    if (g_time_splitk) hipEventRecord(g_splitk_ev[0], st);
+    const int tslot = timing_slot();
+    if (g_time_splitk) hipEventRecord(g_splitk_ev[0][tslot], st);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
         // blocks of 4 waves; each wave walks splits blockIdx.x*4 + wave, +
@@ -1029,7 +1053,10 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
                            m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
     }
-    if (g_time_splitk) hipEventRecord(g_splitk_ev[1], st);
+    if (g_time_splitk) {
+        hipEventRecord(g_splitk_ev[1][tslot], st);
+        if (g_timed < TIMING_PAIRS) ++g_timed;
+    }
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
     // one wave of the combine per 8 partials, up to 16 waves

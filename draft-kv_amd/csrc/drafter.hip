@@ -1,5 +1,5 @@
-// Drafter mirror maintenance: (a1,a3,a4) append + evict, (a9) truncate and
-// per-round resync, (c) rebuild under a new arm, and a gather for `read`.
+// Drafter mirror maintenance: append + evict, truncate and
+// per-round resync, rebuild under a new arm, and a gather for `read`.
 // Reference: draftkv/compress.py:95-241.
 //
 // Storage (mirror_layout.h): per (sequence, layer, kv head) a dense run of
@@ -562,7 +562,7 @@ __global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
     if (threadIdx.x == 0) *nrows_p = n;
 }
 
-// ------------------------------------------------------------ rebuild (c)
+// ------------------------------------------------------------ rebuild
 // grid: x = page, y = sequence, z = index into the changed-layer list. All
 // scores restart at 0, so the survivors are the closed form
 // [0, sink) u [n - (B - sink), n); only those rows are quantized, densely and

@@ -23,7 +23,8 @@ typedef float gf32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t gu32x4_t __attribute__((ext_vector_type(4)));   // a native vector: copies stay in registers
 
 constexpr int GKB = 128;            // k per block: four 32-k MFMA steps
-constexpr int GX_ROW = GKB + 8;     // LDS row of a staged x block (bf16), padded against bank conflicts
+constexpr int GX_ROW = GKB + 8;
+     // LDS row of a staged x block (bf16), padded against bank conflicts
 
 __device__ __forceinline__ gbf16x8_t as_bf16x8(gu32x4_t v) { return __builtin_bit_cast(gbf16x8_t, v); }
 
@@ -57,12 +58,12 @@ struct GemmArgs {
 // One workgroup: 64*NW rows of W (16*NW per wave) against a tile of 16*MB
 // rows of x, over c_per consecutive K chunks. Per 128-k block the tile's x
 // is staged once in LDS (shared by the four waves); each lane streams its W
-// rows straight into registers two blocks ahead (three register sets in
+// rows straight into registers PD - 1 blocks ahead (PD register sets in
 // rotation). MULTI: the chunks' sums are added in chunk order here (the same
 // additions, in the same order, as the reduce kernel applies to partials).
 // PARTIAL: chunks may end in a block of fewer than four 32-k steps (K not a
 // multiple of 128); otherwise every block is whole.
-template <int NW, int MB, bool MULTI, bool PARTIAL>
+template <int NW, int MB, bool MULTI, bool PARTIAL, int PD>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     constexpr int TM = 16 * MB;
     __shared__ __align__(16) uint16_t xs[2][TM][GX_ROW];
@@ -114,19 +115,19 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
 #define DKV_LOAD_W(DST, GB)                                                                                     \
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
-        _Pragma("unroll") for (int f = 0; f < NW; ++f) _Pragma("unroll") for (int j = 0; j < 4; ++j) DST[f][j] = \
-            *reinterpret_cast<const gu32x4_t*>(wrow[f] + k_ + 32 * (PARTIAL ? min(j, st_ - 1) : j));            \
+        _Pragma("unroll") for (int f_ = 0; f_ < NW; ++f_) _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_)       \
+            DST[f_][j_] = *reinterpret_cast<const gu32x4_t*>(wrow[f_] + k_ + 32 * (PARTIAL ? min(j_, st_ - 1) : j_)); \
     } while (0)
-#define DKV_LOAD_X(GB)                                                                                          \
+#define DKV_LOAD_X(XD, GB)                                                                                      \
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
-        _Pragma("unroll") for (int i = 0; i < MB; ++i) xr[i] =                                                 \
-            *reinterpret_cast<const gu32x4_t*>(xsrc[i] + k_ + 8 * (PARTIAL ? min(xc[i], 4 * st_ - 1) : xc[i]));   \
+        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_) XD[i_] = *reinterpret_cast<const gu32x4_t*>(           \
+            xsrc[i_] + k_ + 8 * (PARTIAL ? min(xc[i_], 4 * st_ - 1) : xc[i_]));                                 \
     } while (0)
-#define DKV_STORE_X(BUF)                                                                                        \
+#define DKV_STORE_X(XS, BUF)                                                                                    \
     do {                                                                                                        \
-        _Pragma("unroll") for (int i = 0; i < MB; ++i) *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i] +    \
-                                                                                 8 * xc[i]) = xr[i];            \
+        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_)                                                        \
+            *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i_] + 8 * xc[i_]) = XS[i_];                      \
     } while (0)
 
     gf32x4_t acc[NW][MB], tot[MULTI ? NW : 1][MULTI ? MB : 1];
@@ -135,22 +136,27 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[f][mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    gu32x4_t w0[NW][4], w1[NW][4], w2[NW][4], xr[MB];
-    DKV_LOAD_X(0);
-    DKV_STORE_X(0);
-    DKV_LOAD_W(w0, 0);
-    DKV_LOAD_X(min(1, G - 1));
-    DKV_LOAD_W(w1, min(1, G - 1));
+    // PD register sets of W and of x in rotation: block gb + PD - 1 is fetched while block gb is
+    // multiplied. x is fetched as far ahead as W: loads complete in issue order, so waiting for
+    // x(gb + 1) also waits for every W load issued before it.
+    gu32x4_t wr[PD][NW][4], xr[PD][MB];
+    DKV_LOAD_X(xr[0], 0);
+    DKV_STORE_X(xr[0], 0);
+#pragma unroll
+    for (int pb = 1; pb < PD; ++pb) {
+        DKV_LOAD_X(xr[pb], min(pb, G - 1));
+        DKV_LOAD_W(wr[pb - 1], min(pb - 1, G - 1));
+    }
     __syncthreads();
 
-    // one block: stage x(gb+1), prefetch block gb+2 into NXT (the last block again past the end),
-    // multiply block gb from CUR
-#define DKV_BLOCK(CUR, NXT)                                                                                     \
+    // one block: stage x(gb+1), fetch block gb+PD-1 (the last block again past the end), multiply
+    // block gb
+#define DKV_BLOCK(CUR, XNEXT, NXT, XFETCH)                                                                      \
     do {                                                                                                        \
         const int gb = g0 + v_;                                                                                 \
-        if (gb + 1 < G) DKV_STORE_X((gb + 1) & 1);                                                              \
-        DKV_LOAD_X(min(gb + 2, G - 1));                                                                         \
-        DKV_LOAD_W(NXT, min(gb + 2, G - 1));                                                                    \
+        if (gb + 1 < G) DKV_STORE_X(XNEXT, (gb + 1) & 1);                                                       \
+        DKV_LOAD_X(XFETCH, min(gb + PD - 1, G - 1));                                                            \
+        DKV_LOAD_W(NXT, min(gb + PD - 1, G - 1));                                                               \
         const int st = blk_steps(min(gb, G - 1));                                                               \
         if (live && gb < G) {                                                                                   \
             const uint16_t* xb = &xs[gb & 1][0][0] + col * GX_ROW + 8 * q;                                      \
@@ -180,19 +186,10 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
         __syncthreads();                                                                                        \
     } while (0)
 
-    for (int g0 = 0; g0 < G; g0 += 3) {
-        {
-            constexpr int v_ = 0;
-            DKV_BLOCK(w0, w2);
-        }
-        {
-            constexpr int v_ = 1;
-            DKV_BLOCK(w1, w0);
-        }
-        {
-            constexpr int v_ = 2;
-            DKV_BLOCK(w2, w1);
-        }
+    for (int g0 = 0; g0 < G; g0 += PD) {
+#pragma unroll
+        for (int v_ = 0; v_ < PD; ++v_)
+            DKV_BLOCK(wr[v_], xr[(v_ + 1) % PD], wr[(v_ + PD - 1) % PD], xr[(v_ + PD - 1) % PD]);
     }
 #undef DKV_BLOCK
 #undef DKV_STORE_X
@@ -262,11 +259,11 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
 #define DKV_SLOAD(WD, XD, GB)                                                                                   \
     do {                                                                                                        \
         const int k_ = blk_k(GB);                                                                               \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                        \
-            const int kj = k_ + 32 * j;                                                                         \
-            WD[j] = *reinterpret_cast<const gu32x4_t*>(wrow + kj);                                            \
-            _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) XD[mb][j] =                                      \
-                *reinterpret_cast<const gu32x4_t*>(xrow[mb] + kj);                                            \
+        _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                                     \
+            const int kj = k_ + 32 * j_;                                                                        \
+            WD[j_] = *reinterpret_cast<const gu32x4_t*>(wrow + kj);                                           \
+            _Pragma("unroll") for (int m_ = 0; m_ < MB; ++m_) XD[m_][j_] =                                     \
+                *reinterpret_cast<const gu32x4_t*>(xrow[m_] + kj);                                            \
         }                                                                                                       \
     } while (0)
     gu32x4_t w0[4], w1[4], w2[4], w3[4], x0[MB][4], x1[MB][4], x2[MB][4], x3[MB][4];
@@ -433,8 +430,9 @@ static void launch_small(const GemmArgs& a, int n_wg, hipStream_t st) {
 
 template <int NW, int MB, bool PARTIAL>
 static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
-    if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL>), grid, dim3(256), 0, st, a);
+    constexpr int PD = 3;   // register sets in rotation (4 measured no faster: fewer waves fit)
+    if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD>), grid, dim3(256), 0, st, a);
 }
 
 template <int NW, int MB>

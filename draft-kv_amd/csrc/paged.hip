@@ -1,4 +1,4 @@
-// (a7) paged full-cache append and (a8) causal attention over it.
+// Paged full-cache append and causal attention over it.
 // Reference: draftkv/paged.py:76-176 (cache), draftkv/llama.py:202-218 and
 // gpt2.py/model.py equivalents (read + masked softmax attention).
 #include <algorithm>

@@ -1,4 +1,4 @@
-// (a1) Group quantizer on contiguous rows -- reference draftkv/compress.py:21-46.
+// Group quantizer on contiguous rows -- reference draftkv/compress.py:21-46.
 #include "dkv_common.h"
 
 namespace dkv {

@@ -52,6 +52,7 @@ _SIGS = {
     "dkv_drafter_attention": (C.c_int, [PDrafter, I32, QCfg, P, I32, I32, P, P, SZ, P]),
     "dkv_drafter_kernel_timing": (C.c_int, [I32]),
     "dkv_drafter_kernel_last_ms": (F32, []),
+    "dkv_drafter_kernel_total_ms": (F32, [P]),
     "dkv_drafter_gather": (C.c_int, [PDrafter, I32, I32, QCfg, I32, P, P, P, P, P, P, P, P, P, P]),
     "dkv_sample_workspace": (SZ, [I32, I32]),
     "dkv_sample": (C.c_int, [P, I64, I32, I32, F32, P, P, P, SZ, P]),

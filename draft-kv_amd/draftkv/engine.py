@@ -22,6 +22,7 @@ consumed, so the stream stays where the reference's would be.
 
 from __future__ import annotations
 
+import time
 import warnings
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -220,6 +221,7 @@ class DecodeBatch:
         self._pool = None
         self._pending_key = None
         self.last_draft = None            # (tokens, logits) of the last round's draft steps
+        self.phases = None                # a calibrate.PhaseLog to record per-round phase times
 
     def _sync(self, start) -> None:
         self.comp.sync_from(self.full, start)
@@ -284,17 +286,31 @@ class DecodeBatch:
         gamma = min(int(gamma), max(int(budget.max()) - 1, 0))
         flen = full.lengths()
 
+        ph, ev = self.phases, {}
         if gamma <= 0:
-            logits = model.forward_batch(eng._pending(toks)[:, None], full, n - 1, act)[:, 0]
             u = np.array([eng._g(s).random() if active[s] else 0.5 for s in range(b)])
-            tok = ops.sample(logits, T, ops.to_device(u, dev)).cpu().numpy()
+            u_d = ops.to_device(u, dev)
+            if ph is not None:
+                ev["d1"] = ph.event()
+            logits = model.forward_batch(eng._pending(toks)[:, None], full, n - 1, act)[:, 0]
+            tok = ops.sample(logits, T, u_d)
+            if ph is not None:
+                ev["v1"] = ph.event()
+            tok = tok.cpu().numpy()
+            h0 = time.perf_counter()
             for s in np.flatnonzero(active):
                 toks[s].append(int(tok[s]))
                 res[s].verify_passes += 1
                 res[s].rounds.append(RoundLog(cfg, 0, 0, 1, int(n[s])))
             self.last_emitted = int(active.sum())
+            hs = time.perf_counter() - h0
+            if ph is not None:
+                ev["s0"] = ph.event()
             if self.comp is not None:
                 self._sync(np.where(active, n - 1, full.lengths()))
+            if ph is not None:
+                ev["end"] = ph.event()
+                ph.add(cfg, 0, ev, self.last_emitted, hs)
             return True
 
         # -- drafter's cache: build once, then rebuild only the layers that changed
@@ -339,6 +355,8 @@ class DecodeBatch:
         # layout's first round step 0 runs eagerly (warming every kernel and GEMM
         # shape) and the graph is recorded after it
         n_eager = gamma if graph is None else (1 if graph is _RECORD else 0)
+        if ph is not None:
+            ev["d0"] = ph.event()
         for i in range(n_eager):
             lg = model.forward_batch(x[:, None], comp, n - 1 + i, act)[:, 0]
             if draft_logits is not None:
@@ -351,14 +369,19 @@ class DecodeBatch:
             graph.run(x, [n - 1 + i for i in range(n_eager, gamma)], act, u_draft[n_eager:], draft_tok,
                       draft_logits, col0=n_eager)
         self.last_draft = (draft_tok, draft_logits)
+        if ph is not None:
+            ev["d1"] = ph.event()
 
         # -- verify
         block = torch.cat([pending[:, None], draft_tok], 1).contiguous()
         logits = model.forward_batch(block, full, n - 1, act * (gamma + 1))
         acc, nxt, used = ops.accept(logits, draft_logits, draft_tok, T, u_ver_d)
+        if ph is not None:
+            ev["v1"] = ph.event()
         host = torch.cat([torch.stack([acc, nxt, used], 1), draft_tok], 1).cpu().numpy()
 
         # -- bookkeeping, rollback, resync
+        h0 = time.perf_counter()
         cut = flen.copy()
         emitted_total = 0
         for s in np.flatnonzero(active):
@@ -374,7 +397,13 @@ class DecodeBatch:
             res[s].rounds.append(RoundLog(cfg, gamma, a, len(emitted), int(n[s])))
             res[s].draft_steps += gamma
             res[s].verify_passes += 1
+        hs = time.perf_counter() - h0
+        if ph is not None:
+            ev["s0"] = ph.event()
         full.truncate(cut)
         self._sync(np.where(active, n - 1, full.lengths()))
         self.last_emitted = emitted_total
+        if ph is not None:
+            ev["end"] = ph.event()
+            ph.add(cfg, gamma, ev, emitted_total, hs)
         return True

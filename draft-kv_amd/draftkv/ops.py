@@ -119,7 +119,7 @@ def qcfg(bits: int, group: int = 64, meta_f16: bool = False, sink: int = 4, rece
     return QCfg(int(bits), int(group), int(bool(meta_f16)), int(sink), int(recent))
 
 
-# ------------------------------------------------------------------ (a1)
+# ------------------------------------------------------------------ quantize
 def quantize_codes(x: torch.Tensor, bits: int, group: int = 64, meta_f16: bool = False):
     """Group quantization of the last axis (reference compress.py:21-46).
     Returns (codes u8, scale f32, lo f32, deq f32)."""
@@ -138,7 +138,7 @@ def quantize_codes(x: torch.Tensor, bits: int, group: int = 64, meta_f16: bool =
     return codes, scale, lo, deq
 
 
-# ------------------------------------------------------------------ (a7, a8)
+# ------------------------------------------------------------------ paged full cache
 def paged_append(desc: Paged, layer: int, k: torch.Tensor, v: torch.Tensor, start: torch.Tensor,
                  count: Optional[torch.Tensor] = None) -> None:
     _need(k, "k", ndim=4)
@@ -244,6 +244,14 @@ def drafter_kernel_last_ms() -> float:
     return float(lib().dkv_drafter_kernel_last_ms())
 
 
+def drafter_kernel_total_ms() -> tuple:
+    """(milliseconds, pairs): the summed event pairs recorded since the hook
+    was switched on (at most 1024 calls)."""
+    n = C.c_int32(0)
+    ms = float(lib().dkv_drafter_kernel_total_ms(C.byref(n)))
+    return ms, int(n.value)
+
+
 def drafter_gather(desc: Drafter, seq: int, layer: int, cfg: QCfg, rows: int, device) -> dict:
     H, D = desc.n_kv_heads, desc.head_dim
     ng = 0 if cfg.bits >= 16 else -(-D // cfg.group)
@@ -261,7 +269,7 @@ def drafter_gather(desc: Drafter, seq: int, layer: int, cfg: QCfg, rows: int, de
     return o
 
 
-# ------------------------------------------------------------------ (a10, a11)
+# ------------------------------------------------------------------ sampling and accept
 def sample(logits: torch.Tensor, temperature: float, u: torch.Tensor,
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
     _need(logits, "logits", torch.float32, 2)

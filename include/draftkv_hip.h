@@ -74,7 +74,7 @@ typedef struct {
     int32_t bits, group, meta_f16, sink, recent;
 } dkv_qcfg_t;
 
-/* ---------------------------------------------------------------- (a1) */
+/* ---------------------------------------------------------------- quantize */
 /* Group quantizer on contiguous float32 rows x[rows][d] -- replaces
  * draftkv/compress.py:21-46 (`quantize`). Writes codes u8 [rows][d],
  * scale/lo f32 [rows][ceil(d/group)], deq f32 [rows][d] (any output may be
@@ -83,7 +83,7 @@ int dkv_quantize(const float* x, int64_t rows, int32_t d, int32_t bits, int32_t 
                  int32_t meta_f16, uint8_t* codes, float* scale, float* lo, float* deq,
                  dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a7) */
+/* ---------------------------------------------------------------- paged append */
 /* Write K/V rows into the paged full cache -- replaces
  * draftkv/paged.py:120-128 (`PagedKVCache.append`). k, v: [batch][T][Hkv][D]
  * (in_dtype). Sequence s writes rows t < count[s] at positions start[s]+t;
@@ -93,7 +93,7 @@ int dkv_paged_append(const dkv_paged_t* cache, int32_t layer, const void* k, con
                      int32_t in_dtype, int32_t T, const int32_t* start, const int32_t* count,
                      dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a8) */
+/* ---------------------------------------------------------------- paged attention */
 /* Causal attention of T query rows per sequence over the paged full cache
  * (verify pass, baseline decode, prefill) -- replaces the read + einsum +
  * softmax of draftkv/llama.py:202-218 / gpt2.py:197-206 / model.py:117-127
@@ -114,7 +114,7 @@ int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, const float* q,
                         int32_t max_len, int32_t chunk_keys, float* out, void* work,
                         size_t work_bytes, dkv_stream_t stream);
 
-/* ------------------------------------------------------------ (a1,a3,a4) */
+/* ------------------------------------------------------------ mirror append / evict */
 /* Quantize and append T rows per sequence to one layer of the mirror, then
  * evict down to budget[s] -- replaces draftkv/compress.py:122-133 (`append`)
  * with :154-179 (`budget`, `_evict`). k, v: [batch][T][Hkv][D] (in_dtype);
@@ -127,7 +127,7 @@ int dkv_drafter_append(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t cf
                        const int32_t* start, const int32_t* count, const int32_t* budget,
                        dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a9) */
+/* ---------------------------------------------------------------- mirror truncate / rebuild */
 /* Drop every row at position >= start[s] in all layers -- replaces
  * draftkv/compress.py:181-188 (`truncate`). cfgs: host array of n_layers
  * arms (the row width of each layer). */
@@ -142,7 +142,7 @@ int dkv_drafter_sync(const dkv_drafter_t* mirror, const dkv_paged_t* full, const
                      const int32_t* start, const int32_t* end, const int32_t* budget,
                      dkv_stream_t stream);
 
-/* --------------------------------------------------------------- (c/a9) */
+/* --------------------------------------------------------------- mirror requantize */
 /* Requantize the listed layers from the full cache under new arms -- replaces
  * draftkv/compress.py:209-230 (`rebuild_layers`) and the first build
  * `sync_from(full, 0)`. All scores restart at 0, so the survivors are the
@@ -153,7 +153,7 @@ int dkv_drafter_rebuild(const dkv_drafter_t* mirror, const dkv_paged_t* full,
                         const int32_t* layers, int32_t n_changed, const dkv_qcfg_t* cfgs,
                         const int32_t* len, const int32_t* budget, dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a5,a6) */
+/* ---------------------------------------------------------------- drafter attention */
 /* Drafter attention: one query position per sequence over the live rows of
  * one mirror layer, dequantizing in registers -- replaces the read + einsum
  * + softmax + note_attention of the model forwards against CompressedKVCache
@@ -170,11 +170,16 @@ int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t
 
 /* Measurement hook (no counterpart in the reference; for benchmarks that
  * time the dominant kernel alone): when on, dkv_drafter_attention records
- * a pair of HIP events around its split-K kernel on its launch stream;
- * dkv_drafter_kernel_last_ms waits for the last pair and returns the
- * elapsed milliseconds (-1 when there is none). Not for concurrent callers. */
+ * a pair of HIP events around its split-K kernel on its launch stream, one
+ * pair per call for the first 1024 calls after switching on (later calls
+ * reuse the last pair). dkv_drafter_kernel_last_ms waits for the last pair
+ * and returns its elapsed milliseconds (-1 when there is none);
+ * dkv_drafter_kernel_total_ms sums the recorded pairs (their number to
+ * *n_pairs), so back-to-back calls can be timed with no host wait between
+ * them. Not for concurrent callers. */
 int dkv_drafter_kernel_timing(int32_t on);
 float dkv_drafter_kernel_last_ms(void);
+float dkv_drafter_kernel_total_ms(int32_t* n_pairs);
 
 /* Unpack one layer of one sequence to plain arrays (debug/parity `read`,
  * compress.py:135-142): codes u8 [rows][Hkv][D], scale/lo f32
@@ -186,7 +191,7 @@ int dkv_drafter_gather(const dkv_drafter_t* mirror, int32_t seq, int32_t layer, 
                        uint8_t* v_codes, float* v_scale, float* v_lo, float* v_deq,
                        int32_t* pos, dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a10) */
+/* ---------------------------------------------------------------- sampling */
 /* One draw per row from softmax(logits/T) -- replaces draftkv/engine.py:36-41
  * (`_probs`) + :101-106 (`_sample`). logits f32 rows of length vocab at
  * row_stride; u: f64 uniforms [batch]. T <= 0: first argmax (u unused).
@@ -196,7 +201,7 @@ int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t v
                float temperature, const double* u, int32_t* tokens, void* work,
                size_t work_bytes, dkv_stream_t stream);
 
-/* ---------------------------------------------------------------- (a11) */
+/* ---------------------------------------------------------------- accept */
 /* Verify decision of one round for every sequence -- replaces
  * draftkv/engine.py:188-213. target: f32 [batch][gamma+1][vocab];
  * draft: f32 [batch][gamma][vocab] (the drafter's logits; unused when

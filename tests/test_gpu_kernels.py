@@ -29,7 +29,7 @@ def _bf16(x: np.ndarray) -> np.ndarray:
     return torch.from_numpy(np.ascontiguousarray(x, np.float32)).bfloat16().float().numpy()
 
 
-# ------------------------------------------------------------------ (a1)
+# ------------------------------------------------------------------ quantize
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("d,group", [(16, 64), (64, 64), (128, 32), (80, 64), (40, 32), (128, 128)])
 @pytest.mark.parametrize("meta", ["f32", "f16"])
@@ -56,7 +56,7 @@ def test_quantize_api_numpy_roundtrip(dev):
         assert np.array_equal(draftkv.quantize(x, b), oq(x, b))
 
 
-# ------------------------------------------------------------------ (a7)
+# ------------------------------------------------------------------ paged append
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("block_size", [1, 4, 16, 64])
 def test_paged_tables_and_rows_match_reference(dev, dtype, block_size):
@@ -89,7 +89,7 @@ def test_paged_tables_and_rows_match_reference(dev, dtype, block_size):
             assert np.array_equal(a, b)
 
 
-# ------------------------------------------------------------------ (a8)
+# ------------------------------------------------------------------ paged attention
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (8, 2, 64), (32, 8, 128), (9, 3, 64)])
 @pytest.mark.parametrize("chunk", [32, 64, 512])
@@ -182,7 +182,7 @@ def test_verify_is_batch_invariant_with_decode(dev, dtype, Hq, Hkv, D, g, n):
         assert torch.equal(one[:, 0], ver[:, t]), t
 
 
-# ------------------------------------------------------------------ mirror (a3, a4, a9, c)
+# ------------------------------------------------------------------ mirror maintenance
 def _full_pair(L, H, D, n, rng, dev, dtype=np.float32):
     """An oracle FullKVCache and a device PagedKVCache holding the same rows."""
     import draftkv
@@ -286,7 +286,7 @@ def test_steady_state_eviction_truncate_and_resync(dev, arm):
         assert md.seen_positions == mo.seen_positions
 
 
-# ------------------------------------------------------------------ (a5, a6)
+# ------------------------------------------------------------------ drafter attention
 @pytest.mark.parametrize("arm", [Cfg(8, 1.0), Cfg(4, 0.25, group=32, meta="f16"), Cfg(16, 0.5), Cfg(2, 0.5)],
                          ids=lambda c: f"{c.bits}b{c.keep_frac}")
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (32, 8, 128), (9, 3, 64)])
@@ -331,11 +331,21 @@ def test_splitk_timing_hook_times_each_call(dev):
             k_ms = ops.drafter_kernel_last_ms()
             torch.cuda.synchronize()
             assert 0.0 < k_ms <= s_ev.elapsed_time(e_ev) + 1e-3
+        # back to back: one pair per call, summed once at the end
+        ops.drafter_kernel_timing(True)
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        for _ in range(5):
+            md.attend(0, q, want_mass=True)
+        e_ev.record()
+        total, n = ops.drafter_kernel_total_ms()
+        torch.cuda.synchronize()
+        assert n == 5 and 0.0 < total <= s_ev.elapsed_time(e_ev) + 1e-3
     finally:
         ops.drafter_kernel_timing(False)
 
 
-# ------------------------------------------------------------------ (a10, a11)
+# ------------------------------------------------------------------ sampling and accept
 @pytest.mark.parametrize("V", [128, 50257, 128256])
 @pytest.mark.parametrize("T", [0.0, 0.8, 1.0])
 def test_sample_matches_numpy_choice(dev, V, T):
