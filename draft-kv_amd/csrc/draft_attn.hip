@@ -383,9 +383,16 @@ struct SplitCore {
     // receives the page's scaled logits (rows 4jj+x, 16+4jj+x-4 of column col).
     template <bool TAIL, class Sink>
     __device__ __forceinline__ void page(const Regs& cur, int p0, int r_end, Sink&& sink) {
+        float sv[8];
+        qk(cur, sv);
+        rest<TAIL>(cur, sv, p0, r_end, sink);
+    }
+
+    // The page's scores (unscaled): sv[x] for rows 4jj+x (x < 4) and
+    // 16+4jj+x-4 of column col's head, summed over the head's groups.
+    __device__ __forceinline__ void qk(const Regs& cur, float (&sv)[8]) {
         // ---- QK over the page's two 16-row tiles, folded per (row, group)
         // (the two tiles' MFMA chains interleaved, so each hides the other's latency)
-        float sv[8];
         f32x4_t sa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st) {
@@ -407,6 +414,12 @@ struct SplitCore {
         if (NG >= 2) DKV_DPP_ADD8("row_mirror", sv);            // col ^ 15
         if (NG >= 4) DKV_DPP_ADD8("row_half_mirror", sv);       // col ^ 7
         if (NG >= 8) DKV_DPP_ADD8("quad_perm:[3,2,1,0]", sv);   // col ^ 3
+    }
+
+    // The rest of a page on its scores: scale, mask, hand over the logits,
+    // online softmax, PV.
+    template <bool TAIL, class Sink>
+    __device__ __forceinline__ void rest(const Regs& cur, const float (&sv)[8], int p0, int r_end, Sink&& sink) {
         // scale, mask the tail, hand over, online softmax per column
         float pv[8];
         float mx = -INFINITY;
@@ -753,19 +766,31 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
         else vm_wait(LPP * ahead + SPP * since);
     };
 
-    Regs cur;
-    const int gfull = tail ? T - 1 : T;   // pages computed in the loop (all rows live)
-    for (int g = 0; g < gfull; ++g) {
-        wait_page(g);
+    // Software-pipelined by one page: while page g's softmax and PV run, the
+    // scores of page g+1 are computed from its operands (the two are
+    // independent), so each hides the other's latency. Pages still enter the
+    // softmax in order, so the arithmetic is that of one page at a time.
+    // Waits: when page g+1 is awaited (iteration g, before issuing page
+    // g+S-1), the loads in flight after its own are those of pages
+    // g+2 .. g+S-2 and the logit stores of the pages computed since it was
+    // issued (iterations g-S+2 .. g-1, or all so far for the first pages).
+    Regs ra, rb;
+    float sa_[8], sb_[8];
+    vm_wait(LPP * min(S - 2, T - 1));   // page 0 landed
+    operands(ra);
+    c.qk(ra, sa_);
+    auto step = [&](int g, Regs& cur, float (&scur)[8], Regs& nxt, float (&snxt)[8]) {
+        const bool more = g + 1 < T;                      // wave-uniform
+        if (more) vm_wait(LPP * max(0, min(S - 3, T - 2 - g)) + SPP * min(g, S - 2));
         if (g + S - 1 < T) issue(g + S - 1);
-        operands(cur);
-        c.template page<false>(cur, (pg0 + g) * PAGE, n, store);
-    }
-    if (tail) {
-        const int g = T - 1;
-        wait_page(g);
-        operands(cur);
-        c.template page<true>(cur, (pg0 + g) * PAGE, n, store);
+        if (more) operands(nxt);
+        if (tail && !more) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, store);
+        else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, store);
+        if (more) c.qk(nxt, snxt);
+    };
+    for (int g = 0; g < T; g += 2) {
+        step(g, ra, sa_, rb, sb_);
+        if (g + 1 < T) step(g + 1, rb, sb_, ra, sa_);
     }
     c.finish(part, s, h, Hq, G, n_splits, wid);
 }
