@@ -459,10 +459,11 @@ def run_e2e(args):
     per_arm = {}
     for r in batch.res:
         for x in r.rounds[-args.steps:]:
-            st = per_arm.setdefault(x.cfg.label(), [0, 0, 0])
+            st = per_arm.setdefault(x.cfg.label(), [0, 0, 0, 0])   # accepted, drafted, rounds, declined
             st[0] += x.accepted
             st[1] += x.gamma
             st[2] += 1
+            st[3] += x.gamma == 0
     # drafter attention during the rounds (eager steps only): bytes of each
     # timed call from the rows the mirror held
     live_calls = {}
@@ -509,7 +510,7 @@ def run_e2e(args):
     cost_model = {}
     cost_cal = {}
     for arm, (secs, tok, nr) in arm_time.items():
-        st_ = per_arm.get(arm.label(), [0, 0, 0])
+        st_ = per_arm.get(arm.label(), [0, 0, 0, 0])
         alpha_a = st_[0] / max(st_[1], 1)
         gam = max(1, round(st_[1] / max(st_[2], 1)))
         meas = (tok / secs) / base_tps
@@ -519,7 +520,7 @@ def run_e2e(args):
             "modeled_speedup": cost.speedup(arm, gam, alpha_a, ctx), "gamma": gam, "alpha": alpha_a,
             "frac_of_modeled": meas / cost.speedup(arm, gam, alpha_a, ctx)}
         if calibrated is not None:
-            declined = nr - st_[2] // max(b, 1)
+            declined = st_[3] // max(b, 1)
             cost_cal[arm.label()] = {
                 "ceiling": calibrated.ceiling(arm, ctx), "frac_of_ceiling": meas / calibrated.ceiling(arm, ctx),
                 "modeled_speedup": calibrated.speedup(arm, gam, alpha_a, ctx),

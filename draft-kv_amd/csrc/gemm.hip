@@ -16,6 +16,8 @@
 // row equals the one-token decode row bit for bit.
 #include "dkv_common.h"
 
+#include <type_traits>
+
 namespace dkv {
 
 typedef __bf16 gbf16x8_t __attribute__((ext_vector_type(8)));
@@ -40,8 +42,32 @@ __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// x operands: 8 consecutive elements of a row, bf16 (16 bytes) or float32
+// (32 bytes, kept raw in registers until used, then rounded to bf16 to
+// nearest even -- the rounding of a float32 -> bf16 tensor conversion)
+typedef uint32_t gu32x8_t __attribute__((ext_vector_type(8)));
+template <bool XF32>
+using XRaw = typename std::conditional<XF32, gu32x8_t, gu32x4_t>::type;
+
+template <bool XF32>
+__device__ __forceinline__ XRaw<XF32> load_x8(const void* base, int64_t elem) {
+    if constexpr (XF32) return *reinterpret_cast<const gu32x8_t*>(static_cast<const float*>(base) + elem);
+    else return *reinterpret_cast<const gu32x4_t*>(static_cast<const uint16_t*>(base) + elem);
+}
+
+template <bool XF32>
+__device__ __forceinline__ gu32x4_t x8_bf16(const XRaw<XF32>& r) {
+    if constexpr (XF32)
+        return gu32x4_t{bf16_pair_rne(__uint_as_float(r[0]), __uint_as_float(r[1])),
+                        bf16_pair_rne(__uint_as_float(r[2]), __uint_as_float(r[3])),
+                        bf16_pair_rne(__uint_as_float(r[4]), __uint_as_float(r[5])),
+                        bf16_pair_rne(__uint_as_float(r[6]), __uint_as_float(r[7]))};
+    else return r;
+}
+
 struct GemmArgs {
-    const uint16_t* x;   // [M, K]
+    const void* x;       // [M, K], bf16 or float32 (x_f32)
+    int x_f32;
     const uint16_t* w;   // [N, K]
     const uint16_t* bias;   // [N] bf16 or null, added after the chunk sums
     int M, N, K;
@@ -63,7 +89,7 @@ struct GemmArgs {
 // additions, in the same order, as the reduce kernel applies to partials).
 // PARTIAL: chunks may end in a block of fewer than four 32-k steps (K not a
 // multiple of 128); otherwise every block is whole.
-template <int NW, int MB, bool MULTI, bool PARTIAL, int PD>
+template <int NW, int MB, bool MULTI, bool PARTIAL, int PD, bool XF32>
 __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     constexpr int TM = 16 * MB;
     __shared__ __align__(16) uint16_t xs[2][TM][GX_ROW];
@@ -88,14 +114,14 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     for (int f = 0; f < NW; ++f) wrow[f] = a.w + (int64_t)(live ? n0 + 16 * f + col : col) * K + 8 * q;
     // x piece i of this thread: tile row xr_row[i], k offset 8 xr_c[i] in the block. Tile rows past M
     // reread row M-1 (their outputs are dropped), so every load and LDS write is unconditional.
-    const uint16_t* xsrc[MB];
+    int64_t xsrc[MB];   // element offset of the piece's row in x
     uint32_t xdst[MB];
     int xc[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
         const int p = tid + 256 * i, r = p / 16;
         xc[i] = p % 16;
-        xsrc[i] = a.x + (int64_t)(m0 + min(r, mrows - 1)) * K;
+        xsrc[i] = (int64_t)(m0 + min(r, mrows - 1)) * K;
         xdst[i] = (uint32_t)(r * GX_ROW);
     }
 
@@ -121,13 +147,13 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
 #define DKV_LOAD_X(XD, GB)                                                                                      \
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
-        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_) XD[i_] = *reinterpret_cast<const gu32x4_t*>(           \
-            xsrc[i_] + k_ + 8 * (PARTIAL ? min(xc[i_], 4 * st_ - 1) : xc[i_]));                                 \
+        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_) XD[i_] =                                              \
+            load_x8<XF32>(a.x, xsrc[i_] + k_ + 8 * (PARTIAL ? min(xc[i_], 4 * st_ - 1) : xc[i_]));               \
     } while (0)
 #define DKV_STORE_X(XS, BUF)                                                                                    \
     do {                                                                                                        \
         _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_)                                                        \
-            *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i_] + 8 * xc[i_]) = XS[i_];                      \
+            *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i_] + 8 * xc[i_]) = x8_bf16<XF32>(XS[i_]);       \
     } while (0)
 
     gf32x4_t acc[NW][MB], tot[MULTI ? NW : 1][MULTI ? MB : 1];
@@ -139,7 +165,8 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     // PD register sets of W and of x in rotation: block gb + PD - 1 is fetched while block gb is
     // multiplied. x is fetched as far ahead as W: loads complete in issue order, so waiting for
     // x(gb + 1) also waits for every W load issued before it.
-    gu32x4_t wr[PD][NW][4], xr[PD][MB];
+    gu32x4_t wr[PD][NW][4];
+    XRaw<XF32> xr[PD][MB];
     DKV_LOAD_X(xr[0], 0);
     DKV_STORE_X(xr[0], 0);
 #pragma unroll
@@ -234,7 +261,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
 // first wave adds them in chunk order (then the bias) and writes y -- the
 // same additions as the other plans, with no partials in HBM and no second
 // kernel. Requires S % CW == 0 and chunks of whole 128-k blocks.
-template <int RW, int CW, int MB>
+template <int RW, int CW, int MB, bool XF32>
 __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs a) {
     constexpr int PD = 4;
     extern __shared__ __align__(16) float red[];   // [S][RW][MB][64 lanes][4]
@@ -247,9 +274,9 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
     const int K = a.K, KC = a.KC, S = a.S;
     const int nb = KC / GKB, G = nb * (S / CW);
     const uint16_t* wrow = a.w + (int64_t)(live ? n0 + col : col) * K + 8 * q;
-    const uint16_t* xrow[MB];
+    int64_t xrow[MB];   // element offset of the lane's x row and lane group
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) xrow[mb] = a.x + (int64_t)min(16 * mb + col, a.M - 1) * K + 8 * q;
+    for (int mb = 0; mb < MB; ++mb) xrow[mb] = (int64_t)min(16 * mb + col, a.M - 1) * K + 8 * q;
     // block gb of this wave: chunk cg + CW * (gb / nb), k start, 32-k steps
     auto blk_k = [&](int gb) {
         const int cl = gb / nb;
@@ -262,11 +289,11 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
         _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                                     \
             const int kj = k_ + 32 * j_;                                                                        \
             WD[j_] = *reinterpret_cast<const gu32x4_t*>(wrow + kj);                                           \
-            _Pragma("unroll") for (int m_ = 0; m_ < MB; ++m_) XD[m_][j_] =                                     \
-                *reinterpret_cast<const gu32x4_t*>(xrow[m_] + kj);                                            \
+            _Pragma("unroll") for (int m_ = 0; m_ < MB; ++m_) XD[m_][j_] = load_x8<XF32>(a.x, xrow[m_] + kj);  \
         }                                                                                                       \
     } while (0)
-    gu32x4_t w0[4], w1[4], w2[4], w3[4], x0[MB][4], x1[MB][4], x2[MB][4], x3[MB][4];
+    gu32x4_t w0[4], w1[4], w2[4], w3[4];
+    XRaw<XF32> x0[MB][4], x1[MB][4], x2[MB][4], x3[MB][4];
     gf32x4_t acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -280,8 +307,8 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
         if (gb < G) {                                                                                           \
             _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                     \
                 _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) acc[mb] =                                     \
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(WC[j]), as_bf16x8(XC[mb][j]), acc[mb],    \
-                                                            0, 0, 0);                                           \
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(WC[j]), as_bf16x8(x8_bf16<XF32>(XC[mb][j])), \
+                                                            acc[mb], 0, 0, 0);                                  \
             }                                                                                                   \
             if ((gb + 1) % nb == 0) { /* a chunk ends: park its sum */                                         \
                 const int c = cg + CW * (gb / nb);                                                              \
@@ -425,14 +452,20 @@ extern "C" size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K) {
 template <int RW, int CW, int MB>
 static void launch_small(const GemmArgs& a, int n_wg, hipStream_t st) {
     const size_t lds = sizeof(float) * 4 * WAVE * (size_t)a.S * RW * MB;
-    hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
+    if (a.x_f32) hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, true>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
+    else hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, false>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
 }
 
 template <int NW, int MB, bool PARTIAL>
 static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr int PD = 3;   // register sets in rotation (4 measured no faster: fewer waves fit)
-    if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD>), grid, dim3(256), 0, st, a);
+    if (a.x_f32) {
+        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, true>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, true>), grid, dim3(256), 0, st, a);
+    } else {
+        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, false>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, false>), grid, dim3(256), 0, st, a);
+    }
 }
 
 template <int NW, int MB>
@@ -441,12 +474,13 @@ static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
     else launch_gemm<NW, MB, true>(a, grid, st);
 }
 
-extern "C" int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int32_t M, int32_t N, int32_t K, void* y,
-                             int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream) {
+extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
+                             int32_t K, void* y, int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream) {
     DKV_REQUIRE(x && w && y, "dkv_gemm_bf16: NULL argument");
     DKV_REQUIRE(M >= 0 && N > 0 && K > 0, "dkv_gemm_bf16: bad sizes");
     DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
     DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
+    DKV_REQUIRE(x_dtype == DKV_BF16 || x_dtype == DKV_F32, "dkv_gemm_bf16: x must be bf16 or float32");
     DKV_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(y) % 16 == 0,
                 "dkv_gemm_bf16: x, w and y must be 16-byte aligned");
@@ -459,7 +493,8 @@ extern "C" int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int
         return fail(DKV_EWORKSPACE, "dkv_gemm_bf16: workspace too small (need " + std::to_string(need) + ")");
     DKV_REQUIRE(reinterpret_cast<uintptr_t>(work) % 16 == 0, "dkv_gemm_bf16: workspace must be 16-byte aligned");
     GemmArgs a;
-    a.x = static_cast<const uint16_t*>(x);
+    a.x = x;
+    a.x_f32 = x_dtype == DKV_F32;
     a.w = static_cast<const uint16_t*>(w);
     a.bias = static_cast<const uint16_t*>(bias);
     a.M = M, a.N = N, a.K = K, a.S = S, a.KC = K / S, a.c_per = p.c_per;

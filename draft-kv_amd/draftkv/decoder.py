@@ -124,7 +124,7 @@ class Decoder:
         GEMM when it takes the shapes, else torch's."""
         if ops.gemm_bf16_ok(x, w, bias):
             return ops.gemm_bf16(x, w, bias, out_dtype)
-        y = F.linear(x, w, bias)
+        y = F.linear(x.to(w.dtype), w, bias)
         return y if out_dtype == torch.bfloat16 else y.to(out_dtype)
 
     def _residual(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias, nw, nb) -> torch.Tensor:
@@ -198,8 +198,8 @@ class Decoder:
         for L, p in enumerate(self.layers):
             q, k, v = ops.qkv_split(self._proj(x, p.wqkv), p.bqkv, Hq, Hkv, D, positions, cs, cs_len)
             a = attn(L, q.view(b, T, Hq, D), k.view(b, T, Hkv, D), v.view(b, T, Hkv, D)).view(R, Hq * D)
-            if self.act_dtype != torch.float32:
-                a = a.to(self.act_dtype)
+            # float32 attention output: a bf16 model's o-proj GEMM rounds it to
+            # bf16 as it reads it (the same bits as converting it first)
             x = self._residual(h, a, p.wo, p.bo, p.n2w, p.n2b)
             nxt = self.layers[L + 1] if L + 1 < nL else None
             nw, nb = (nxt.n1w, nxt.n1b) if nxt is not None else (self.nfw, self.nfb)

@@ -442,10 +442,10 @@ def gemm_f32(x: torch.Tensor, w: torch.Tensor, w_layout: int, bias: Optional[tor
 
 
 def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None) -> bool:
-    """Whether dkv_gemm_bf16 takes this product (bf16 contiguous x [M, K] and
-    w [N, K], N % 16 == 0, K % 32 == 0, 16-byte aligned; bias None or bf16
-    contiguous [N], 8-byte aligned)."""
-    ok = (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2
+    """Whether dkv_gemm_bf16 takes this product (contiguous x [M, K], bf16 or
+    float32, and bf16 w [N, K], N % 16 == 0, K % 32 == 0, 16-byte aligned;
+    bias None or bf16 contiguous [N], 8-byte aligned)."""
+    ok = (x.dtype in (torch.bfloat16, torch.float32) and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2
           and x.is_cuda and w.is_cuda and x.is_contiguous() and w.is_contiguous()
           and x.shape[1] == w.shape[1] and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0
           and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
@@ -457,8 +457,9 @@ def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] 
 
 def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
               out_dtype=torch.bfloat16) -> torch.Tensor:
-    """x [M, K] @ w[N, K]^T (+ bias), bf16 in, float32 accumulation, bf16 (or
-    float32) out; a row's result is the same for any M."""
+    """x [M, K] @ w[N, K]^T (+ bias), bf16 in (a float32 x is rounded to bf16
+    as it is read), float32 accumulation, bf16 (or float32) out; a row's
+    result is the same for any M."""
     if not gemm_bf16_ok(x, w, bias):
         raise ValueError(f"gemm_bf16: unsupported operands x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}"
                          + ("" if bias is None else f", bias {tuple(bias.shape)} {bias.dtype}"))
@@ -467,6 +468,7 @@ def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = N
     out = torch.empty((M, N), dtype=out_dtype, device=x.device)
     nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)
     ws = _WS.get(x.device, nbytes) if nbytes else None
-    check(lib().dkv_gemm_bf16(x.data_ptr(), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(), _odt(out_dtype),
+    check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
+                              _odt(out_dtype),
                               _ptr(ws), 0 if ws is None else ws.numel(), _stream()), "dkv_gemm_bf16")
     return out

@@ -267,7 +267,9 @@ int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, in
                  const void* bias, int32_t bias_dtype, float* out, int32_t accumulate, dkv_stream_t stream);
 /* y[M][N] = x[M][K] . w[N][K]^T (+ bias[N]), bf16 inputs, float32
  * accumulation, y bf16 (rounded once, to nearest even) or float32 (y_dtype
- * DKV_BF16 / DKV_F32); bias bf16 or NULL. N a multiple of 16, K of 32; x, w,
+ * DKV_BF16 / DKV_F32); bias bf16 or NULL. x is bf16 or float32 (x_dtype);
+ * a float32 x is rounded to bf16 (nearest even) as it is read, so the
+ * result equals that of the converted x. N a multiple of 16, K of 32; x, w,
  * y 16-byte aligned, bias 8-byte aligned. K is cut into chunks fixed by
  * (N, K) alone; every output is one in-order chain of MFMA steps per chunk,
  * the chunk sums are added in chunk order and the bias last, so a row's
@@ -276,8 +278,8 @@ int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, in
  * needed)  -- the x @ W (+ b) products of the bf16 model forwards
  * (model.py:113-133, gpt2.py:191-213, llama.py:187-225) */
 size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K);
-int dkv_gemm_bf16(const void* x, const void* w, const void* bias, int32_t M, int32_t N, int32_t K, void* y,
-                  int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream);
+int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
+                  int32_t K, void* y, int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream);
 
 /* ---------------------------------------------------------------- misc */
 const char* dkv_last_error(void);

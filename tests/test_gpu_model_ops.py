@@ -160,6 +160,22 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
         assert torch.equal(part, y[3:17])
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 96, 160), (8, 512, 14336), (32, 4096, 4096),
+                                   (96, 1024, 2048), (200, 272, 96)])
+def test_gemm_bf16_float32_x_equals_converting_first(dev, M, N, K):
+    """A float32 x is rounded to bf16 (nearest even) as the kernels read it:
+    the result is bit for bit that of x.to(bfloat16), for every launch plan."""
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K)
+    x = torch.randn((M, K), generator=g, device=dev) * 3.0
+    w = (0.05 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+    bias = torch.randn((N,), generator=g, device=dev).to(torch.bfloat16)
+    for b in (None, bias):
+        assert torch.equal(ops.gemm_bf16(x, w, b), ops.gemm_bf16(x.to(torch.bfloat16), w, b))
+        assert torch.equal(ops.gemm_bf16(x, w, b, out_dtype=torch.float32),
+                           ops.gemm_bf16(x.to(torch.bfloat16), w, b, out_dtype=torch.float32))
+
+
 def test_gemm_bf16_rejects_unsupported_operands(dev):
     ops = _ops()
     x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
@@ -170,6 +186,8 @@ def test_gemm_bf16_rejects_unsupported_operands(dev):
     with pytest.raises(ValueError):
         ops.gemm_bf16(x, torch.zeros((32, 64), dtype=torch.bfloat16, device=dev),
                       torch.zeros((32,), dtype=torch.float32, device=dev))            # bias dtype
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(x.to(torch.float16), torch.zeros((32, 64), dtype=torch.bfloat16, device=dev))   # x dtype
 
 
 def test_embed_with_positions(dev):
