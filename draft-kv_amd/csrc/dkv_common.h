@@ -16,6 +16,21 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
+// Reserve `lds` bytes of dynamic LDS for kernel `fn` (needed above 64 KB).
+// The attribute persists, so it is set once per kernel and device, at the
+// largest size asked for so far: setting it on every launch can stall the
+// host behind the work already queued. `done` is the caller's per-kernel
+// record (one slot per device).
+inline bool reserve_lds(const void* fn, size_t lds, size_t (&done)[16]) {
+    if (lds <= 64 * 1024) return true;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+    if (done[dev] >= lds) return true;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
+    done[dev] = lds;
+    return true;
+}
+
 #define DKV_REQUIRE(cond, msg)                                   \
     do {                                                         \
         if (!(cond)) return ::dkv::fail(DKV_EINVAL, (msg));      \

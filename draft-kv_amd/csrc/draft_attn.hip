@@ -1033,8 +1033,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     do {                                                                                                          \
         auto kfn = draft_attn_dma_kernel<128, MM, ST, LP>;                                                        \
         const size_t lds = (size_t)4 * dma_stages(LP) * LP * 1024;                                                \
-        if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),                            \
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+        static size_t lds_done[16] = {};                                                                         \
+        if (!reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))                                      \
             return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
         hipLaunchKernelGGL(kfn, grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, scale, rps, ns, part,      \
                            logits);                                                                               \

@@ -585,8 +585,8 @@ extern "C" int dkv_paged_attention(const dkv_paged_t* cache, int32_t layer, cons
 #define DKV_VERIFY(DD, WW)                                                                                         \
     do {                                                                                                           \
         auto kfn = dkv::paged_attn_mfma_kernel<DD, WW>;                                                            \
-        if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),                             \
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+        static size_t lds_done[16] = {};                                                                           \
+        if (!dkv::reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))                                   \
             return dkv::fail(DKV_ELAUNCH, "dkv_paged_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
         hipLaunchKernelGGL(kfn, grid, blk, lds, st, c, layer, q, T, n_q_heads, start, count, chunk_keys,          \
                            n_qgroups, n_chunks, n_qtiles, scale, part);                                            \
