@@ -15,7 +15,17 @@ from . import _lib
 from ._lib import DKV_BF16, DKV_F32, Drafter, Paged, QCfg, check, lib
 
 
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream() -> int:
+    """The current HIP stream of the current device (the capture stream while
+    a graph is recorded). torch's C accessors, when present, skip the Python
+    layers of torch.cuda.current_stream(), which cost several microseconds on
+    every launch."""
+    if _raw_stream is not None and _get_device is not None:
+        return _raw_stream(_get_device())
     return torch.cuda.current_stream().cuda_stream
 
 

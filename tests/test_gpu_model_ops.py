@@ -199,3 +199,14 @@ def test_embed_with_positions(dev):
     pos = torch.randint(0, 40, (33,), generator=g, device=dev, dtype=torch.int32)
     out = ops.embed(table, tok, pos_t, pos)
     torch.testing.assert_close(out, table.float()[tok.long()] + pos_t.float()[pos.long()], rtol=0, atol=0)
+
+
+def test_library_stream_is_torchs_current_stream(dev):
+    """Every launch goes to torch's current stream: the default stream, a
+    side stream entered with torch.cuda.stream, and back."""
+    from draftkv import ops
+    assert ops._stream() == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert ops._stream() == s.cuda_stream
+    assert ops._stream() == torch.cuda.current_stream().cuda_stream
