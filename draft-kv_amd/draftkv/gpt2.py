@@ -16,6 +16,7 @@ from typing import Optional
 import numpy as np
 import torch
 
+from .bpe import BPETokenizer  # noqa: F401  (gpt2.py:65; re-exported here)
 from .decoder import Decoder, Layer
 
 _NP = {"F32": np.float32, "F16": np.float16, "I64": np.int64, "I32": np.int32}
@@ -142,8 +143,12 @@ def default_model_dir() -> Optional[Path]:                               # gpt2.
 
 def load_real_model(d=None, **kw):                                       # gpt2.py:232-245
     """Returns (model, tokenizer) from a local checkpoint; raises FileNotFoundError
-    when there is none. The tokenizer is not part of the GPU build (None)."""
+    when there is none. The tokenizer is None when the directory has no
+    vocab.json / merges.txt."""
     d = Path(d) if d else default_model_dir()
     if d is None:
         raise FileNotFoundError("no distilgpt2 checkpoint; set DRAFTKV_GPT2_DIR (no download here)")
-    return GPT2.from_dir(d, **kw), None
+    tok = None
+    if (d / "vocab.json").exists() and (d / "merges.txt").exists():
+        tok = BPETokenizer(d / "vocab.json", d / "merges.txt")
+    return GPT2.from_dir(d, **kw), tok

@@ -17,6 +17,7 @@ from typing import Optional
 import numpy as np
 import torch
 
+from .bpe import ByteLevelBPE  # noqa: F401  (llama.py:29; re-exported here)
 from .decoder import Decoder, Layer
 from .gpt2 import load_safetensors
 
@@ -123,11 +124,12 @@ class LlamaLike(Decoder):
 
 def load_llama(d, **kw):                                                   # llama.py:228-234
     """Returns (model, tokenizer) for a local Llama/Qwen2-style checkpoint
-    directory; the tokenizer is not part of the GPU build (None)."""
+    directory; the tokenizer is None when it has no tokenizer.json."""
     d = Path(d)
     if not (d / "model.safetensors").exists():
         raise FileNotFoundError(f"no checkpoint at {d} (no download here)")
-    return LlamaLike.from_dir(d, **kw), None
+    tok = ByteLevelBPE(d / "tokenizer.json") if (d / "tokenizer.json").exists() else None
+    return LlamaLike.from_dir(d, **kw), tok
 
 
 def default_llama_dir(name: str = "smollm2-135m") -> Optional[Path]:       # llama.py:237-244
