@@ -424,7 +424,8 @@ def run_e2e(args):
         # fit the cost model's time terms to this device: full-KV steps, then
         # each arm at two draft lengths (real decode rounds, before the timed ones)
         log(f"calibrating the cost model ({cal_rounds} rounds)")
-        calibrated = calibrate(batch, cost, arms, gammas=cal_gammas, reps=2)
+        # (the arms in reverse, so the mirror ends up as the first timed round needs it)
+        calibrated = calibrate(batch, cost, arms[::-1], gammas=cal_gammas, reps=2)
         ctrl.cost = calibrated
         torch.cuda.synchronize()
     comp = batch.comp
