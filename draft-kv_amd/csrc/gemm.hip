@@ -55,6 +55,16 @@ __device__ __forceinline__ XRaw<XF32> load_x8(const void* base, int64_t elem) {
     else return *reinterpret_cast<const gu32x4_t*>(static_cast<const uint16_t*>(base) + elem);
 }
 
+// SwiGLU of one (gate, up) pair of outputs, both first rounded to bf16 as the
+// unfused GEMM would store them, then g / (1 + exp(-g)) * u in float32 (the
+// SwiGLU kernel's arithmetic) rounded to bf16
+__device__ __forceinline__ float bf16_round(float v) { return __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16); }
+__device__ __forceinline__ uint32_t swiglu_pair(float g0, float u0, float g1, float u1) {
+    const float a = bf16_round(g0), b = bf16_round(u0), c = bf16_round(g1), d = bf16_round(u1);
+    return (uint32_t)f32_to_bf16_rne(a / (1.0f + __expf(-a)) * b) |
+           ((uint32_t)f32_to_bf16_rne(c / (1.0f + __expf(-c)) * d) << 16);
+}
+
 template <bool XF32>
 __device__ __forceinline__ gu32x4_t x8_bf16(const XRaw<XF32>& r) {
     if constexpr (XF32)
@@ -79,6 +89,7 @@ struct GemmArgs {
     float* part;         // [S][M][N] float32 partials when c_per == 1 < S
     void* y;
     int y_f32;
+    int swiglu;          // rows of W interleave (gate_i, up_i); y[m][i] = silu(gate) * up, bf16, N / 2 columns
 };
 
 // One workgroup: 64*NW rows of W (16*NW per wave) against a tile of 16*MB
@@ -245,6 +256,9 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
             }
             if (to_part) {
                 *reinterpret_cast<float4*>(a.part + (int64_t)c0 * a.M * a.N + o) = make_float4(t[0], t[1], t[2], t[3]);
+            } else if (a.swiglu) {   // rows n .. n+3 are (gate, up) of outputs n/2 and n/2 + 1
+                *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (int64_t)m * (a.N / 2) + n / 2) =
+                    swiglu_pair(t[0], t[1], t[2], t[3]);
             } else if (a.y_f32) {
                 *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
             } else {
@@ -363,7 +377,10 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
             t[3] = t[3] + bv.w;
         }
         const int64_t o = (int64_t)m * a.N + n;
-        if (a.y_f32) {
+        if (a.swiglu) {
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (int64_t)m * (a.N / 2) + n / 2) =
+                swiglu_pair(t[0], t[1], t[2], t[3]);
+        } else if (a.y_f32) {
             *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
         } else {
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + o) =
@@ -375,7 +392,7 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
 // y = sum of the K chunks' partials, in chunk order, then the bias; 4 outputs per thread
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, int64_t MN, int S, int N,
                                                           const uint16_t* __restrict__ bias, void* __restrict__ y,
-                                                          int y_f32) {
+                                                          int y_f32, int swiglu) {
     const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (i >= MN) return;
     float4 t = *reinterpret_cast<const float4*>(part + i);
@@ -393,7 +410,8 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restric
         t.z += bv.z;
         t.w += bv.w;
     }
-    if (y_f32) *reinterpret_cast<float4*>(static_cast<float*>(y) + i) = t;
+    if (swiglu) *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(y) + i / 2) = swiglu_pair(t.x, t.y, t.z, t.w);
+    else if (y_f32) *reinterpret_cast<float4*>(static_cast<float*>(y) + i) = t;
     else *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + i) = make_uint2(bf16_pair_rne(t.x, t.y),
                                                                                bf16_pair_rne(t.z, t.w));
 }
@@ -475,12 +493,17 @@ static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
 }
 
 extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
-                             int32_t K, void* y, int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream) {
+                             int32_t K, void* y, int32_t y_dtype, int32_t flags, void* work, size_t work_bytes,
+                             dkv_stream_t stream) {
     DKV_REQUIRE(x && w && y, "dkv_gemm_bf16: NULL argument");
     DKV_REQUIRE(M >= 0 && N > 0 && K > 0, "dkv_gemm_bf16: bad sizes");
     DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
     DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
     DKV_REQUIRE(x_dtype == DKV_BF16 || x_dtype == DKV_F32, "dkv_gemm_bf16: x must be bf16 or float32");
+    DKV_REQUIRE((flags & ~DKV_GEMM_SWIGLU) == 0, "dkv_gemm_bf16: unknown flags");
+    const int swiglu = (flags & DKV_GEMM_SWIGLU) != 0;
+    DKV_REQUIRE(!swiglu || (y_dtype == DKV_BF16 && !bias),
+                "dkv_gemm_bf16: the SwiGLU epilogue writes bf16 and takes no bias");
     DKV_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(y) % 16 == 0,
                 "dkv_gemm_bf16: x, w and y must be 16-byte aligned");
@@ -503,6 +526,7 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     a.part = need ? static_cast<float*>(work) : nullptr;
     a.y = y;
     a.y_f32 = y_dtype == DKV_F32;
+    a.swiglu = swiglu;
     hipStream_t st = as_stream(stream);
     if (p.small) {
         DKV_REQUIRE((int64_t)S * p.rw * p.mb * 4 * WAVE * sizeof(float) <= 64 * 1024, "dkv_gemm_bf16: too many K chunks");
@@ -521,6 +545,6 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     if (rc || !need) return rc;
     const int64_t MN = (int64_t)M * N;   // a multiple of 16
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, a.part, MN, S, N,
-                       a.bias, y, a.y_f32);
+                       a.bias, y, a.y_f32, a.swiglu);
     return check_launch("dkv_gemm_bf16(reduce)");
 }

@@ -70,7 +70,7 @@ _SIGS = {
     "dkv_add": (C.c_int, [P, P, I32, P, I32, I32, I32, P]),
     "dkv_gemm_f32": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P]),
     "dkv_gemm_bf16_workspace": (SZ, [I32, I32, I32]),
-    "dkv_gemm_bf16": (C.c_int, [P, I32, P, P, I32, I32, I32, P, I32, P, SZ, P]),
+    "dkv_gemm_bf16": (C.c_int, [P, I32, P, P, I32, I32, I32, P, I32, I32, P, SZ, P]),
     "dkv_last_error": (C.c_char_p, []),
     "dkv_version": (I32, []),
 }

@@ -135,8 +135,24 @@ class Decoder:
             return self._norm(h, nw, nb)
         return ops.add_norm(h, self._linear(x, w), bias, nw, nb, self.eps, self.norm == "layer", self.act_dtype)
 
+    def _interleave_gate_up(self) -> None:
+        """bf16 SwiGLU models: reorder each fused [gate; up] weight to rows
+        (gate_0, up_0, gate_1, up_1, ...), so the GEMM's epilogue holds both
+        halves of a pair and writes silu(gate) * up directly."""
+        if self.mlp != "swiglu" or self.wdtype != torch.bfloat16:
+            return
+        for p in self.layers:
+            ff2, k = p.w1.shape
+            p.w1 = p.w1.view(2, ff2 // 2, k).transpose(0, 1).reshape(ff2, k).contiguous()
+        self.gate_up_interleaved = True
+
     def _mlp_inner(self, x: torch.Tensor, p: Layer) -> torch.Tensor:
         if self.mlp == "swiglu":
+            if getattr(self, "gate_up_interleaved", False):
+                if ops.gemm_bf16_ok(x, p.w1):
+                    return ops.gemm_bf16(x, p.w1, swiglu=True)
+                y = F.linear(x.to(p.w1.dtype), p.w1)
+                return ops.silu_mul(torch.cat([y[:, 0::2], y[:, 1::2]], 1), self.act_dtype)
             return ops.silu_mul(self._proj(x, p.w1), self.act_dtype)
         if self.mlp == "gelu":
             return ops.bias_gelu(self._proj(x, p.w1), p.b1, self.act_dtype)

@@ -466,19 +466,22 @@ def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] 
 
 
 def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
-              out_dtype=torch.bfloat16) -> torch.Tensor:
+              out_dtype=torch.bfloat16, swiglu: bool = False) -> torch.Tensor:
     """x [M, K] @ w[N, K]^T (+ bias), bf16 in (a float32 x is rounded to bf16
     as it is read), float32 accumulation, bf16 (or float32) out; a row's
-    result is the same for any M."""
+    result is the same for any M. swiglu: w's rows interleave (gate_i, up_i)
+    and the result is silu(gate) * up, bf16 [M, N / 2] (no bias)."""
     if not gemm_bf16_ok(x, w, bias):
         raise ValueError(f"gemm_bf16: unsupported operands x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}"
                          + ("" if bias is None else f", bias {tuple(bias.shape)} {bias.dtype}"))
     M, K = x.shape
     N = w.shape[0]
-    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if swiglu and (bias is not None or out_dtype != torch.bfloat16):
+        raise ValueError("gemm_bf16: the SwiGLU epilogue writes bf16 and takes no bias")
+    out = torch.empty((M, N // 2 if swiglu else N), dtype=out_dtype, device=x.device)
     nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)
     ws = _WS.get(x.device, nbytes) if nbytes else None
     check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
-                              _odt(out_dtype),
+                              _odt(out_dtype), 1 if swiglu else 0,
                               _ptr(ws), 0 if ws is None else ws.numel(), _stream()), "dkv_gemm_bf16")
     return out

@@ -277,9 +277,13 @@ int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, in
  * decode agree bit for bit). work: dkv_gemm_bf16_workspace() bytes (0: none
  * needed)  -- the x @ W (+ b) products of the bf16 model forwards
  * (model.py:113-133, gpt2.py:191-213, llama.py:187-225) */
+#define DKV_GEMM_SWIGLU 1  /* flags: W's rows interleave (gate_i, up_i); y is bf16 [M][N/2] with
+                              y[m][i] = silu(g) * u of the two outputs, each first rounded to bf16
+                              (the SwiGLU of llama.py:220-222 fused into the gate/up product; no bias) */
 size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K);
 int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
-                  int32_t K, void* y, int32_t y_dtype, void* work, size_t work_bytes, dkv_stream_t stream);
+                  int32_t K, void* y, int32_t y_dtype, int32_t flags, void* work, size_t work_bytes,
+                  dkv_stream_t stream);
 
 /* ---------------------------------------------------------------- misc */
 const char* dkv_last_error(void);

@@ -176,6 +176,23 @@ def test_gemm_bf16_float32_x_equals_converting_first(dev, M, N, K):
                            ops.gemm_bf16(x.to(torch.bfloat16), w, b, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("M,ff,K", [(1, 2048, 4096), (5, 48, 160), (8, 512, 2048), (32, 14336, 4096),
+                                    (96, 512, 1024), (200, 136, 96)])
+def test_gemm_bf16_swiglu_epilogue_equals_unfused(dev, M, ff, K):
+    """The SwiGLU epilogue (interleaved gate/up rows) gives bit for bit the
+    unfused result: the [gate; up] GEMM rounded to bf16, then the SwiGLU
+    kernel -- for every launch plan, bf16 and float32 x."""
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M + ff + K)
+    w = (0.05 * torch.randn((2 * ff, K), generator=g, device=dev)).to(torch.bfloat16)
+    wi = w.view(2, ff, K).transpose(0, 1).reshape(2 * ff, K).contiguous()
+    x = torch.randn((M, K), generator=g, device=dev) * 2.0
+    for xx in (x, x.to(torch.bfloat16)):
+        ref = ops.silu_mul(ops.gemm_bf16(xx, w), torch.bfloat16)
+        got = ops.gemm_bf16(xx, wi, swiglu=True)
+        assert got.shape == (M, ff) and torch.equal(got, ref)
+
+
 def test_gemm_bf16_rejects_unsupported_operands(dev):
     ops = _ops()
     x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
@@ -188,6 +205,9 @@ def test_gemm_bf16_rejects_unsupported_operands(dev):
                       torch.zeros((32,), dtype=torch.float32, device=dev))            # bias dtype
     with pytest.raises(ValueError):
         ops.gemm_bf16(x.to(torch.float16), torch.zeros((32, 64), dtype=torch.bfloat16, device=dev))   # x dtype
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(x, torch.zeros((32, 64), dtype=torch.bfloat16, device=dev),
+                      torch.zeros((32,), dtype=torch.bfloat16, device=dev), swiglu=True)   # SwiGLU takes no bias
 
 
 def test_embed_with_positions(dev):
