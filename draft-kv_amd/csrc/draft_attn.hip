@@ -391,9 +391,16 @@ struct SplitCore {
     // The page's scores (unscaled): sv[x] for rows 4jj+x (x < 4) and
     // 16+4jj+x-4 of column col's head, summed over the head's groups.
     __device__ __forceinline__ void qk(const Regs& cur, float (&sv)[8]) {
-        // ---- QK over the page's two 16-row tiles, folded per (row, group)
-        // (the two tiles' MFMA chains interleaved, so each hides the other's latency)
-        f32x4_t sa[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        f32x4_t sa[2];
+        qk_mfma(cur, sa);
+        qk_fold(cur, sa, sv);
+    }
+
+    // QK over the page's two 16-row tiles (the two tiles' MFMA chains
+    // interleaved, so each hides the other's latency)
+    __device__ __forceinline__ void qk_mfma(const Regs& cur, f32x4_t (&sa)[2]) {
+        sa[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        sa[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st) {
             const f16x8_t kv0 = codes_to_f16<CB>(cur.k[0] + st * (CB / 4));
@@ -403,6 +410,11 @@ struct SplitCore {
             sa[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv0, qlo[st], sa[0], 0, 0, 0);
             sa[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv1, qlo[st], sa[1], 0, 0, 0);
         }
+    }
+
+    // the products folded per (row, group) with the K meta, then summed over
+    // the head's group columns
+    __device__ __forceinline__ void qk_fold(const Regs& cur, const f32x4_t (&sa)[2], float (&sv)[8]) {
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -766,10 +778,11 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
         else vm_wait(LPP * ahead + SPP * since);
     };
 
-    // Software-pipelined by one page: while page g's softmax and PV run, the
-    // scores of page g+1 are computed from its operands (the two are
-    // independent), so each hides the other's latency. Pages still enter the
-    // softmax in order, so the arithmetic is that of one page at a time.
+    // Software-pipelined by one page: the QK MFMAs of page g+1 are issued
+    // before page g's softmax and PV (the two are independent), so the matrix
+    // pipe works through them while the softmax runs on the VALU; their fold
+    // into scores follows. Pages still enter the softmax in order, so the
+    // arithmetic is that of one page at a time.
     // Waits: when page g+1 is awaited (iteration g, before issuing page
     // g+S-1), the loads in flight after its own are those of pages
     // g+2 .. g+S-2 and the logit stores of the pages computed since it was
@@ -779,18 +792,31 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     vm_wait(LPP * min(S - 2, T - 1));   // page 0 landed
     operands(ra);
     c.qk(ra, sa_);
+    // a page that has a successor (g + 1 < T; never the partial tail page)
     auto step = [&](int g, Regs& cur, float (&scur)[8], Regs& nxt, float (&snxt)[8]) {
-        const bool more = g + 1 < T;                      // wave-uniform
-        if (more) vm_wait(LPP * max(0, min(S - 3, T - 2 - g)) + SPP * min(g, S - 2));
+        vm_wait(LPP * max(0, min(S - 3, T - 2 - g)) + SPP * min(g, S - 2));
         if (g + S - 1 < T) issue(g + S - 1);
-        if (more) operands(nxt);
-        if (tail && !more) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, store);
-        else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, store);
-        if (more) c.qk(nxt, snxt);
+        operands(nxt);
+        f32x4_t acc_next[2];
+        c.qk_mfma(nxt, acc_next);
+        c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, store);
+        c.qk_fold(nxt, acc_next, snxt);
     };
-    for (int g = 0; g < T; g += 2) {
+    // the stream's last page (g = T - 1)
+    auto last = [&](int g, const Regs& cur, const float (&scur)[8]) {
+        if (tail) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, store);
+        else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, store);
+    };
+    int g = 0;
+    for (; g + 2 < T; g += 2) {
         step(g, ra, sa_, rb, sb_);
-        if (g + 1 < T) step(g + 1, rb, sb_, ra, sa_);
+        step(g + 1, rb, sb_, ra, sa_);
+    }
+    if (g + 1 < T) {   // two pages left
+        step(g, ra, sa_, rb, sb_);
+        last(g + 1, rb, sb_);
+    } else {           // one page left
+        last(g, ra, sa_);
     }
     c.finish(part, s, h, Hq, G, n_splits, wid);
 }
