@@ -442,7 +442,8 @@ def run_e2e(args):
         t.on = True
     log(f"timing {args.steps} rounds (arm switch every {args.period} rounds)")
     emitted = 0
-    arm_time = {}      # arm -> [seconds, tokens, rounds] (each round ends in a host read-back)
+    arm_time = {}      # arm -> [seconds, tokens, rounds] (host time per round; a declined round's
+                       # GPU time lands in the next round that waits for the device)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -455,6 +456,7 @@ def run_e2e(args):
         at[2] += 1
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    batch.resolve_tokens()     # the declined rounds' tokens, already on the host
     for t in timers:
         t.on = False
     per_arm = {}

@@ -186,6 +186,16 @@ class DraftKVEngine:
 _RECORD = object()   # DecodeBatch._draft_graph: record a graph after this round's first step
 
 
+class _Landed:
+    """Event stand-in for a host tensor (nothing to wait for)."""
+
+    def query(self) -> bool:
+        return True
+
+    def synchronize(self) -> None:
+        pass
+
+
 class DecodeBatch:
     """A batch in the middle of self-speculative decoding: token lists, the
     full cache (holding positions 0 .. len-2 of every sequence), the drafter
@@ -222,6 +232,13 @@ class DecodeBatch:
         self._pending_key = None
         self.last_draft = None            # (tokens, logits) of the last round's draft steps
         self.phases = None                # a calibrate.PhaseLog to record per-round phase times
+        # A round that declines to draft (gamma 0) does not wait for its token:
+        # the next round reads it from the device (_dev_pending), and the host
+        # copy lands in a pinned buffer and fills the placeholder appended to
+        # the token list when resolve_tokens() (or a drafted round's read-back)
+        # comes to it. The token streams are the same; only the wait moves.
+        self._dev_pending = None          # device int32 [b]: every sequence's last token
+        self._deferred: list = []         # (pinned int32 [b], event, sequences, list positions)
 
     def _sync(self, start) -> None:
         self.comp.sync_from(self.full, start)
@@ -263,7 +280,28 @@ class DecodeBatch:
         self._graphs[key] = g
         return g
 
+    def _pending_dev(self) -> torch.Tensor:
+        """The last token of every sequence as a device int32 [b]."""
+        if self._dev_pending is not None:
+            return self._dev_pending
+        return self.engine._pending(self.toks)
+
+    def resolve_tokens(self, wait: bool = True) -> None:
+        """Write the tokens of declined rounds into the token lists (waiting
+        for their copies when ``wait``; else only those already landed)."""
+        keep = []
+        for hbuf, ev, seqs, at in self._deferred:
+            if not wait and not ev.query():
+                keep.append((hbuf, ev, seqs, at))
+                continue
+            ev.synchronize()
+            v = hbuf.numpy()
+            for s, j in zip(seqs, at):
+                self.toks[s][j] = int(v[s])
+        self._deferred = keep
+
     def results(self) -> list:
+        self.resolve_tokens()
         for s in range(self.b):
             del self.toks[s][int(self.plen[s]) + self.max_new:]
             self.res[s].tokens = self.toks[s]
@@ -278,7 +316,9 @@ class DecodeBatch:
         self.last_emitted = 0
         self.last_draft = None
         if not active.any():
+            self.resolve_tokens()
             return False
+        self.resolve_tokens(wait=False)
         act = active.astype(np.int64)
         budget = np.where(active, self.max_new - produced, 0)
         ctx = int(n[active].max())
@@ -292,16 +332,27 @@ class DecodeBatch:
             u_d = ops.to_device(u, dev)
             if ph is not None:
                 ev["d1"] = ph.event()
-            logits = model.forward_batch(eng._pending(toks)[:, None], full, n - 1, act)[:, 0]
+            logits = model.forward_batch(self._pending_dev()[:, None], full, n - 1, act)[:, 0]
             tok = ops.sample(logits, T, u_d)
             if ph is not None:
                 ev["v1"] = ph.event()
-            tok = tok.cpu().numpy()
+            # no wait: the next round reads tok on the device; the host copy
+            # fills the placeholders when resolved
+            if tok.device.type == "cuda":
+                hbuf = torch.empty(tok.shape, dtype=tok.dtype, pin_memory=True)
+                hbuf.copy_(tok, non_blocking=True)
+                landed = torch.cuda.Event()
+                landed.record()
+                self._dev_pending = tok
+            else:
+                hbuf, landed = tok, _Landed()
             h0 = time.perf_counter()
-            for s in np.flatnonzero(active):
-                toks[s].append(int(tok[s]))
+            seqs = np.flatnonzero(active)
+            for s in seqs:
+                toks[s].append(-1)
                 res[s].verify_passes += 1
                 res[s].rounds.append(RoundLog(cfg, 0, 0, 1, int(n[s])))
+            self._deferred.append((hbuf, landed, seqs, [len(toks[s]) - 1 for s in seqs]))
             self.last_emitted = int(active.sum())
             hs = time.perf_counter() - h0
             if ph is not None:
@@ -346,7 +397,7 @@ class DecodeBatch:
         u_ver_d = ops.to_device(u_ver, dev)
 
         # -- draft
-        x = eng._pending(toks)
+        x = self._pending_dev()
         pending = x
         draft_tok = torch.empty((b, gamma), dtype=torch.int32, device=dev)
         draft_logits = torch.empty((b, gamma, V), dtype=torch.float32, device=dev) if T > 0 else None
@@ -379,6 +430,8 @@ class DecodeBatch:
         if ph is not None:
             ev["v1"] = ph.event()
         host = torch.cat([torch.stack([acc, nxt, used], 1), draft_tok], 1).cpu().numpy()
+        self.resolve_tokens()             # the read-back above waited for every earlier copy
+        self._dev_pending = None
 
         # -- bookkeeping, rollback, resync
         h0 = time.perf_counter()
