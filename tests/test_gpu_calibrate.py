@@ -73,3 +73,31 @@ def test_declined_rounds_keep_greedy_output_identical(dev):
     r = DraftKVEngine(m, _Decline(arms[1]), seed=0).generate(prompts[0], 30, 0.0)
     assert r.tokens == base
     assert any(x.gamma == 0 for x in r.rounds) and any(x.gamma > 0 for x in r.rounds)
+
+
+class _AlwaysDecline(_Decline):
+    def select(self, ctx, key=None):
+        return self.arm, 0
+
+
+def test_consecutive_declined_rounds_resolve_their_tokens(dev):
+    # every round declines: each one's token stays on the device until the
+    # batch resolves it; the streams equal plain full-KV decoding
+    from draftkv import DraftKVEngine
+    from draftkv.engine import DecodeBatch
+    m, prompts, arms, *_ = _setup()
+    base = [DraftKVEngine(m, seed=0).generate_baseline(p, 12, 0.0) for p in prompts]
+    eng = DraftKVEngine(m, _AlwaysDecline(arms[0]), seed=0)
+    toks = eng._check_prompts(prompts, m.vocab_size)
+    full = eng._new_full(len(toks), max(len(t) for t in toks) + 32)
+    eng._prefill(toks, full)
+    batch = DecodeBatch(eng, toks, full, 12, 0.0)
+    for _ in range(5):
+        assert batch.step()
+    batch.resolve_tokens()
+    assert all(-1 not in t for t in batch.toks)
+    assert [t[: len(p) + 5] for t, p in zip(batch.toks, prompts)] == [b[: len(p) + 5] for b, p in zip(base, prompts)]
+    while batch.step():
+        pass
+    assert [r.tokens for r in batch.results()] == base
+    assert all(x.gamma == 0 for r in batch.res for x in r.rounds)
