@@ -432,8 +432,15 @@ struct SplitCore {
     // online softmax, PV.
     template <bool TAIL, class Sink>
     __device__ __forceinline__ void rest(const Regs& cur, const float (&sv)[8], int p0, int r_end, Sink&& sink) {
-        // scale, mask the tail, hand over, online softmax per column
         float pv[8];
+        rest_head<TAIL>(sv, p0, r_end, sink, pv);
+        rest_tail<TAIL>(cur, pv, p0, r_end);
+    }
+
+    // scale, mask the tail, hand over the logits, the column max and the lazy
+    // rescale; pv gets the scaled logits
+    template <bool TAIL, class Sink>
+    __device__ __forceinline__ void rest_head(const float (&sv)[8], int p0, int r_end, Sink&& sink, float (&pv)[8]) {
         float mx = -INFINITY;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
@@ -457,6 +464,11 @@ struct SplitCore {
             for (int t = 0; t < NDT; ++t) acc[t] *= alpha;
             m_run = m_new;
         }
+    }
+
+    // probabilities, row sums and the PV product of the page
+    template <bool TAIL>
+    __device__ __forceinline__ void rest_tail(const Regs& cur, float (&pv)[8], int p0, int r_end) {
         // m_run is finite from the first page on (every split starts with a
         // live row), so masked rows give exp(-inf) = 0 with no test
 #pragma unroll
@@ -778,10 +790,11 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
         else vm_wait(LPP * ahead + SPP * since);
     };
 
-    // Software-pipelined by one page: the QK MFMAs of page g+1 are issued
-    // before page g's softmax and PV (the two are independent), so the matrix
-    // pipe works through them while the softmax runs on the VALU; their fold
-    // into scores follows. Pages still enter the softmax in order, so the
+    // Software-pipelined by one page: page g+1's operands are read from LDS
+    // while page g's scores are scaled, stored and reduced to the column max;
+    // then the QK MFMAs of page g+1 are issued, the matrix pipe works through
+    // them while page g's probabilities and PV run, and their fold into
+    // scores follows. Pages still enter the softmax in order, so the
     // arithmetic is that of one page at a time.
     // Waits: when page g+1 is awaited (iteration g, before issuing page
     // g+S-1), the loads in flight after its own are those of pages
@@ -797,9 +810,11 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
         vm_wait(LPP * max(0, min(S - 3, T - 2 - g)) + SPP * min(g, S - 2));
         if (g + S - 1 < T) issue(g + S - 1);
         operands(nxt);
+        float pv[8];
+        c.template rest_head<false>(scur, (pg0 + g) * PAGE, n, store, pv);
         f32x4_t acc_next[2];
         c.qk_mfma(nxt, acc_next);
-        c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, store);
+        c.template rest_tail<false>(cur, pv, (pg0 + g) * PAGE, n);
         c.qk_fold(nxt, acc_next, snxt);
     };
     // the stream's last page (g = T - 1)
