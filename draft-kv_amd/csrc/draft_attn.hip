@@ -780,15 +780,6 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
             *reinterpret_cast<float4*>(lrow + p0 + 16) = make_float4(pv[4], pv[5], pv[6], pv[7]);
         }
     };
-    // In flight after page g's loads: the loads of the pages issued after it
-    // (at most S-2 ahead) and the logit stores of the pages computed since it
-    // was issued (at most S-1). The steady state is one immediate.
-    constexpr int N_STEADY = LPP * (S - 2) + SPP * (S - 1);
-    auto wait_page = [&](int g) {
-        const int ahead = min(S - 2, T - 1 - g), since = min(g, S - 1);
-        if (ahead == S - 2 && since == S - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_STEADY) : "memory");
-        else vm_wait(LPP * ahead + SPP * since);
-    };
 
     // Software-pipelined by one page: page g+1's operands are read from LDS
     // while page g's scores are scaled, stored and reduced to the column max;
