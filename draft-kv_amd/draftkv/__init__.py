@@ -8,17 +8,15 @@ running in a gfx950 HIP library (``_lib/libdraftkv_hip.so``).
 
 from .compress import CompressedKVCache, FullKVCache, quantize
 from .config import CompressionConfig, LayerPlan, default_arms
-from .controller import DepthThompsonController, FixedPolicy, FlatBandit, OraclePolicy, ThompsonController
+from .controller import Controller, FixedPolicy
 from .engine import DraftKVEngine, GenerationResult, RoundLog
 from .model import TinyTransformer
 from .paged import BlockPool, BlockPoolExhausted, PagedKVCache, plan_blocks_needed
-from .throughput import CostModel, best_gamma, best_gamma_profile, expected_tokens, expected_tokens_profile
+from .throughput import CostModel, best_gamma, expected_tokens
 
 __all__ = [
-    "BlockPool", "BlockPoolExhausted", "CompressedKVCache", "CompressionConfig", "CostModel",
-    "DepthThompsonController", "DraftKVEngine", "FixedPolicy", "FlatBandit", "FullKVCache", "GenerationResult",
-    "LayerPlan", "OraclePolicy", "PagedKVCache", "RoundLog", "ThompsonController", "TinyTransformer", "best_gamma",
-    "best_gamma_profile", "default_arms", "expected_tokens", "expected_tokens_profile", "plan_blocks_needed",
-    "quantize",
+    "BlockPool", "BlockPoolExhausted", "CompressedKVCache", "CompressionConfig", "Controller", "CostModel",
+    "DraftKVEngine", "FixedPolicy", "FullKVCache", "GenerationResult", "LayerPlan", "PagedKVCache", "RoundLog",
+    "TinyTransformer", "best_gamma", "default_arms", "expected_tokens", "plan_blocks_needed", "quantize",
 ]
 __version__ = "0.1.0"

@@ -136,7 +136,7 @@ class CompressedKVCache:
         self.batch = batch
         self.device = torch.device(device) if device is not None else default_device()
         self.seen = np.zeros(batch, np.int64)          # logical context length (layer-0 appends)
-        self._reserve = list(reserve_cfgs)
+        self._reserve = list(dict.fromkeys(reserve_cfgs))     # distinct arms the pages must fit
         self._cap_hint = cap
         self._ready = False
         if n_kv_heads is not None and d_head is not None:
@@ -149,7 +149,7 @@ class CompressedKVCache:
         """Bytes per page slot: the widest page among the arms this mirror holds."""
         from ._lib import lib
         return max(int(lib().dkv_page_bytes(c.bits, self.d_head, c.group, int(c.scale_fp16)))
-                   for c in list(cfgs) + self._reserve)
+                   for c in dict.fromkeys(list(cfgs) + self._reserve))
 
     def _alloc(self, H: int, D: int, cap: int) -> None:
         cap = -(-cap // self.PAGE) * self.PAGE
@@ -165,7 +165,7 @@ class CompressedKVCache:
     def _regrow(self, cap: int, cfgs=None) -> None:
         """Re-layout for a larger row capacity and/or wider pages, keeping rows."""
         cfgs = cfgs if cfgs is not None else self.cfgs
-        self._reserve = self._reserve + list(cfgs)
+        self._reserve = list(dict.fromkeys(self._reserve + list(cfgs)))
         stride = self._page_stride(cfgs)
         if cap <= self.cap and stride <= self.page_stride:
             return

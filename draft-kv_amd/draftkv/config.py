@@ -10,7 +10,7 @@ them in float32, the default here).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterator, Sequence
+from typing import Iterator, Optional, Sequence
 
 
 @dataclass(frozen=True, order=True)
@@ -40,12 +40,17 @@ class CompressionConfig:
     def lossless(self) -> bool:
         return self.bits == 16 and self.keep_frac >= 1.0
 
-    def bytes_per_entry(self, d_head: int, group: int = 64) -> float:
-        """Bytes of one (token, head) K or V vector: ``bits`` per element plus one
-        fp16 scale and one fp16 zero per ``group`` elements (config.py:39-48)."""
+    def bytes_per_entry(self, d_head: int, group: Optional[int] = None) -> float:
+        """Bytes of one (token, head) K or V vector as the mirror stores it:
+        ``bits`` per element plus one scale and one zero per group of
+        ``group`` (default: this arm's) channels, each 2 bytes with
+        ``scale_fp16`` and 4 bytes (float32) without. With 64-channel groups
+        and fp16 meta this is the reference formula (config.py:39-48)."""
         if self.bits == 16:
             return 2.0 * d_head
-        return d_head * self.bits / 8.0 + 4.0 * max(1, -(-d_head // group))
+        g = self.group if group is None else group
+        meta = 4.0 if self.scale_fp16 else 8.0
+        return d_head * self.bits / 8.0 + meta * max(1, -(-d_head // g))
 
     def label(self) -> str:
         b = "fp16" if self.bits == 16 else f"{self.bits}b"

@@ -174,13 +174,34 @@ class DraftKVEngine:
         exactly the reference's cap ``min(gamma, budget - 1)``)."""
         toks = self._check_prompts(prompts, self.model.vocab_size)
         plen = np.array([len(t) for t in toks], np.int64)
-        # gamma <= budget - 1, so no round writes past position len(prompt) + max_new - 2
-        full = self._new_full(len(toks), int(plen.max()) + max_new_tokens + 16)
+        full = self._new_full(len(toks), rows_needed(plen, max_new_tokens, self.controller))
         self._prefill(toks, full)
         batch = DecodeBatch(self, toks, full, max_new_tokens, temperature, context_key)
         while batch.step():
             pass
         return batch.results()
+
+
+def gamma_bound(controller, max_new_tokens: int) -> int:
+    """The longest draft a round can run: the engine caps gamma at the largest
+    remaining budget minus one (engine.py:175), and a controller that states
+    its own bound (``gamma_max``, or a fixed ``gamma``) caps it further."""
+    bound = max(int(max_new_tokens) - 1, 0)
+    for attr in ("gamma_max", "gamma"):
+        g = getattr(controller, attr, None)
+        if isinstance(g, (int, np.integer)) and g >= 0:
+            return min(bound, int(g))
+    return bound
+
+
+def rows_needed(plen, max_new_tokens: int, controller) -> int:
+    """Cache rows per sequence that decoding ``max_new_tokens`` after prompts of
+    lengths ``plen`` can write. A sequence is decoded while it has produced
+    fewer than max_new tokens, so its pending position is at most
+    len + max_new - 2, and a round writes gamma + 1 rows from there. In a
+    batch, one gamma serves every sequence, so a sequence one token short of
+    its budget still writes the whole verify block."""
+    return int(np.max(plen)) + int(max_new_tokens) + gamma_bound(controller, max_new_tokens)
 
 
 _RECORD = object()   # DecodeBatch._draft_graph: record a graph after this round's first step
@@ -218,7 +239,7 @@ class DecodeBatch:
         self.comp: Optional[CompressedKVCache] = None
         self.comp_cfg = None
         # the mirror never holds more rows per segment than the sequence has positions
-        need = int(self.plen.max()) + max_new_tokens + 16
+        need = rows_needed(self.plen, max_new_tokens, engine.controller)
         self.cap_tokens = min(int(getattr(full, "max_tokens", need) or need), need)
         self.last_emitted = 0             # tokens emitted by the last step, summed over the batch
         # arms the mirror may switch to: its pages are sized for the widest from the start
@@ -324,6 +345,11 @@ class DecodeBatch:
         ctx = int(n[active].max())
         cfg, gamma = eng.controller.select(ctx, self.key)
         gamma = min(int(gamma), max(int(budget.max()) - 1, 0))
+        # a round writes rows n-1 .. n-1+gamma of every active sequence: never
+        # more than the caches were sized for (a controller past its own bound)
+        room = int(getattr(full, "max_tokens", 0) or 0)
+        if room:
+            gamma = max(0, min(gamma, room - int(n[active].max()), self.cap_tokens - int(n[active].max())))
         flen = full.lengths()
 
         ph, ev = self.phases, {}

@@ -1,15 +1,17 @@
 """Tokens per verify pass and the memory-traffic cost model.
 
-Reference: draftkv/throughput.py:24-268. The formulas are the reference's
-(the API is kept untouched, so a CostModel built with MI355X parameters --
-``bandwidth=8e12`` -- prices the same decisions); the implementation is this
-package's own.
+Reference: draftkv/throughput.py:24-155,188-268 (``expected_tokens``,
+``CostModel``'s byte, time, throughput, speedup and ceiling terms,
+``best_gamma``). The formulas are the reference's, so a CostModel built with
+MI355X parameters -- ``bandwidth=8e12`` -- prices the same decisions; the
+depth-profile and arm-switch terms, which only the reference's bandit
+controllers use, are not part of the decode round and are left out.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional, Sequence
+from typing import Optional
 
 from .config import CompressionConfig
 
@@ -27,14 +29,6 @@ def expected_tokens(alpha: float, gamma: int) -> float:
         return float(gamma + 1)
     return (1.0 - a ** (gamma + 1)) / (1.0 - a)
 
-
-def expected_tokens_profile(accept: Sequence[float]) -> float:
-    """E = 1 + sum_k prod_{i<k} a_i for a depth-indexed acceptance profile."""
-    total = run = 1.0
-    for a in accept:
-        run *= _clip01(a)
-        total += run
-    return total
 
 
 @dataclass
@@ -99,20 +93,6 @@ class CostModel:
                 + self.compute_per_token + self.fixed_verify)
 
     # objectives
-    def rebuild_cost(self, ctx: int, layers_changed: Optional[int] = None) -> float:
-        frac = 1.0 if layers_changed is None else min(1.0, layers_changed / max(1, self.n_layers))
-        return ctx * self.resync_per_token * frac * self.n_layers / max(1, self.n_layers)
-
-    def round_cost_profile(self, cfg, accept: Sequence[float], ctx: int, extra_cost: float = 0.0) -> float:
-        g = len(accept)
-        return (g * self.t_draft(cfg, ctx) + self.t_verify(ctx, g)
-                + expected_tokens_profile(accept) * self.resync_per_token + self.controller_overhead + extra_cost)
-
-    def throughput_profile(self, cfg, accept: Sequence[float], ctx: int, extra_cost: float = 0.0) -> float:
-        if not accept:
-            return 1.0 / self.t_baseline(ctx)
-        return expected_tokens_profile(accept) / self.round_cost_profile(cfg, accept, ctx, extra_cost)
-
     def round_cost(self, cfg, gamma: int, alpha: float, ctx: int, extra_cost: float = 0.0) -> float:
         return (gamma * self.t_draft(cfg, ctx) + self.t_verify(ctx, gamma)
                 + expected_tokens(alpha, gamma) * self.resync_per_token + self.controller_overhead + extra_cost)
@@ -132,15 +112,6 @@ class CostModel:
         return (base + self.compute_per_token + self.fixed_verify) / (
             draft + self.compute_per_token + self.fixed_draft + self.resync_per_token)
 
-
-def best_gamma_profile(cost: CostModel, cfg, accept: Sequence[float], ctx: int,
-                       extra_cost: float = 0.0) -> tuple[int, float]:
-    best, best_t = 0, cost.throughput_profile(cfg, (), ctx)
-    for g in range(1, len(accept) + 1):
-        t = cost.throughput_profile(cfg, accept[:g], ctx, extra_cost)
-        if t > best_t:
-            best, best_t = g, t
-    return best, best_t
 
 
 def best_gamma(cost: CostModel, cfg, alpha: float, ctx: int, gamma_max: int = 8,

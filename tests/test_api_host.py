@@ -13,23 +13,43 @@ from draftkv import (BlockPool, BlockPoolExhausted, CompressionConfig, CostModel
 @pytest.mark.parametrize("batch,ctxs,want", [(1, (1024, 32768, 262144), (1.008, 1.222, 2.417)),
                                              (32, (1024, 32768, 262144), (1.222, 4.342, 6.538))])
 def test_ceiling_reproduces_published_rows(batch, ctxs, want):
-    # README.md:82-85: 4b/keep0.5, HBM-resident cache, Llama-3-8B shape, 2 TB/s
+    # README.md:82-85: 4b/keep0.5, HBM-resident cache, Llama-3-8B shape, 2 TB/s; the
+    # reference prices fp16 scale/zero pairs per 64 channels (config.py:39-48)
     cm = CostModel(batch=batch)
-    got = tuple(round(cm.ceiling(CompressionConfig(4, 0.5), c), 3) for c in ctxs)
+    got = tuple(round(cm.ceiling(F16(4, 0.5), c), 3) for c in ctxs)
     assert got == want
 
 
 def test_offloaded_ceiling_row():
     # README.md:86: full cache offloaded over PCIe5 (64 GB/s), 1 GB HBM budget
     cm = CostModel(full_kv_bandwidth=6.4e10, hbm_kv_budget=1e9)
-    got = [round(cm.ceiling(CompressionConfig(4, 0.5), c), 2) for c in (1024, 32768, 262144)]
+    got = [round(cm.ceiling(F16(4, 0.5), c), 2) for c in (1024, 32768, 262144)]
     assert got == [1.26, 9.04, 7.97]
 
 
 def test_mi355x_target_ceilings():
     cm = CostModel(bandwidth=8e12, batch=32)
-    assert cm.ceiling(CompressionConfig(4, 0.25), 32768) == pytest.approx(5.967, abs=1e-3)
-    assert cm.ceiling(CompressionConfig(8, 1.0), 32768) == pytest.approx(1.724, abs=1e-3)
+    assert cm.ceiling(F16(4, 0.25), 32768) == pytest.approx(5.967, abs=1e-3)
+    assert cm.ceiling(F16(8, 1.0), 32768) == pytest.approx(1.724, abs=1e-3)
+
+
+def F16(bits, keep, group=64):
+    return CompressionConfig(bits, keep, group=group, scale_fp16=True)
+
+
+def test_bytes_per_entry_prices_the_stored_group_and_meta():
+    # reference formula (config.py:39-48): D*bits/8 + 4*ceil(D/64) -- fp16 scale and zero per 64 channels
+    for d in (64, 80, 128):
+        for b in (2, 3, 4, 8):
+            assert F16(b, 1.0).bytes_per_entry(d) == d * b / 8 + 4 * -(-d // 64)
+    assert F16(4, 0.25, 32).bytes_per_entry(128) == 64 + 4 * 4          # int4 g32: 80 B
+    assert CompressionConfig(4, 0.25, group=32).bytes_per_entry(128) == 64 + 8 * 4   # f32 meta: 96 B
+    assert F16(8, 1.0).bytes_per_entry(128, group=32) == 128 + 16
+    assert CompressionConfig(16, 1.0).bytes_per_entry(128) == 256
+    # the cost model prices the g32 arm's larger meta
+    cm = CostModel(bandwidth=8e12, batch=32)
+    assert cm.draft_kv_bytes(F16(4, 0.25, 32), 32768) == pytest.approx(
+        cm.draft_kv_bytes(F16(4, 0.25), 32768) * 80 / 72)
 
 
 def test_expected_tokens_and_speedup_bound():          # reference tests/test_math.py:8-55

@@ -180,14 +180,36 @@ def test_batched_generate_equals_one_at_a_time(dev, tiny_setup):
     assert [r.tokens for r in res] == single
 
 
+class _Adaptive:
+    """A test-local controller (the select/update protocol): cycles through the
+    arms, lengthens the draft after a fully accepted round and shortens it
+    (down to 0, a plain full-KV step) after a rejection."""
+
+    def __init__(self, arms, gamma=2, gamma_max=9):
+        self.arms, self.gamma, self.gamma_max, self.n = list(arms), gamma, gamma_max, 0
+
+    def select(self, ctx, key=None):
+        arm = self.arms[self.n % len(self.arms)]
+        self.n += 1
+        return arm, self.gamma
+
+    def update(self, cfg, gamma, accepted, ctx, key=None):
+        if gamma == 0:
+            self.gamma = 1
+        elif accepted == gamma:
+            self.gamma = min(self.gamma_max, gamma + 2)
+        else:
+            self.gamma = max(0, accepted - 1)
+
+
 def test_controller_driven_run_is_lossless(dev, tiny_setup):
-    from draftkv import CostModel, DraftKVEngine, ThompsonController, default_arms
+    from draftkv import DraftKVEngine, default_arms
     m, prompt, base = tiny_setup
-    cm = CostModel(n_layers=m.n_layers, n_kv_heads=m.n_heads, d_head=m.d_head, weight_bytes=2.0e6,
-                   bandwidth=2.0e10, full_kv_bandwidth=6.4e8, hbm_kv_budget=2.0e5)
-    r = DraftKVEngine(m, ThompsonController(cm, default_arms(), seed=3), seed=0).generate(prompt, 32, 0.0)
+    ctrl = _Adaptive(default_arms())
+    r = DraftKVEngine(m, ctrl, seed=0).generate(prompt, 32, 0.0)
     assert r.tokens == base
     assert r.verify_passes <= r.new_tokens
+    assert len({x.cfg for x in r.rounds}) > 3 and len({x.gamma for x in r.rounds}) > 2
 
 
 @pytest.mark.parametrize("attn_bias", [False, True])
