@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--workload", choices=["e2e", "kernels", "copy", "requant", "accept"], default="e2e")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=32768)
-    ap.add_argument("--gamma", type=int, default=16)
+    ap.add_argument("--gamma", type=int, default=20)
     ap.add_argument("--temperature", type=float, default=0.8)
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--keep", type=float, default=0.25)
@@ -237,19 +237,43 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
     return out
 
 
-def cpu_baseline(ctx: int, gamma: int, T: float, bits: int, keep: float, group: int, tokens_per_round: float):
-    """The numpy oracle on a bounded sample of the same round: one sequence,
-    one decode round (gamma drafts, verify, accept, rollback, resync) of the
-    Llama-3-8B shape with 1 and with 2 decoder layers over ctx synthetic rows;
-    the per-layer time is extrapolated to 32 layers. The rate is
-    ``tokens_per_round`` (per sequence, as measured on the GPU at the same
-    config) over that round time. Returns (tok/s, sample)."""
+def cpu_baseline(ctx: int, T: float, arms: list):
+    """The numpy oracle on a bounded sample of the timed rounds: for each arm
+    the GPU ran, one sequence, one decode round (gamma drafts at the arm's
+    mean timed gamma, verify, accept, rollback, resync) of the Llama-3-8B
+    shape with no decoder layer and with one over ctx synthetic rows, the
+    per-layer time extrapolated to 32 layers; first with every BLAS thread,
+    then with one. ``arms``: [(bits, keep, group, gamma, rounds, tokens per
+    round per sequence)] as measured on the GPU. The rate mixes the arms' rounds
+    as the timed region did: sum(rounds x tokens per round) / sum(rounds x
+    round time). Returns (tok/s all threads, tok/s 1 thread, threads, sample)."""
     import numpy as np
-    from oracle.caches import CompressedKVCache, FullKVCache
-    from oracle.config import Cfg
-    from oracle.engine import Engine, fixed
-    from oracle.models import LlamaLike
+    from threadpoolctl import threadpool_limits
 
+    w = _oracle_llama_weights(ctx)
+    per_arm, lines = [], []
+    for bits, keep, group, gamma, rounds, tpr in arms:
+        t_all = _oracle_round_time(w, ctx, gamma, T, bits, keep, group)
+        with threadpool_limits(limits=1):
+            t_one = _oracle_round_time(w, ctx, gamma, T, bits, keep, group)
+        per_arm.append((rounds, tpr, t_all[2], t_one[2]))
+        lines.append(f"int{bits} g{group} keep {keep} at gamma {gamma}: 0/1 layers {t_all[0]:.2f}/{t_all[1]:.2f} s, "
+                     f"32 layers {t_all[2]:.1f} s per round ({t_one[2]:.1f} s on 1 thread), "
+                     f"{tpr:.2f} tokens/round over {rounds} GPU rounds")
+    tok = sum(r * t for r, t, _, _ in per_arm)
+    v_all = tok / sum(r * a for r, _, a, _ in per_arm)
+    v_one = tok / sum(r * o for r, _, _, o in per_arm)
+    sample = ("numpy oracle, 1 sequence, one decode round per timed arm of the Llama-3-8B shape at ctx "
+              f"{ctx} (T {T}), timed with 0 and 1 decoder layers and extrapolated to 32; "
+              + "; ".join(lines) + "; rate = the timed region's round mix over the oracle's round times")
+    return v_all, v_one, blas_threads(), sample
+
+
+def _oracle_llama_weights(ctx: int):
+    """One decoder layer, embedding and head of the Llama-3-8B shape (float32,
+    uniform +-0.035, the oracle's own draw), ctx-1 rows of N(0,1) K/V per
+    layer and a ctx-token prompt."""
+    import numpy as np
     d, H, KV, D, ff, V = 4096, 32, 8, 128, 14336, 128256
     rng = np.random.default_rng(0)
 
@@ -258,7 +282,7 @@ def cpu_baseline(ctx: int, gamma: int, T: float, bits: int, keep: float, group: 
 
     emb = R(V, d)
     layer_w = {}
-    for i in range(2):
+    for i in range(1):
         p = f"model.layers.{i}."
         layer_w[p + "input_layernorm.weight"] = np.ones(d, np.float32)
         layer_w[p + "post_attention_layernorm.weight"] = np.ones(d, np.float32)
@@ -270,16 +294,29 @@ def cpu_baseline(ctx: int, gamma: int, T: float, bits: int, keep: float, group: 
         layer_w[p + "mlp.up_proj.weight"] = R(ff, d)
         layer_w[p + "mlp.down_proj.weight"] = R(d, ff)
     kv = [(rng.standard_normal((ctx - 1, KV, D)).astype(np.float32),
-           rng.standard_normal((ctx - 1, KV, D)).astype(np.float32)) for _ in range(2)]
-    cfg = Cfg(bits, keep, group=group, meta="f16")
+           rng.standard_normal((ctx - 1, KV, D)).astype(np.float32))]
     prompt = [int(x) for x in rng.integers(0, V, ctx)]
-    times, emitted = [], 0
-    for n_layers in (1, 2):
-        w = {"model.embed_tokens.weight": emb, "model.norm.weight": np.ones(d, np.float32)}
-        w.update({k: v for k, v in layer_w.items() if int(k.split(".")[2]) < n_layers})
+    return {"emb": emb, "layers": layer_w, "kv": kv, "prompt": prompt}
+
+
+def _oracle_round_time(w, ctx, gamma, T, bits, keep, group):
+    """Seconds of one oracle decode round with no decoder layer (embedding,
+    head, sampling, accept) and with one, and the 32-layer extrapolation."""
+    import numpy as np
+    from oracle.caches import CompressedKVCache, FullKVCache
+    from oracle.config import Cfg
+    from oracle.engine import Engine, fixed
+    from oracle.models import LlamaLike
+    d, H, KV, D, V = 4096, 32, 8, 128, 128256
+    emb, layer_w, kv, prompt = w["emb"], w["layers"], w["kv"], w["prompt"]
+    cfg = Cfg(bits, keep, group=group, meta="f16")
+    times = []
+    for n_layers in (0, 0, 1):        # the first pass only pages the head in
+        wl = {"model.embed_tokens.weight": emb, "model.norm.weight": np.ones(d, np.float32)}
+        wl.update({k: v for k, v in layer_w.items() if int(k.split(".")[2]) < n_layers})
         c = dict(num_hidden_layers=n_layers, hidden_size=d, num_attention_heads=H, num_key_value_heads=KV,
                  head_dim=D, vocab_size=V, rms_norm_eps=1e-5, rope_theta=500000.0)
-        m = LlamaLike(w, c)
+        m = LlamaLike(wl, c)
 
         full = FullKVCache(n_layers)
         for L in range(n_layers):
@@ -289,16 +326,10 @@ def cpu_baseline(ctx: int, gamma: int, T: float, bits: int, keep: float, group: 
         comp.sync_from(full, 0)
         # one round, timed: drafts + verify + accept + rollback + resync
         t0 = time.perf_counter()
-        r = _oracle_one_round(eng, m, prompt, full, comp, gamma, T)
+        _oracle_one_round(eng, m, prompt, full, comp, gamma, T)
         times.append(time.perf_counter() - t0)
-        emitted = r
-    per_layer = max(times[1] - times[0], 1e-9)
-    t32 = times[0] + 31 * per_layer
-    sample = (f"numpy oracle, 1 sequence, 1 decode round (gamma {gamma}, T {T}, int{bits} g{group} keep {keep}) "
-              f"of the Llama-3-8B shape at ctx {ctx} with 1 and 2 layers ({times[0]:.1f} s, {times[1]:.1f} s), "
-              f"round time extrapolated to 32 layers = {t32:.1f} s; rate = {tokens_per_round:.2f} tokens/round "
-              f"(GPU-measured acceptance at this config) / round time ({emitted} emitted in the sampled round)")
-    return tokens_per_round / t32, sample
+    t0, t1 = times[1], times[2]
+    return t0, t1, t0 + 32 * max(t1 - t0, 1e-9)
 
 
 def _oracle_one_round(eng, m, prompt, full, comp, gamma, T):
@@ -355,7 +386,7 @@ class ScheduledArms:
     Gamma 0 -- a plain full-KV step -- when no draft length beats it, as the
     reference's controller declines to draft (controller.py:149-152)."""
 
-    def __init__(self, arms, period, cost, ctx, gamma_max=16, decay=0.98):
+    def __init__(self, arms, period, cost, ctx, gamma_max=20, decay=0.98):
         from draftkv.throughput import best_gamma
         self.best_gamma = best_gamma
         self.arms, self.period, self.cost, self.ctx = list(arms), period, cost, ctx
@@ -440,7 +471,12 @@ def run_e2e(args):
     timers = [t for t in (t_draft, t_ver, t_req) if t is not None]
     for t in timers:
         t.on = True
-    log(f"timing {args.steps} rounds (arm switch every {args.period} rounds)")
+    # the timed rounds cover both arms: the first arm for `period` rounds, then
+    # the second; with fewer than 2 x period timed rounds the switch comes
+    # half way through (so the requantize of the switch is timed too)
+    period = args.period if args.steps >= 2 * args.period else max(1, args.steps // 2)
+    ctrl.period, ctrl.round = period, 0
+    log(f"timing {args.steps} rounds (arm switch every {period} rounds)")
     emitted = 0
     arm_time = {}      # arm -> [seconds, tokens, rounds] (host time per round; a declined round's
                        # GPU time lands in the next round that waits for the device)
@@ -555,12 +591,15 @@ def run_e2e(args):
                 "outlier channels x8 written straight into the paged cache in place of a 32k prefill)",
         "config": {"workload": f"Llama-3-8B-shape decode rounds, batch {b}, ctx {ctx}, drafter arms int8 g64 "
                                f"keep 1.0 / int{args.bits} g{args.group} keep {args.keep} (fp16 scale/zero) "
-                               f"switched every {args.period} rounds, gamma by cost model (max {gmax}; 0 = a "
+                               f"switched every {period} rounds of the timed region (every {args.period}, or half "
+                               f"way when fewer than {2 * args.period} rounds are timed), gamma by cost model (max {gmax}; 0 = a "
                                f"full-KV step when drafting does not pay; "
                                f"{'nominal 8 TB/s' if calibrated is None else 'fitted to this device'}), "
                                f"T {args.temperature} rejection sampling, 16-token pages, shuffled block tables",
-                   "layers": L, "batch": b, "ctx": ctx, "temperature": args.temperature,
+                   "layers": L, "batch": b, "ctx": ctx, "temperature": args.temperature, "switch_period": period,
                    "rounds_per_arm": {k: v[2] // b for k, v in per_arm.items()},
+                   "tok_s_per_arm": {a.label(): v[1] / v[0] for a, v in arm_time.items()},
+                   "gamma_mean_per_arm": {k: v[1] / max(v[2], 1) for k, v in per_arm.items()},
                    "acceptance_per_arm": alpha, "acceptance": acc_total / max(drafted, 1),
                    "gamma_mean": float(np.mean(ctrl.gammas[-args.steps:])),
                    "tokens_per_round": emitted / args.steps / b,
@@ -594,11 +633,18 @@ def run_e2e(args):
     del batch, comp, full, model, eng
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        log("cpu baseline (numpy oracle, bounded sample)")
-        v, sample = cpu_baseline(ctx, max(1, round(out["config"]["gamma_mean"])), args.temperature, args.bits,
-                                 args.keep, args.group, emitted / args.steps / b)
-        out["cpu_baseline"] = {"value": v, "unit": "tok/s", "cores": blas_threads(), "kind": "port",
-                               "sample": sample}
+        log("cpu baseline (numpy oracle, bounded sample of the timed arms)")
+        timed_arms = []
+        for arm in arms:
+            st_ = per_arm.get(arm.label())
+            if not st_:
+                continue
+            nr = st_[2] // b
+            timed_arms.append((arm.bits, arm.keep_frac, arm.group, round(st_[1] / max(st_[2], 1)), nr,
+                               arm_time[arm][1] / max(arm_time[arm][2], 1) / b))
+        v, v1, threads, sample = cpu_baseline(ctx, args.temperature, timed_arms)
+        out["cpu_baseline"] = {"value": v, "unit": "tok/s", "cores": threads, "kind": "port",
+                               "value_1thread": v1, "sample": sample}
     else:
         out["cpu_baseline"] = None
     return out

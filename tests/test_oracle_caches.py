@@ -164,3 +164,27 @@ def test_heavy_hitters_survive_eviction():
     comp.append(0, x[:4], x[:4], np.arange(6, 10))     # budget 5: rows 0,4,5,6,7,8,9
     # unprotected: 4 (score 9), 5, 6, 7 (score 0) -> drop the two oldest zeros: 5, 6
     assert comp.pos[0].tolist() == [0, 4, 7, 8, 9]
+
+
+@pytest.mark.parametrize("cfg", [Cfg(4, 0.25, group=32, meta="f16"), Cfg(8, 1.0, group=64, meta="f16"),
+                                 Cfg(2, 0.5), Cfg(3, 0.3, 2, 5)])
+def test_build_equals_quantizing_only_the_kept_rows(cfg):
+    """A build (sync_from(full, 0): quantize every row, then one eviction with
+    all scores 0) leaves exactly the closed-form kept rows, each quantized as
+    if it were quantized alone: the quantizer works row by row, so parity
+    tests at large shapes may quantize only the kept rows."""
+    from oracle.quant import quantize_codes
+    rng = np.random.default_rng(cfg.bits)
+    n, H, D = 1001, 3, 128
+    k = rng.standard_normal((n, H, D)).astype(np.float32)
+    v = rng.standard_normal((n, H, D)).astype(np.float32)
+    full = FullKVCache(1)
+    full.append(0, k, v, np.arange(n))
+    comp = CompressedKVCache(1, cfg)
+    comp.sync_from(full, 0)
+    kept = closed_form_kept(n, cfg, n)
+    assert comp.pos[0].tolist() == kept
+    for got, x in ((comp.kq[0], k), (comp.vq[0], v)):
+        want = quantize_codes(x[kept], cfg.bits, cfg.group, cfg.meta)
+        for a, b in zip(got, want[:3]):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
