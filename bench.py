@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--gamma", type=int, default=20)
+    ap.add_argument("--verify-gamma", type=int, default=8,
+                    help="--workload kernels: the verify pass runs verify_gamma + 1 queries per sequence")
     ap.add_argument("--temperature", type=float, default=0.8)
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--keep", type=float, default=0.25)
@@ -478,20 +480,29 @@ def run_e2e(args):
     ctrl.period, ctrl.round = period, 0
     log(f"timing {args.steps} rounds (arm switch every {period} rounds)")
     emitted = 0
-    arm_time = {}      # arm -> [seconds, tokens, rounds] (host time per round; a declined round's
-                       # GPU time lands in the next round that waits for the device)
+    # arm -> [seconds, tokens, rounds]: the rounds of one arm run back to back,
+    # and the device is drained once at each switch (and at the end), so an
+    # arm's time holds all of its rounds' device work, its requantize included
+    arm_time = {}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    seg_arm, seg_t0 = None, t0
     for _ in range(args.steps):
-        tr = time.perf_counter()
+        nxt = ctrl.arms[(ctrl.round // ctrl.period) % len(ctrl.arms)]
+        if seg_arm is not None and nxt != seg_arm:
+            torch.cuda.synchronize()
+            now = time.perf_counter()
+            arm_time[seg_arm][0] += now - seg_t0
+            seg_t0 = now
+        seg_arm = nxt
         batch.step()
         emitted += batch.last_emitted
         at = arm_time.setdefault(ctrl.last_arm, [0.0, 0, 0])
-        at[0] += time.perf_counter() - tr
         at[1] += batch.last_emitted
         at[2] += 1
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    arm_time[seg_arm][0] += t0 + dt - seg_t0
     batch.resolve_tokens()     # the declined rounds' tokens, already on the host
     for t in timers:
         t.on = False
@@ -660,7 +671,7 @@ def run_kernels(args):
     from draftkv import CompressedKVCache, CompressionConfig
     L = max(2, min(args.layers, 8))
     Hkv, D, Hq = 8, 128, 32
-    b, ctx, gamma = args.batch, args.ctx, args.gamma
+    b, ctx, gamma = args.batch, args.ctx, args.verify_gamma
     log(f"synthetic full cache: batch {b}, ctx {ctx}, {L} layers")
     full = shuffled_full_cache(L, Hkv, D, b, ctx + 1, gamma + 16, torch.bfloat16)
     arm = CompressionConfig(args.bits, args.keep, group=args.group, scale_fp16=True)

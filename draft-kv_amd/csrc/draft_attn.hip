@@ -477,8 +477,12 @@ struct SplitCore {
 #pragma unroll
         for (int x = 1; x < 8; ++x) sum += pv[x];
         l_run += lanegroup_sum(sum);
-        // ---- PV: B[row (jj, e)][col] = f16(p * scaleV), rows e<4: 4jj+e, e>=4: 16+4jj+e-4
-        f16x8_t bop;
+        // ---- PV: B[row (jj, e)][col] = p * scaleV as an f16 pair hi + lo,
+        // rows e<4: 4jj+e, e>=4: 16+4jj+e-4. One f16 alone would carry an
+        // error of 2^-12 |v - zero| per row, which a peaked softmax over a
+        // wide-range (outlier) channel does not average away; the pair
+        // carries ~22 bits, and the codes (A) are exact.
+        f16x8_t bhi, blo;
         float zs = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -489,15 +493,17 @@ struct SplitCore {
                 sc = ok ? sc : 0.0f;
                 lo = ok ? lo : 0.0f;
             }
-            // one rounding of the exact product (v_fma_mix to f16); p, sc >= 0
-            bop[e] = (_Float16)fmaf(pv[e], sc, 0.0f);
+            const float x = pv[e] * sc;            // p, sc >= 0
+            bhi[e] = (_Float16)x;
+            blo[e] = (_Float16)(x - (float)bhi[e]);   // exact difference, rounded once
             zs = fmaf(pv[e], lo, zs);
         }
         zsum += zs;
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
             const f16x8_t av = codes_to_f16<CB>(cur.v + t * (CB / 4));
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bop, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bhi, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, blo, acc[t], 0, 0, 0);
         }
     }
 
@@ -873,8 +879,8 @@ __global__ void __launch_bounds__(64 * COMB_WAVES) draft_combine_kernel(dkv_draf
     so[w][lane + WAVE] = o1;
     if (lane == 0) sl[w] = l;
     __syncthreads();
-    if (threadIdx.x < D) {
-        const int d = threadIdx.x;
+    // every channel, whatever the block width (one wave covers 64 per pass)
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float lt = 0.0f, ot = 0.0f;
         for (int i = 0; i < nw; ++i) {
             lt += sl[i];

@@ -140,11 +140,11 @@ def test_requantize_both_arms_and_switches_bit_exact(dev, cache):
     md = _mirror([INT8] * L, [INT8, INT4])
     md.sync_from(full, 0)
     _check_build(md, host, INT8, [0, 7, 18, 31])
-    md.rebuild_layers(full, [LAYER], [INT8, INT4])
+    md.rebuild_layers(full, [LAYER], [_dcfg(INT8), _dcfg(INT4)])
     assert md.cfgs[LAYER] == _dcfg(INT4) and md.cfgs[0] == _dcfg(INT8)
     _check_build(md, host, INT4, list(range(B)))
     # back to int8: the pages held int4 rows in another layout
-    md.rebuild_layers(full, [LAYER], [INT8, INT8])
+    md.rebuild_layers(full, [LAYER], [_dcfg(INT8), _dcfg(INT8)])
     _check_build(md, host, INT8, [3, 12, 25])
     # the other layer was never touched
     g0 = md.read_codes(0, 5)
@@ -225,7 +225,7 @@ def test_draft_step_eviction_and_resync_match_oracle(dev, cache):
         assert y["pos"].tolist() == o.pos[0].tolist(), f"seq {s}: kept set after the resync"
         assert np.array_equal(y["score"], o.score[0]), f"seq {s}: scores after the resync"
         _same_codes(y, o.kq[0], o.vq[0], f"seq {s} resync")
-        return s
+        return len(o.pos[0])
 
-    assert sorted(_POOL.map(one, range(B))) == list(range(B))
-    assert (md.rows()[:, LAYER] == [budget(cfg, int(n)) for n in LENS]).all()
+    kept = list(_POOL.map(one, range(B)))
+    assert md.rows()[:, LAYER].tolist() == kept
