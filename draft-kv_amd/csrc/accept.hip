@@ -15,6 +15,8 @@
 // Sampling one row (dkv_sample) is the gamma = 0 case: the bonus row is it.
 #include "dkv_common.h"
 
+#include <mutex>
+
 namespace dkv {
 
 constexpr int VCH = 4096;
@@ -417,4 +419,57 @@ extern "C" int dkv_sample(const float* logits, int64_t row_stride, int32_t batch
     int32_t* scratch_i = reinterpret_cast<int32_t*>(w + ((acc_ws + 255) / 256) * 256);
     return dkv_accept(logits, nullptr, nullptr, batch, 0, vocab, temperature, u, scratch_i, tokens,
                       scratch_i + batch, work, acc_ws, stream);
+}
+
+// ---------------------------------------------------------------- no allocation
+// dkv_accept for callers that cannot allocate (code under stream capture,
+// serving loops that forbid it): the workspace is this file-scope device
+// array, one copy per GPU for the life of the process. Its address on a
+// device comes from hipGetSymbolAddress, taken once per device with that
+// device current; the array's name is never used as a device address on the
+// host. Every call on a GPU shares that GPU's array, so calls that overlap on
+// one GPU (two streams, two host threads) race. The kernels write every
+// workspace entry before they read it, so nothing needs clearing between
+// calls.
+static __device__ __align__(256) unsigned char scratch[DKV_ACCEPT_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+int scratch_of_current_device(void** out, const char* who) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return dkv::fail(DKV_ELAUNCH, std::string(who) + ": hipGetDevice: " + hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return dkv::fail(DKV_EINVAL, std::string(who) + ": device id out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return dkv::fail(DKV_ELAUNCH, std::string(who) + ": hipGetSymbolAddress(scratch): " +
+                                              (e != hipSuccess ? hipGetErrorString(e) : "null address"));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DKV_OK;
+}
+}  // namespace
+
+extern "C" int dkv_accept_noalloc(const float* target, const float* draft, const int32_t* draft_tokens,
+                                  int32_t batch, int32_t gamma, int32_t vocab, float temperature, const double* u,
+                                  int32_t* accepted, int32_t* next_token, int32_t* n_uniforms,
+                                  dkv_stream_t stream) {
+    DKV_REQUIRE(batch > 0 && gamma >= 0 && vocab > 0, "dkv_accept_noalloc: bad sizes");
+    const size_t need = dkv_accept_workspace(batch, gamma, vocab);
+    if (need > DKV_ACCEPT_SCRATCH_BYTES)
+        return dkv::fail(DKV_ECAPACITY, "dkv_accept_noalloc: batch " + std::to_string(batch) + ", gamma " +
+                                            std::to_string(gamma) + ", vocab " + std::to_string(vocab) + " need " +
+                                            std::to_string(need) + " B of workspace; the static scratch holds " +
+                                            std::to_string((size_t)DKV_ACCEPT_SCRATCH_BYTES));
+    void* ws = nullptr;
+    int rc = scratch_of_current_device(&ws, "dkv_accept_noalloc");
+    if (rc) return rc;
+    return dkv_accept(target, draft, draft_tokens, batch, gamma, vocab, temperature, u, accepted, next_token,
+                      n_uniforms, ws, DKV_ACCEPT_SCRATCH_BYTES, stream);
 }

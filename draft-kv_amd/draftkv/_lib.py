@@ -58,6 +58,7 @@ _SIGS = {
     "dkv_sample": (C.c_int, [P, I64, I32, I32, F32, P, P, P, SZ, P]),
     "dkv_accept_workspace": (SZ, [I32, I32, I32]),
     "dkv_accept": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P, SZ, P]),
+    "dkv_accept_noalloc": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P]),
     "dkv_embed": (C.c_int, [P, I32, P, I32, I32, P, P, P, P]),
     "dkv_rmsnorm": (C.c_int, [P, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_layernorm": (C.c_int, [P, P, P, I32, I32, I32, F32, P, I32, P]),

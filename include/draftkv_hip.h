@@ -216,6 +216,20 @@ int dkv_accept(const float* target, const float* draft, const int32_t* draft_tok
                int32_t* accepted, int32_t* next_token, int32_t* n_uniforms, void* work,
                size_t work_bytes, dkv_stream_t stream);
 
+/* dkv_accept with no workspace argument and no allocation: the workspace is a
+ * static device array of DKV_ACCEPT_SCRATCH_BYTES inside the library (one per
+ * GPU, held until the process ends). No counterpart in the reference; it is
+ * for callers that cannot allocate device memory -- code under stream/graph
+ * capture, serving loops that forbid hipMalloc. Returns DKV_ECAPACITY when
+ * dkv_accept_workspace(batch, gamma, vocab) exceeds the scratch (at vocab
+ * 128256 it holds batch 128 with gamma <= 24). Calls that overlap on one GPU
+ * share the array and race; calls in stream order do not. */
+#define DKV_ACCEPT_SCRATCH_BYTES ((size_t)4 << 20)
+int dkv_accept_noalloc(const float* target, const float* draft, const int32_t* draft_tokens,
+                       int32_t batch, int32_t gamma, int32_t vocab, float temperature,
+                       const double* u, int32_t* accepted, int32_t* next_token,
+                       int32_t* n_uniforms, dkv_stream_t stream);
+
 /* ------------------------------------------------------ model forward ops */
 /* The non-attention pieces of the model forwards (reference
  * draftkv/model.py:100-133, draftkv/gpt2.py:182-213, draftkv/llama.py:175-225)

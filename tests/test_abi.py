@@ -48,3 +48,17 @@ def test_host_validation_errors_without_gpu():
     assert rc == -1 and b"bits" in L.dkv_last_error()
     with pytest.raises(ValueError, match="bits"):
         _lib.check(rc, "dkv_quantize")
+
+
+def test_noalloc_accept_refuses_oversize_without_gpu():
+    """The no-allocation accept checks its request against the static
+    scratch on the host, before touching a device."""
+    from draftkv import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    rc = L.dkv_accept_noalloc(p, p, p, 100000, 20, 128256, 0.8, p, p, p, p, None)
+    assert rc == -4 and b"static scratch" in L.dkv_last_error()
+    rc = L.dkv_accept_noalloc(p, p, p, 0, 20, 128256, 0.8, p, p, p, p, None)
+    assert rc == -1

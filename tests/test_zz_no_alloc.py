@@ -1,0 +1,66 @@
+"""dkv_accept_noalloc -- the accept decision with its workspace in the
+library's static device scratch (no allocation) -- against dkv_accept with a
+caller workspace, through the C ABI: accepted counts, next tokens and draws
+consumed equal bit for bit, greedy and sampled, on two calls in a row (the
+second smaller, so it runs over what the first left in the scratch), and a
+request larger than the scratch is refused before any launch."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, b, gamma, V, dev):
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal((b, 1, V)).astype(np.float32) * 2
+    target = (base + 0.3 * rng.standard_normal((b, gamma + 1, V))).astype(np.float32)
+    draft = (base[:, :1] + 0.3 * rng.standard_normal((b, gamma, V))).astype(np.float32)
+    toks = np.zeros((b, gamma), np.int32)
+    for s in range(b):
+        for i in range(gamma):
+            toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.8 else int(rng.integers(V))
+    u = rng.random((b, gamma + 1))
+    return [torch.from_numpy(x).to(dev) for x in (target, draft, toks, u)]
+
+
+def _run(fn_noalloc, target, draft, toks, u, T):
+    from draftkv._lib import check, lib
+    b, g1, V = target.shape
+    gamma = g1 - 1
+    outs = [torch.full((b,), -7, dtype=torch.int32, device=target.device) for _ in range(3)]
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = (target.data_ptr(), draft.data_ptr(), toks.data_ptr(), b, gamma, V, float(T), u.data_ptr(),
+            *(o.data_ptr() for o in outs))
+    if fn_noalloc:
+        check(lib().dkv_accept_noalloc(*args, stream), "dkv_accept_noalloc")
+    else:
+        nbytes = lib().dkv_accept_workspace(b, gamma, V)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=target.device)
+        check(lib().dkv_accept(*args, ws.data_ptr(), nbytes, stream), "dkv_accept")
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in outs]
+
+
+@pytest.mark.parametrize("T", [0.0, 0.8])
+def test_noalloc_equals_workspace_entry_point_twice(dev, T):
+    for seed, (b, gamma, V) in ((1, (16, 8, 50257)), (2, (5, 2, 3000))):
+        target, draft, toks, u = _case(seed + int(T * 10), b, gamma, V, dev)
+        want = _run(False, target, draft, toks, u, T)
+        got = _run(True, target, draft, toks, u, T)
+        for w, g, name in zip(want, got, ("accepted", "next_token", "n_uniforms")):
+            assert np.array_equal(w, g), (b, gamma, V, name)
+        assert (want[0] >= 0).all() and (want[0] <= gamma).all()
+
+
+def test_noalloc_refuses_more_than_the_scratch(dev):
+    from draftkv._lib import lib
+    L = lib()
+    nbytes = L.dkv_accept_workspace(4096, 24, 128256)
+    assert nbytes > (4 << 20)
+    rc = L.dkv_accept_noalloc(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), 4096, 24, 128256, 0.8,
+                              C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None)
+    assert rc == -4 and b"static scratch" in L.dkv_last_error()
