@@ -54,7 +54,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--period", type=int, default=64)
     ap.add_argument("--baseline-steps", type=int, default=8)
-    ap.add_argument("--workload", choices=["e2e", "kernels", "copy", "requant", "accept"], default="e2e")
+    ap.add_argument("--workload", choices=["e2e", "kernels", "copy", "requant", "accept", "gemm"], default="e2e")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--gamma", type=int, default=20)
@@ -845,6 +845,61 @@ def run_accept(args):
             "cpu_baseline": None}
 
 
+def run_gemm(args):
+    """The four projection GEMMs of a Llama-3-8B decoder layer (qkv 6144x4096,
+    o 4096x4096 on the float32 attention output, gate/up 28672x4096 with the
+    SwiGLU epilogue, down 4096x14336), bf16 weights N(0, 0.02), at the row
+    counts of a b=32 decode step (M = 32), a gamma-2 verify (96) and a gamma-8
+    verify (288), rotating over 8 layers' weights (3.5 GB, so every call
+    streams its weights from HBM). Each call timed with HIP events on the
+    launch stream; algorithmic bytes: the weights once, x once, y once."""
+    import torch
+    from draftkv import ops
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    d, ff, nq = 4096, 14336, 6144
+    nl = 8
+    shapes = {"qkv": (nq, d, torch.bfloat16, False), "o": (d, d, torch.float32, False),
+              "gate_up": (2 * ff, d, torch.bfloat16, True), "down": (d, ff, torch.bfloat16, False)}
+    W = {k: [torch.empty((n, kk), dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
+             for _ in range(nl)] for k, (n, kk, _, _) in shapes.items()}
+    res = {}
+    for M in (32, 96, 288):
+        X = {k: torch.randn((M, kk), generator=g, device=dev).to(xd) for k, (n, kk, xd, _) in shapes.items()}
+        per = {}
+        for rep in range(args.warmup + args.steps):
+            for i in range(nl):
+                for k, (n, kk, xd, sw) in shapes.items():
+                    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    s_ev.record()
+                    ops.gemm_bf16(X[k], W[k][i], None, torch.bfloat16, swiglu=sw)
+                    e_ev.record()
+                    if rep >= args.warmup:
+                        per.setdefault(k, []).append((s_ev, e_ev))
+        torch.cuda.synchronize()
+        row = {}
+        tot_b = tot_us = 0.0
+        for k, (n, kk, xd, sw) in shapes.items():
+            us = 1e3 * sum(a.elapsed_time(c) for a, c in per[k]) / len(per[k])
+            nbytes = n * kk * 2 + M * kk * (4 if xd == torch.float32 else 2) + M * (n // 2 if sw else n) * 2
+            row[k] = {"us": us, "GB/s": nbytes / (us * 1e-6) / 1e9, "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+            tot_b += nbytes
+            tot_us += us
+        row["layer"] = {"us": tot_us, "GB/s": tot_b / (tot_us * 1e-6) / 1e9,
+                        "frac": tot_b / (tot_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        res[f"M={M}"] = row
+        log(f"M={M}: layer {tot_us:.1f} us, {row['layer']['GB/s']:.0f} GB/s")
+    main_ = res["M=32"]["layer"]
+    return {"metric": "Llama-3-8B layer GEMMs (bf16 weights) GB/s at M=32", "value": main_["GB/s"], "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": main_["us"] / 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "qkv / o / gate_up+SwiGLU / down GEMMs of a Llama-3-8B layer, M = 32, 96, 288"},
+            "roofline": {"bound": "hbm", "achieved": main_["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": main_["frac"], "traffic": None},
+            "kernels": res, "cpu_baseline": None}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -856,7 +911,7 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
     out = {"e2e": run_e2e, "kernels": run_kernels, "copy": run_copy, "requant": run_requant,
-           "accept": run_accept}[args.workload](args)
+           "accept": run_accept, "gemm": run_gemm}[args.workload](args)
     print(json.dumps(out), flush=True)
 
 

@@ -127,24 +127,32 @@ __device__ __forceinline__ double prob(float x, const RowNorm& r, float T) {
     return exp((double)x * (1.0 / (double)T) - r.m) * r.iS;
 }
 
-// One wave per sequence: the lanes merge each row's chunk statistics, then
-// lane 0 runs the accept tests (a handful of reads) and picks the final
-// distribution.
-__global__ void __launch_bounds__(WAVE) decide_kernel(const float* __restrict__ target,
-                                                      const float* __restrict__ draft,
-                                                      const int32_t* __restrict__ draft_tokens, int gamma, int vocab,
-                                                      float T, const double* __restrict__ u, int n_chunks,
-                                                      const ChunkStat* __restrict__ stats,
-                                                      RowNorm* __restrict__ norms, SeqState* __restrict__ state,
-                                                      int32_t* accepted, int32_t* next_token,
-                                                      int32_t* n_uniforms) {
-    const int s = blockIdx.x, lane = threadIdx.x;
+// One block per sequence, one wave per row (rows w, w + DECIDE_WAVES, ...):
+// each wave merges its row's chunk statistics. Then the lanes of wave 0
+// evaluate the accept test's p and q of every drafted position at once (the
+// scattered reads in flight together), and lane 0 walks the tests in order --
+// the same decisions, in the same order, as one lane reading as it goes.
+constexpr int DECIDE_WAVES = 16;
+constexpr int PICK_MAX_CHUNKS = 1024;   // vocab up to 4M
+constexpr int DECIDE_MAX_GAMMA = 64;
+__global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float* __restrict__ target,
+                                                                     const float* __restrict__ draft,
+                                                                     const int32_t* __restrict__ draft_tokens,
+                                                                     int gamma, int vocab, float T,
+                                                                     const double* __restrict__ u, int n_chunks,
+                                                                     const ChunkStat* __restrict__ stats,
+                                                                     RowNorm* __restrict__ norms,
+                                                                     SeqState* __restrict__ state, int32_t* accepted,
+                                                                     int32_t* next_token, int32_t* n_uniforms) {
+    const int s = blockIdx.x, lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
     const bool samp = T > 0.0f;
     const int R = 2 * gamma + 1;
     const ChunkStat* st = stats + (int64_t)s * R * n_chunks;
     const int n_rows = samp ? R : gamma + 1;
     RowNorm* nr = norms + (int64_t)s * R;
-    for (int r = 0; r < n_rows; ++r) {
+    __shared__ RowNorm snr[2 * DECIDE_MAX_GAMMA + 1];
+    __shared__ double sp[DECIDE_MAX_GAMMA], sq[DECIDE_MAX_GAMMA];
+    for (int r = w; r < n_rows; r += DECIDE_WAVES) {
         const ChunkStat* sr = st + (int64_t)r * n_chunks;
         float mx = -INFINITY;
         int arg = INT_MAX;
@@ -170,8 +178,29 @@ __global__ void __launch_bounds__(WAVE) decide_kernel(const float* __restrict__ 
             rn.S = wave_sum_d(S);
             rn.iS = 1.0 / rn.S;
         }
-        if (lane == 0) nr[r] = rn;
+        if (lane == 0) {
+            nr[r] = rn;
+            snr[r] = rn;
+        }
     }
+    __syncthreads();
+    if (w != 0) return;
+    // p and q of the drafted token at every position (lane i: position i)
+    if (samp) {
+        for (int i = lane; i < gamma; i += WAVE) {
+            const int d = draft_tokens[(int64_t)s * gamma + i];
+            double p = 0.0, q = 0.0;
+            if (d >= 0 && d < vocab) {
+                p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], snr[i], T);
+                q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], snr[gamma + 1 + i], T);
+            }
+            sp[i] = p;
+            sq[i] = q;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane != 0) return;
     int acc = 0, used = 0;
     const double* us = u + (int64_t)s * (gamma + 1);
@@ -182,11 +211,9 @@ __global__ void __launch_bounds__(WAVE) decide_kernel(const float* __restrict__ 
             ok = false;              // not a token of this vocabulary: never read past the row
             if (T > 0.0f) ++used;
         } else if (T <= 0.0f) {
-            ok = nr[i].arg == d;
+            ok = snr[i].arg == d;
         } else {
-            const double p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], nr[i], T);
-            const double q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], nr[gamma + 1 + i], T);
-            const double ratio = q > 0.0 ? p / q : 0.0;
+            const double ratio = sq[i] > 0.0 ? sp[i] / sq[i] : 0.0;
             ok = us[used] < fmin(1.0, ratio);
             ++used;
         }
@@ -195,7 +222,7 @@ __global__ void __launch_bounds__(WAVE) decide_kernel(const float* __restrict__ 
     }
     SeqState ss{0, acc, 0.0};
     if (T <= 0.0f) {
-        next_token[s] = nr[acc].arg;
+        next_token[s] = snr[acc].arg;
         if (acc == gamma) ++used;   // the bonus draw is taken even though p is one-hot
     } else {
         ss.mode = (acc == gamma) ? 1 : 2;
@@ -257,28 +284,36 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
     const ChunkStat* pst = stats + ((int64_t)s * R + ss.row) * n_chunks;
     __shared__ int s_chunk, s_mode;
     __shared__ double s_before, s_target;
+    // the chunk masses, read (and for p, computed) by all threads at once; the
+    // sums over them stay sequential in chunk order on thread 0
+    __shared__ double s_cs[PICK_MAX_CHUNKS], s_pm[PICK_MAX_CHUNKS];
+    {
+        const RowNorm pn = nr[ss.row];
+        for (int c = threadIdx.x; c < n_chunks; c += blockDim.x) {
+            s_cs[c] = cs[c];
+            s_pm[c] = pst[c].sum * exp((double)pst[c].mx * (1.0 / (double)T) - pn.m) * pn.iS;
+        }
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
         int mode = ss.mode;
         double total = 0.0;
-        for (int c = 0; c < n_chunks; ++c) total += cs[c];
+        for (int c = 0; c < n_chunks; ++c) total += s_cs[c];
         // an all-zero residual falls back to p itself (engine.py:210-211); p's
         // chunk masses then come from the row statistics
         const bool from_p = (mode == 2 && !(total > 0.0));
         if (from_p) mode = 1;
-        const RowNorm pn = nr[ss.row];
-        auto chunk_mass = [&](int c) -> double {
-            return from_p ? pst[c].sum * exp((double)pst[c].mx * (1.0 / (double)T) - pn.m) * pn.iS : cs[c];
-        };
+        const double* cmass = from_p ? s_pm : s_cs;
         if (from_p) {
             total = 0.0;
-            for (int c = 0; c < n_chunks; ++c) total += chunk_mass(c);
+            for (int c = 0; c < n_chunks; ++c) total += cmass[c];
         }
         const double tgt = ss.u * total;
         double run = 0.0;
         int chosen = n_chunks - 1;
         bool hit = false;
         for (int c = 0; c < n_chunks; ++c) {
-            const double cm = chunk_mass(c);
+            const double cm = cmass[c];
             if (run + cm > tgt) {
                 chosen = c;
                 hit = true;
@@ -287,7 +322,7 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
             run += cm;
         }
         // rounding carried the draw past the end: scan the last chunk from its start
-        if (!hit) run -= chunk_mass(chosen);
+        if (!hit) run -= cmass[chosen];
         s_chunk = chosen;
         s_mode = mode;
         s_before = run;
@@ -370,6 +405,8 @@ extern "C" int dkv_accept(const float* target, const float* draft, const int32_t
                           dkv_stream_t stream) {
     DKV_REQUIRE(target && accepted && next_token && n_uniforms && u, "dkv_accept: NULL argument");
     DKV_REQUIRE(batch > 0 && gamma >= 0 && vocab > 0, "dkv_accept: bad sizes");
+    DKV_REQUIRE(gamma <= DECIDE_MAX_GAMMA, "dkv_accept: gamma must be at most 64");
+    DKV_REQUIRE(chunks_of(vocab) <= PICK_MAX_CHUNKS, "dkv_accept: vocab too large");
     DKV_REQUIRE(gamma == 0 || draft_tokens, "dkv_accept: draft_tokens is NULL");
     DKV_REQUIRE(temperature <= 0.0f || gamma == 0 || draft, "dkv_accept: draft logits needed when T > 0");
     const size_t need = dkv_accept_workspace(batch, gamma, vocab);
@@ -390,7 +427,8 @@ extern "C" int dkv_accept(const float* target, const float* draft, const int32_t
                        temperature, nc, stats);
     int rc = check_launch("dkv_accept(stats)");
     if (rc) return rc;
-    hipLaunchKernelGGL(decide_kernel, dim3(batch), dim3(WAVE), 0, st, target, draft, draft_tokens, gamma, vocab,
+    hipLaunchKernelGGL(decide_kernel, dim3(batch), dim3(WAVE * DECIDE_WAVES), 0, st, target, draft, draft_tokens,
+                       gamma, vocab,
                        temperature, u, nc, stats, norms, state, accepted, next_token, n_uniforms);
     if ((rc = check_launch("dkv_accept(decide)"))) return rc;
     if (temperature <= 0.0f) return DKV_OK;

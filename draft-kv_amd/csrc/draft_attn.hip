@@ -649,9 +649,11 @@ __global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m
 // too, so the count covers both.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-// 16 bytes per lane from base + voff to LDS byte address lds + 16 * lane
+// 16 bytes per lane from base + voff to LDS byte address lds + 16 * lane,
+// non-temporal: the pages are read once per call, so they should not push
+// other data out of the caches (measured 3% faster than the default policy)
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop

@@ -792,18 +792,23 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
             sm.off[b][i] = off;
         }
     };
-    const int step = gridDim.x;
-    int page = blockIdx.x;
-    if (page * PAGE >= kept) return;
+    // each block takes a contiguous run of the segment's pages, so a source
+    // block shared by two pages is read twice in a row by one block (the
+    // second time from its XCD's L2)
+    const int npg = (kept + PAGE - 1) / PAGE;
+    const int per = (npg + (int)gridDim.x - 1) / (int)gridDim.x;
+    int page = blockIdx.x * per;
+    const int pend = min(npg, page + per);
+    if (page >= pend) return;
     RawPage<BF> raw;
     lookup(page, 0);
     __syncthreads();
     load_raw<BF>(raw, f, h, D, min(PAGE, kept - page * PAGE), sm.blk[0], sm.off[0]);
-    for (int it = 0; page * PAGE < kept; page += step, ++it) {
+    for (int it = 0; page < pend; ++page, ++it) {
         const int r0 = page * PAGE;
         const int rows = min(PAGE, kept - r0);
-        const int nxt = page + step;
-        const bool more = nxt * PAGE < kept;
+        const int nxt = page + 1;
+        const bool more = nxt < pend;
         uint8_t* pg = page_ptr(m, s, L, h, page);
         __syncthreads();   // the previous page's quantize and packing are done with LDS
         stage_raw<BF>(raw, sm, D, rows);
@@ -997,17 +1002,22 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
         for (int x = 0; x < 16; ++x) sm.x[1][vi][vd + 8 * x] = vi < rows ? rv[x] : uint16_t(0);
     };
 
-    const int step = gridDim.x;
-    int page = blockIdx.x;
-    if (page * PAGE >= kept) return;
+    // each block takes a contiguous run of the segment's pages: a 16-token
+    // source block that straddles two pages is then read by one block twice in
+    // a row (the second time from its XCD's L2) instead of by two blocks
+    const int npg = (kept + PAGE - 1) / PAGE;
+    const int per = (npg + (int)gridDim.x - 1) / (int)gridDim.x;
+    int page = blockIdx.x * per;
+    const int pend = min(npg, page + per);
+    if (page >= pend) return;
     lookup(page, 0);
     __syncthreads();
     load(0, min(PAGE, kept - page * PAGE));
-    for (int it = 0; page * PAGE < kept; page += step, ++it) {
+    for (int it = 0; page < pend; ++page, ++it) {
         const int r0 = page * PAGE;
         const int rows = min(PAGE, kept - r0);
-        const int nxt = page + step;
-        const bool more = nxt * PAGE < kept;
+        const int nxt = page + 1;
+        const bool more = nxt < pend;
         uint8_t* pg = page_ptr(m, s, L, h, page);
         __syncthreads();   // the previous page's quantize and packing are done with LDS
         stage(rows);
