@@ -52,7 +52,7 @@ class FullKVCache(PagedKVCache):
 
     def __init__(self, n_layers: int, n_heads: Optional[int] = None, d_head: Optional[int] = None, *,
                  dtype=np.float32, batch: int = 1, max_tokens: int = 1 << 20, device=None,
-                 block_size: int = 16, chunk_keys: int = 2048) -> None:
+                 block_size: int = 16, chunk_keys: Optional[int] = None) -> None:
         self._lazy = dict(n_layers=n_layers, dtype=dtype, batch=batch, max_tokens=max_tokens, device=device,
                           block_size=block_size, chunk_keys=chunk_keys)
         self.n_layers = n_layers

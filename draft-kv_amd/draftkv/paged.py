@@ -18,6 +18,7 @@ them.
 
 from __future__ import annotations
 
+import math
 from typing import Optional, Sequence
 
 import numpy as np
@@ -87,6 +88,17 @@ def _torch_dtype(dtype) -> torch.dtype:
     raise ValueError(f"unsupported cache dtype {dtype!r} (float32 or bfloat16)")
 
 
+def auto_chunk_keys(batch: int, n_heads: int, max_tokens: int) -> int:
+    """Keys per work unit of the verify/decode attention kernel: about 1024
+    units (four per CU) over the cache's capacity, a power of two in
+    [2048, 8192]. Measured on one MI355X (bf16, head_dim 128): at batch 32,
+    ctx 32k, 8192-key units are 2.5-4% faster than 2048; at batch 1, ctx 262k,
+    2048 is best. Verify and decode use the cache's one value, so their rows
+    stay bit-identical whatever it is."""
+    units = max(1.0, batch * n_heads * max_tokens / 1024.0)
+    return int(min(8192, max(2048, 1 << int(round(math.log2(units))))))
+
+
 def default_device() -> torch.device:
     if not torch.cuda.is_available():
         raise RuntimeError("draftkv needs a ROCm GPU (torch.cuda.is_available() is False)")
@@ -99,18 +111,19 @@ class PagedKVCache:
     ``PagedKVCache(n_layers, n_heads, d_head, block_size=16, n_blocks=512,
     dtype=np.float32)`` is the reference signature (n_heads = KV heads);
     ``batch``, ``max_tokens``, ``device`` and ``chunk_keys`` (the fixed key
-    chunk of the attention kernel) are additions.
+    chunk of the attention kernel; by default ``auto_chunk_keys``) are
+    additions.
     """
 
     def __init__(self, n_layers: int, n_heads: int, d_head: int, block_size: int = 16,
                  n_blocks: int = 512, dtype=np.float32, *, batch: int = 1,
-                 max_tokens: Optional[int] = None, device=None, chunk_keys: int = 2048) -> None:
+                 max_tokens: Optional[int] = None, device=None, chunk_keys: Optional[int] = None) -> None:
         self.n_layers, self.n_heads, self.d_head = n_layers, n_heads, d_head
         self.block_size, self.n_blocks, self.batch = block_size, n_blocks, batch
         self.dtype = _torch_dtype(dtype)
         self.device = torch.device(device) if device is not None else default_device()
-        self.chunk_keys = chunk_keys
         self.max_tokens = max_tokens if max_tokens is not None else n_blocks * block_size
+        self.chunk_keys = chunk_keys if chunk_keys is not None else auto_chunk_keys(batch, n_heads, self.max_tokens)
         self.max_blocks = -(-self.max_tokens // block_size)
         self.pools = [BlockPool(n_blocks, block_size) for _ in range(batch)]
         per_block = 2 * n_heads * block_size * d_head
