@@ -240,12 +240,21 @@ class Decoder:
         cache.reserve(ct)
         start_d = ops.to_device(st.astype(np.int32), self.device)
         count_d = None if np.all(ct == T) else ops.to_device(ct.astype(np.int32), self.device)
+        attn = self.paged_attn(cache, start_d, count_d, max_pos)
+        attn.finish = lambda: cache.commit(ct)
+        return attn
 
+    @staticmethod
+    def paged_attn(cache: PagedKVCache, start_d, count_d, max_len: int):
+        """attn(L, q, k, v) of a forward over the full cache, device tensors
+        only: append the rows to layer L at start_d (count_d rows, or all),
+        then attend the queries over keys 0 .. start + t. max_len bounds the
+        key count of every sequence (it sizes the launch, not the arithmetic)."""
         def attn(L, q, k, v):
             cache.append_layer(L, k, v, start_d, count_d)
-            return cache.attend(L, q, start_d, max_pos, count=count_d)
+            return cache.attend(L, q, start_d, max_len, count=count_d)
 
-        attn.finish = lambda: cache.commit(ct)
+        attn.finish = lambda: None
         return attn
 
     def _mirror_attention(self, cache: CompressedKVCache, b, T, st, ct):

@@ -32,7 +32,8 @@ import torch
 
 from . import ops
 from .compress import CompressedKVCache
-from .graphs import DraftStepGraph, graph_key
+from .paged import PagedKVCache
+from .graphs import DraftStepGraph, FullStepGraph, full_graph_key, graph_key
 from .config import CompressionConfig
 from .controller import Controller, FixedPolicy
 
@@ -301,6 +302,46 @@ class DecodeBatch:
         self._graphs[key] = g
         return g
 
+    # ------------------------------------------------------------ gamma-0 step graphs
+    def _full_key(self):
+        """The key of the gamma-0 step graph for the current full cache, or
+        None where none applies (a cache without device block tables)."""
+        full, model = self.full, self.model
+        if not isinstance(full, PagedKVCache) or not getattr(full, "_ready", True):
+            return None
+        if model.rope_theta is not None:
+            model._cos_sin(min(self.cap_tokens, full.max_tokens))   # never regrown under the graph
+        return full_graph_key(model, full, self.b, self.T, min(self.cap_tokens, full.max_tokens))
+
+    def _full_graph(self, n, act):
+        """The recorded gamma-0 step, or None: the round then runs eagerly and
+        records one after (its first run warms every kernel and GEMM shape)."""
+        model = self.model
+        last = np.where(act > 0, n - 1, 0)
+        if model.pos_table is not None and int(last.max()) >= model.pos_table.shape[0]:
+            raise IndexError(f"position {int(last.max())} beyond the position table ({model.pos_table.shape[0]})")
+        key = self._full_key()
+        return None if key is None else self._graphs.get(key)
+
+    def _record_full_graph(self) -> None:
+        key = self._full_key()
+        if key is None or key in self._graphs:
+            return
+        try:
+            if self._pool is None:
+                self._pool = torch.cuda.graph_pool_handle()
+            g = FullStepGraph(self.model, self.full, self.b, self.T, min(self.cap_tokens, self.full.max_tokens),
+                              self._pool)
+        except Exception as e:            # keep decoding eagerly
+            warnings.warn(f"gamma-0 step graph recording failed ({e}); decoding eagerly")
+            self.use_graphs = False
+            return
+        if g.key != key:
+            raise RuntimeError("the full cache moved while a gamma-0 step graph was recorded")
+        while len(self._graphs) >= 4:
+            self._graphs.pop(next(iter(self._graphs)))
+        self._graphs[key] = g
+
     def _pending_dev(self) -> torch.Tensor:
         """The last token of every sequence as a device int32 [b]."""
         if self._dev_pending is not None:
@@ -355,11 +396,21 @@ class DecodeBatch:
         ph, ev = self.phases, {}
         if gamma <= 0:
             u = np.array([eng._g(s).random() if active[s] else 0.5 for s in range(b)])
-            u_d = ops.to_device(u, dev)
             if ph is not None:
                 ev["d1"] = ph.event()
-            logits = model.forward_batch(self._pending_dev()[:, None], full, n - 1, act)[:, 0]
-            tok = ops.sample(logits, T, u_d)
+            graph = None
+            if self.use_graphs:
+                full.reserve(act)         # first: the pool may grow (and move) to take the rows
+                graph = self._full_graph(n, act)
+            if graph is not None:
+                tok = graph.run(self._pending_dev(), n - 1, act, u)
+                full.commit(act)
+            else:
+                u_d = ops.to_device(u, dev)
+                logits = model.forward_batch(self._pending_dev()[:, None], full, n - 1, act)[:, 0]
+                tok = ops.sample(logits, T, u_d)
+                if self.use_graphs:
+                    self._record_full_graph()
             if ph is not None:
                 ev["v1"] = ph.event()
             # no wait: the next round reads tok on the device; the host copy

@@ -18,6 +18,16 @@ move it) and ships them in one copy; each replay is preceded by a
 device-to-device copy of its row. The graph holds raw pointers to the
 mirror's buffers, the RoPE table and its own scratch (a private workspace),
 so it is keyed on them and recorded again when any of them changes.
+
+``FullStepGraph`` does the same for a round that declines to draft (gamma
+0: engine.py:147-153 of the reference, one forward of the pending token
+against the full cache, then a sample). It reads the start positions, row
+counts and uniforms from its own fixed buffer; the full cache's block tables
+are a device tensor that never moves (new blocks are written into it by
+``reserve`` before the replay), and its attention is recorded for every key
+up to the batch's position bound (the launch grows with that bound, the
+arithmetic of each sequence does not: chunks past a sequence's end are
+skipped, and the merge covers its own chunks only).
 """
 
 from __future__ import annotations
@@ -111,3 +121,67 @@ class DraftStepGraph:
                 draft_logits[:, col0 + i].copy_(self.logits)
             draft_tok[:, col0 + i].copy_(self.tok)
         return self.tok
+
+
+def full_graph_key(model, full, b: int, temperature: float, max_len: int) -> tuple:
+    cs = getattr(model, "_cs", None)
+    return (b, float(temperature), full.store.data_ptr(), full.d_tables.data_ptr(), int(max_len),
+            full.chunk_keys, None if cs is None else (cs.data_ptr(), model._cs_len))
+
+
+class FullStepGraph:
+    """One recorded gamma-0 step (a plain forward of the pending token over the
+    full cache and its sample) for a fixed (model, full cache, batch,
+    temperature); see the module docstring."""
+
+    def __init__(self, model, full, b: int, temperature: float, max_len: int, pool) -> None:
+        """max_len: a bound on every sequence's key count (its last position + 1)
+        over the graph's life; the RoPE table is grown to it first."""
+        if model.device.type != "cuda":
+            raise RuntimeError("full-step graphs need a ROCm device")
+        dev = model.device
+        self.model, self.full, self.b, self.T = model, full, b, float(temperature)
+        self.max_len = max_len = int(min(max_len, full.max_tokens))
+        cs, cs_len = (None, 0)
+        if model.rope_theta is not None:
+            cs, cs_len = model._cos_sin(max_len)
+        self.key = full_graph_key(model, full, b, temperature, max_len)
+        # [u as 2b words | start b | count b]
+        self.n_words = 4 * b
+        self.inp = torch.zeros(self.n_words, dtype=torch.int32, device=dev)
+        self.u = self.inp[: 2 * b].view(torch.float64)
+        self.start = self.inp[2 * b: 3 * b]
+        self.count = self.inp[3 * b:]
+        self.tok = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.ws = ops.Workspace()
+        self._host = torch.empty(self.n_words, dtype=torch.int32, pin_memory=True)
+        self._copied: Optional[torch.cuda.Event] = None
+        self.replays = 0
+        attn = model.paged_attn(full, self.start, self.count, max_len)
+        self.graph = torch.cuda.CUDAGraph()
+        with ops.private_workspace(self.ws):
+            with torch.cuda.graph(self.graph, pool=pool):
+                lg = model._core(self.tok, self.start, b, 1, attn, cs, cs_len)[:, 0]
+                ops.sample(lg, self.T, self.u, out=self.tok)
+        self.logits = lg
+
+    def run(self, x0: torch.Tensor, start: np.ndarray, act: np.ndarray, u: np.ndarray) -> torch.Tensor:
+        """One step from token x0 (int32 [b], device): sequence s appends its
+        row at start[s] when act[s] (rows of inactive sequences are neither
+        written nor read), samples with uniform u[s]. The caller reserves the
+        cache's blocks before and commits the rows after. Returns the sampled
+        tokens (a new device tensor)."""
+        b = self.b
+        if self._copied is not None:
+            self._copied.synchronize()            # the pinned row is free again
+        row = self._host.numpy()
+        row[: 2 * b] = np.ascontiguousarray(u, np.float64).view(np.int32)
+        row[2 * b: 3 * b] = np.where(act > 0, start, 0)
+        row[3 * b:] = act
+        self.inp.copy_(self._host, non_blocking=True)
+        self._copied = torch.cuda.Event()
+        self._copied.record()
+        self.tok.copy_(x0)
+        self.graph.replay()
+        self.replays += 1
+        return self.tok.clone()

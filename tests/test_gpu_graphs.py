@@ -117,3 +117,58 @@ def test_graph_is_rerecorded_when_the_rope_table_grows(dev):
         if rg is not None:
             np.testing.assert_array_equal(rg[0], re_[0])
     assert len(bg._graphs) >= 2 and sum(g.replays for g in bg._graphs.values()) > 0
+
+
+class Pattern:
+    """One arm, gamma from a repeating pattern (0 = a plain full-KV step)."""
+
+    def __init__(self, arm, gammas):
+        self.arm, self.gammas, self.n = arm, list(gammas), 0
+
+    def select(self, ctx, key=None):
+        g = self.gammas[self.n % len(self.gammas)]
+        self.n += 1
+        return self.arm, g
+
+    def update(self, cfg, gamma, accepted, ctx, key=None):
+        pass
+
+
+def _decode_pattern(m, prompts, max_new, T, arm, gammas, graphs):
+    from draftkv import DraftKVEngine
+    from draftkv.engine import DecodeBatch
+    eng = DraftKVEngine(m, Pattern(arm, gammas), seed=4)
+    eng.draft_graphs = graphs
+    toks = eng._check_prompts(prompts, m.vocab_size)
+    full = eng._new_full(len(toks), max(len(t) for t in toks) + max_new + 16)
+    eng._prefill(toks, full)
+    batch = DecodeBatch(eng, toks, full, max_new, T)
+    while batch.step():
+        pass
+    return batch.results(), batch
+
+
+@pytest.mark.parametrize("name,T", [("llama", 0.0), ("llama_bf16", 0.8), ("gpt2", 0.0), ("tiny", 0.9)])
+def test_gamma0_graph_replays_equal_eager_rounds(dev, name, T):
+    """Rounds that decline to draft (gamma 0) replayed from a recorded full-KV
+    step graph: the tokens, accepted runs and mirror rows equal an eager
+    decode's, over a ragged batch whose sequences finish in different rounds
+    (inactive rows in the replayed step) with drafted rounds in between."""
+    from draftkv import CompressionConfig
+    from draftkv.graphs import FullStepGraph
+    m = _model(name)
+    rng = np.random.default_rng(12)
+    prompts = [[int(x) for x in rng.integers(0, m.vocab_size, n)] for n in (60, 33, 81)]
+    arm = CompressionConfig(4, 0.5, group=32, scale_fp16=True)
+    gammas = [0, 0, 3, 0, 0, 0, 2]
+    budgets = 37
+    res_g, bg = _decode_pattern(m, prompts, budgets, T, arm, gammas, graphs=True)
+    res_e, be = _decode_pattern(m, prompts, budgets, T, arm, gammas, graphs=False)
+    full_graphs = [g for g in bg._graphs.values() if isinstance(g, FullStepGraph)]
+    assert full_graphs and sum(g.replays for g in full_graphs) >= 10, "the gamma-0 graph did not run"
+    for a, b in zip(res_g, res_e):
+        assert a.tokens == b.tokens
+        assert [x.accepted for x in a.rounds] == [x.accepted for x in b.rounds]
+        assert [x.gamma for x in a.rounds] == [x.gamma for x in b.rounds]
+    np.testing.assert_array_equal(bg.comp.rows(), be.comp.rows())
+    np.testing.assert_array_equal(bg.full.lengths(), be.full.lengths())
