@@ -460,6 +460,13 @@ static GemmPlan gemm_plan(int M, int N, int K) {
 
 using namespace dkv;
 
+extern "C" int32_t dkv_gemm_bf16_partials(int32_t M, int32_t N, int32_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int S = gemm_chunks(N, K);
+    const GemmPlan p = gemm_plan(M, N, K);
+    return !p.small && p.c_per == 1 && S > 1 ? S : 0;
+}
+
 extern "C" size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const int S = gemm_chunks(N, K);
@@ -500,8 +507,11 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
     DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
     DKV_REQUIRE(x_dtype == DKV_BF16 || x_dtype == DKV_F32, "dkv_gemm_bf16: x must be bf16 or float32");
-    DKV_REQUIRE((flags & ~DKV_GEMM_SWIGLU) == 0, "dkv_gemm_bf16: unknown flags");
+    DKV_REQUIRE((flags & ~(DKV_GEMM_SWIGLU | DKV_GEMM_DEFER)) == 0, "dkv_gemm_bf16: unknown flags");
     const int swiglu = (flags & DKV_GEMM_SWIGLU) != 0;
+    const int defer = (flags & DKV_GEMM_DEFER) != 0;
+    DKV_REQUIRE(!defer || (!swiglu && !bias && y_dtype == DKV_BF16),
+                "dkv_gemm_bf16: deferred partials are for a bf16 y without bias or SwiGLU");
     DKV_REQUIRE(!swiglu || (y_dtype == DKV_BF16 && !bias),
                 "dkv_gemm_bf16: the SwiGLU epilogue writes bf16 and takes no bias");
     DKV_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
@@ -542,7 +552,7 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     else if (p.mb == 2) launch_gemm<1, 2>(a, grid, st);
     else launch_gemm<1, 4>(a, grid, st);
     int rc = check_launch("dkv_gemm_bf16");
-    if (rc || !need) return rc;
+    if (rc || !need || defer) return rc;   // deferred: the consumer sums the partials
     const int64_t MN = (int64_t)M * N;   // a multiple of 16
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, a.part, MN, S, N,
                        a.bias, y, a.y_f32, a.swiglu);

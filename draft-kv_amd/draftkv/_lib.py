@@ -14,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "libdraftkv_hip.so")
 
 DKV_F32, DKV_BF16 = 0, 1
+DKV_GEMM_SWIGLU, DKV_GEMM_DEFER = 1, 2
 _ERRORS = {-1: ValueError, -2: RuntimeError, -3: MemoryError, -4: MemoryError}
 
 
@@ -65,12 +66,15 @@ _SIGS = {
     "dkv_add_rmsnorm": (C.c_int, [P, P, I32, P, I32, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_add_layernorm": (C.c_int, [P, P, I32, P, I32, P, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_qkv_split": (C.c_int, [P, I32, P, I32, I32, I32, I32, I32, P, P, I32, P, P, P, P]),
+    "dkv_add_norm_partials": (C.c_int, [P, P, I32, P, I32, P, P, I32, I32, I32, I32, F32, P, I32, P]),
+    "dkv_qkv_split_partials": (C.c_int, [P, I32, P, I32, I32, I32, I32, I32, P, P, I32, P, P, P, P]),
     "dkv_silu_mul": (C.c_int, [P, I32, I32, I32, P, I32, P]),
     "dkv_bias_gelu": (C.c_int, [P, I32, P, I32, I32, I32, P, I32, P]),
     "dkv_relu": (C.c_int, [P, I32, I32, I32, P, I32, P]),
     "dkv_add": (C.c_int, [P, P, I32, P, I32, I32, I32, P]),
     "dkv_gemm_f32": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P]),
     "dkv_gemm_bf16_workspace": (SZ, [I32, I32, I32]),
+    "dkv_gemm_bf16_partials": (I32, [I32, I32, I32]),
     "dkv_gemm_bf16": (C.c_int, [P, I32, P, P, I32, I32, I32, P, I32, I32, P, SZ, P]),
     "dkv_last_error": (C.c_char_p, []),
     "dkv_version": (I32, []),

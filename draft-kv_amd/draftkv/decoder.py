@@ -112,18 +112,21 @@ class Decoder:
             return ops.rmsnorm(h, w, self.eps, self.act_dtype)
         return ops.layernorm(h, w, b, self.eps, self.act_dtype)
 
-    def _proj(self, x: torch.Tensor, w: torch.Tensor, bias=None) -> torch.Tensor:
-        """x @ W (+ bias); float32 out for float32 models, bf16 out for bf16 models."""
+    def _proj(self, x: torch.Tensor, w: torch.Tensor, bias=None, defer: bool = False):
+        """x @ W (+ bias); float32 out for float32 models, bf16 out for bf16 models
+        (with ``defer``, possibly the bf16 GEMM's partials for a consumer that takes them)."""
         if self.wdtype == torch.float32:
             return ops.gemm_f32(x, w, self.layout, bias)
-        return self._linear(x, w, bias)
+        return self._linear(x, w, bias, defer=defer)
 
     @staticmethod
-    def _linear(x: torch.Tensor, w: torch.Tensor, bias=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+    def _linear(x: torch.Tensor, w: torch.Tensor, bias=None, out_dtype=torch.bfloat16, defer: bool = False):
         """bf16 x @ W^T (+ b) (W as [N, K]): the library's batch-invariant
-        GEMM when it takes the shapes, else torch's."""
+        GEMM when it takes the shapes, else torch's. ``defer``: the caller
+        takes ``ops.Partials`` (qkv_split, add_norm), so the GEMM may leave
+        its per-chunk partials to it instead of reducing them itself."""
         if ops.gemm_bf16_ok(x, w, bias):
-            return ops.gemm_bf16(x, w, bias, out_dtype)
+            return ops.gemm_bf16(x, w, bias, out_dtype, defer=defer)
         y = F.linear(x.to(w.dtype), w, bias)
         return y if out_dtype == torch.bfloat16 else y.to(out_dtype)
 
@@ -133,7 +136,8 @@ class Decoder:
         if self.wdtype == torch.float32:
             ops.gemm_f32(x, w, self.layout, bias, out=h, accumulate=True)
             return self._norm(h, nw, nb)
-        return ops.add_norm(h, self._linear(x, w), bias, nw, nb, self.eps, self.norm == "layer", self.act_dtype)
+        return ops.add_norm(h, self._linear(x, w, defer=True), bias, nw, nb, self.eps, self.norm == "layer",
+                            self.act_dtype)
 
     def _interleave_gate_up(self) -> None:
         """bf16 SwiGLU models: reorder each fused [gate; up] weight to rows
@@ -212,7 +216,7 @@ class Decoder:
         nL = len(self.layers)
         x = self._norm(h, self.layers[0].n1w, self.layers[0].n1b)
         for L, p in enumerate(self.layers):
-            q, k, v = ops.qkv_split(self._proj(x, p.wqkv), p.bqkv, Hq, Hkv, D, positions, cs, cs_len)
+            q, k, v = ops.qkv_split(self._proj(x, p.wqkv, defer=True), p.bqkv, Hq, Hkv, D, positions, cs, cs_len)
             a = attn(L, q.view(b, T, Hq, D), k.view(b, T, Hkv, D), v.view(b, T, Hkv, D)).view(R, Hq * D)
             # float32 attention output: a bf16 model's o-proj GEMM rounds it to
             # bf16 as it reads it (the same bits as converting it first)

@@ -12,7 +12,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import DKV_BF16, DKV_F32, Drafter, Paged, QCfg, check, lib
+from ._lib import DKV_BF16, DKV_F32, DKV_GEMM_DEFER, Drafter, Paged, QCfg, check, lib
 
 
 _get_device = getattr(torch._C, "_cuda_getDevice", None)
@@ -352,10 +352,20 @@ def add_norm(h: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor], w: 
              b: Optional[torch.Tensor], eps: float, layer_norm: bool, out_dtype=torch.float32) -> torch.Tensor:
     """h += x (+ bias) in place, then return RMSNorm(h) (or LayerNorm when ``layer_norm``)."""
     _need(h, "h", torch.float32, 2)
+    rows, d = h.shape
+    if isinstance(x, Partials):
+        if x.shape != (rows, d):
+            raise ValueError("add_norm: shapes differ")
+        out = torch.empty((rows, d), dtype=out_dtype, device=h.device)
+        bp, bd = _bias(bias)
+        check(lib().dkv_add_norm_partials(h.data_ptr(), x.data_ptr(), x.n_part, bp, bd, w.data_ptr(),
+                                          _ptr(b) if layer_norm else None, _dt(w), 1 if layer_norm else 0, rows, d,
+                                          float(eps), out.data_ptr(), _odt(out_dtype), _stream()),
+              "dkv_add_norm_partials")
+        return out
     _need(x, "x")
     if x.numel() != h.numel():
         raise ValueError("add_norm: shapes differ")
-    rows, d = h.shape
     out = torch.empty((rows, d), dtype=out_dtype, device=h.device)
     bp, bd = _bias(bias)
     if layer_norm:
@@ -375,8 +385,11 @@ def _bias(b: Optional[torch.Tensor]):
 def qkv_split(qkv: torch.Tensor, bias: Optional[torch.Tensor], n_q_heads: int, n_kv_heads: int, d: int,
               positions: Optional[torch.Tensor] = None, cos_sin: Optional[torch.Tensor] = None, max_pos: int = 0):
     """Fused projection rows [q | k | v] (+ bias) -> float32 q [rows, Hq, d], k, v [rows, Hkv, d];
-    RoPE on q and k when ``cos_sin`` (cos table then sin table, [2, max_pos, d/2]) is given."""
-    _need(qkv, "qkv", ndim=2)
+    RoPE on q and k when ``cos_sin`` (cos table then sin table, [2, max_pos, d/2]) is given.
+    ``qkv`` may be a bf16 GEMM's ``Partials``."""
+    part = isinstance(qkv, Partials)
+    if not part:
+        _need(qkv, "qkv", ndim=2)
     rows = qkv.shape[0]
     if qkv.shape[1] != (n_q_heads + 2 * n_kv_heads) * d:
         raise ValueError(f"qkv width {qkv.shape[1]} != (Hq + 2 Hkv) * d")
@@ -385,6 +398,11 @@ def qkv_split(qkv: torch.Tensor, bias: Optional[torch.Tensor], n_q_heads: int, n
     k = torch.empty((rows, n_kv_heads, d), dtype=torch.float32, device=dev)
     v = torch.empty((rows, n_kv_heads, d), dtype=torch.float32, device=dev)
     bp, bd = _bias(bias)
+    if part:
+        check(lib().dkv_qkv_split_partials(qkv.data_ptr(), qkv.n_part, bp, bd, rows, n_q_heads, n_kv_heads, d,
+                                           _ptr(positions), _ptr(cos_sin), max_pos, q.data_ptr(), k.data_ptr(),
+                                           v.data_ptr(), _stream()), "dkv_qkv_split_partials")
+        return q, k, v
     check(lib().dkv_qkv_split(qkv.data_ptr(), _dt(qkv), bp, bd, rows, n_q_heads, n_kv_heads, d, _ptr(positions),
                               _ptr(cos_sin), max_pos, q.data_ptr(), k.data_ptr(), v.data_ptr(), _stream()),
           "dkv_qkv_split")
@@ -465,12 +483,37 @@ def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] 
     return ok
 
 
+class Partials:
+    """A bf16 GEMM's per-chunk float32 partials [S, M, N] left for its
+    consumer (``add_norm``, ``qkv_split``), which sums them in chunk order and
+    rounds to bf16: the values the GEMM would have stored. The buffer is the
+    op workspace, valid until the next op that takes workspace."""
+
+    __slots__ = ("part", "n_part", "shape")
+
+    def __init__(self, part: torch.Tensor, n_part: int, shape: tuple) -> None:
+        self.part, self.n_part, self.shape = part, n_part, shape
+
+    @property
+    def device(self):
+        return self.part.device
+
+    def numel(self) -> int:
+        return self.shape[0] * self.shape[1]
+
+    def data_ptr(self) -> int:
+        return self.part.data_ptr()
+
+
 def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
-              out_dtype=torch.bfloat16, swiglu: bool = False) -> torch.Tensor:
+              out_dtype=torch.bfloat16, swiglu: bool = False, defer: bool = False):
     """x [M, K] @ w[N, K]^T (+ bias), bf16 in (a float32 x is rounded to bf16
     as it is read), float32 accumulation, bf16 (or float32) out; a row's
     result is the same for any M. swiglu: w's rows interleave (gate_i, up_i)
-    and the result is silu(gate) * up, bf16 [M, N / 2] (no bias)."""
+    and the result is silu(gate) * up, bf16 [M, N / 2] (no bias). defer (bf16
+    out, no bias or SwiGLU): when the launch plan makes per-chunk partials,
+    return them as ``Partials`` for a consumer that sums them (one launch
+    fewer); else the tensor as usual."""
     if not gemm_bf16_ok(x, w, bias):
         raise ValueError(f"gemm_bf16: unsupported operands x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}"
                          + ("" if bias is None else f", bias {tuple(bias.shape)} {bias.dtype}"))
@@ -478,9 +521,16 @@ def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = N
     N = w.shape[0]
     if swiglu and (bias is not None or out_dtype != torch.bfloat16):
         raise ValueError("gemm_bf16: the SwiGLU epilogue writes bf16 and takes no bias")
-    out = torch.empty((M, N // 2 if swiglu else N), dtype=out_dtype, device=x.device)
+    defer = defer and not swiglu and bias is None and out_dtype == torch.bfloat16 and M > 0
+    S = lib().dkv_gemm_bf16_partials(M, N, K) if defer else 0
     nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)
     ws = _WS.get(x.device, nbytes) if nbytes else None
+    if S > 0:
+        check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), None, M, N, K, ws.data_ptr(),
+                                  _odt(out_dtype), DKV_GEMM_DEFER, ws.data_ptr(), ws.numel(), _stream()),
+              "dkv_gemm_bf16")
+        return Partials(ws, S, (M, N))
+    out = torch.empty((M, N // 2 if swiglu else N), dtype=out_dtype, device=x.device)
     check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
                               _odt(out_dtype), 1 if swiglu else 0,
                               _ptr(ws), 0 if ws is None else ws.numel(), _stream()), "dkv_gemm_bf16")

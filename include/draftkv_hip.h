@@ -255,6 +255,13 @@ int dkv_add_rmsnorm(float* h, const void* x, int32_t x_dtype, const void* bias, 
 int dkv_add_layernorm(float* h, const void* x, int32_t x_dtype, const void* bias, int32_t bias_dtype, const void* w,
                       const void* b, int32_t w_dtype, int32_t rows, int32_t d, float eps, void* out,
                       int32_t out_dtype, dkv_stream_t stream);
+/* dkv_add_rmsnorm / dkv_add_layernorm (layer_norm != 0) with x the bf16 GEMM's deferred
+ * partials part [n_part][rows][d] (DKV_GEMM_DEFER): x[r][i] = bf16(sum over chunks, in chunk
+ * order), the value dkv_gemm_bf16 would have stored, so the result is bit for bit that of the
+ * GEMM followed by the add-norm; the GEMM's reduce launch is saved  -- the same reference lines */
+int dkv_add_norm_partials(float* h, const float* part, int32_t n_part, const void* bias, int32_t bias_dtype,
+                          const void* w, const void* b, int32_t w_dtype, int32_t layer_norm, int32_t rows, int32_t d,
+                          float eps, void* out, int32_t out_dtype, dkv_stream_t stream);
 /* Split fused projection rows [q heads | k heads | v heads] (+ bias) into f32 q [rows][Hq][d],
  * k and v [rows][Hkv][d]; with cos_sin (cos table [max_pos][d/2] then sin table) apply
  * rotate-half RoPE to q and k at positions[r]  -- model.py:118-120, gpt2.py:193-196,
@@ -262,6 +269,12 @@ int dkv_add_layernorm(float* h, const void* x, int32_t x_dtype, const void* bias
 int dkv_qkv_split(const void* qkv, int32_t qkv_dtype, const void* bias, int32_t bias_dtype, int32_t rows,
                   int32_t n_q_heads, int32_t n_kv_heads, int32_t d, const int32_t* positions,
                   const float* cos_sin, int32_t max_pos, float* q, float* k, float* v, dkv_stream_t stream);
+/* dkv_qkv_split with the projection rows as the bf16 GEMM's deferred partials
+ * part [n_part][rows][(Hq + 2 Hkv) d] (DKV_GEMM_DEFER), summed and rounded as
+ * dkv_add_norm_partials does  -- the same reference lines */
+int dkv_qkv_split_partials(const float* part, int32_t n_part, const void* bias, int32_t bias_dtype, int32_t rows,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t d, const int32_t* positions,
+                           const float* cos_sin, int32_t max_pos, float* q, float* k, float* v, dkv_stream_t stream);
 /* out = silu(gate) * up with gate_up = [rows][2*ff]  -- llama.py:102-103,222 */
 int dkv_silu_mul(const void* gate_up, int32_t gate_up_dtype, int32_t rows, int32_t ff, void* out, int32_t out_dtype,
                  dkv_stream_t stream);
@@ -294,7 +307,15 @@ int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, in
 #define DKV_GEMM_SWIGLU 1  /* flags: W's rows interleave (gate_i, up_i); y is bf16 [M][N/2] with
                               y[m][i] = silu(g) * u of the two outputs, each first rounded to bf16
                               (the SwiGLU of llama.py:220-222 fused into the gate/up product; no bias) */
+#define DKV_GEMM_DEFER 2   /* flags: when the launch plan for (M, N, K) makes per-chunk partials
+                              (dkv_gemm_bf16_partials > 0), leave them, float32 [S][M][N], at the
+                              start of work and skip the reduce: y is not written, and the consumer
+                              sums them (dkv_add_norm_partials, dkv_qkv_split_partials); otherwise
+                              y is written as usual. bf16 y only, no bias, no SwiGLU */
 size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K);
+/* the chunk count S of the partials dkv_gemm_bf16 writes for (M, N, K), or 0 when its plan
+ * writes y directly (a function of the launch plan, not of the arithmetic) */
+int32_t dkv_gemm_bf16_partials(int32_t M, int32_t N, int32_t K);
 int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
                   int32_t K, void* y, int32_t y_dtype, int32_t flags, void* work, size_t work_bytes,
                   dkv_stream_t stream);

@@ -193,6 +193,62 @@ def test_gemm_bf16_swiglu_epilogue_equals_unfused(dev, M, ff, K):
         assert got.shape == (M, ff) and torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(32, 4096, 4096), (96, 4096, 14336), (1, 4096, 4096), (288, 4096, 4096),
+                                   (32, 256, 512)])
+@pytest.mark.parametrize("layer_norm", [False, True])
+def test_add_norm_on_deferred_partials_equals_gemm_then_add_norm(dev, M, N, K, layer_norm):
+    """A GEMM that leaves its per-chunk partials (DKV_GEMM_DEFER) to the
+    residual add + norm gives bit for bit the GEMM's bf16 output followed by
+    the add-norm: the same out and the same updated residual, with a bias,
+    float32 and bf16 x; plans without partials return the tensor as usual."""
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K + layer_norm)
+    w = (0.05 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16)
+    nb = (0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16)
+    bias = (0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16)
+    h0 = torch.randn((M, N), generator=g, device=dev)
+    x = torch.randn((M, K), generator=g, device=dev) * 2.0
+    planned = ops.lib().dkv_gemm_bf16_partials(M, N, K)
+    for xx in (x, x.to(torch.bfloat16)):
+        y = ops.gemm_bf16(xx, w)
+        h_ref = h0.clone()
+        ref = ops.add_norm(h_ref, y, bias, nw, nb, 1e-5, layer_norm, torch.bfloat16)
+        p = ops.gemm_bf16(xx, w, defer=True)
+        assert isinstance(p, ops.Partials) == (planned > 0)
+        h_got = h0.clone()
+        got = ops.add_norm(h_got, p, bias, nw, nb, 1e-5, layer_norm, torch.bfloat16)
+        assert torch.equal(got, ref) and torch.equal(h_got, h_ref)
+    if (M, N, K) == (32, 4096, 4096):
+        assert planned > 1, "the Llama-3-8B o projection at M = 32 should run with partials"
+
+
+@pytest.mark.parametrize("M,rope,bias", [(32, True, False), (96, True, True), (3, False, True), (32, False, False)])
+def test_qkv_split_on_deferred_partials_equals_gemm_then_split(dev, M, rope, bias):
+    """qkv_split reading the qkv GEMM's deferred partials equals the split of
+    the GEMM's bf16 output bit for bit (q, k, v; RoPE and a projection bias)."""
+    ops = _ops()
+    Hq, Hkv, D, K = 32, 8, 128, 4096
+    N = (Hq + 2 * Hkv) * D
+    g = torch.Generator(device=dev).manual_seed(M + 31 * rope + bias)
+    w = (0.05 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16) if bias else None
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    pos = torch.randint(0, 4000, (M,), generator=g, device=dev, dtype=torch.int32)
+    cs, n = None, 0
+    if rope:
+        n = 4096
+        inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+        ang = torch.outer(torch.arange(n, dtype=torch.float64), inv)
+        cs = torch.stack([ang.cos(), ang.sin()]).float().to(dev).contiguous()
+    ref = ops.qkv_split(ops.gemm_bf16(x, w), b, Hq, Hkv, D, pos, cs, n)
+    p = ops.gemm_bf16(x, w, defer=True)
+    assert isinstance(p, ops.Partials) == (ops.lib().dkv_gemm_bf16_partials(M, N, K) > 0)
+    got = ops.qkv_split(p, b, Hq, Hkv, D, pos, cs, n)
+    for r, o in zip(ref, got):
+        assert torch.equal(r, o)
+
+
 def test_gemm_bf16_rejects_unsupported_operands(dev):
     ops = _ops()
     x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
