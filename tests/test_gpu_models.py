@@ -180,6 +180,40 @@ def test_batched_generate_equals_one_at_a_time(dev, tiny_setup):
     assert [r.tokens for r in res] == single
 
 
+class _Gamma:
+    """A controller with no stated bound (no gamma / gamma_max attribute): one
+    arm, gamma 20 every round."""
+
+    def __init__(self, arm):
+        self.arm = arm
+
+    def select(self, ctx, key=None):
+        return self.arm, 20
+
+    def update(self, cfg, gamma, accepted, ctx, key=None):
+        pass
+
+
+@pytest.mark.parametrize("bounded", [True, False])
+def test_batched_long_drafts_with_uneven_progress_fit_the_caches(dev, tiny_setup, bounded):
+    """One gamma serves the batch and is capped only by the largest remaining
+    budget, so with gamma 20 a sequence one token short of its budget still
+    verifies 21 rows while another has many left: the caches are sized for
+    that (the controller's bound, or the budget when it states none), and the
+    output equals plain decoding of each prompt."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    m, _, _ = tiny_setup
+    prompts = [_prompt(40 + s, n, m.vocab_size) for s, n in enumerate((57, 23, 90, 41))]
+    cfg = CompressionConfig(4, 0.5)
+    single = [DraftKVEngine(m, seed=0).generate_baseline(p, 26, 0.0) for p in prompts]
+    ctrl = FixedPolicy(cfg, 20) if bounded else _Gamma(cfg)
+    res = DraftKVEngine(m, ctrl, seed=0).generate_batch(prompts, 26, 0.0)
+    assert [r.tokens for r in res] == single
+    # progress was uneven (the sequences accepted different runs), and long drafts ran
+    assert len({tuple(x.accepted for x in r.rounds) for r in res}) > 1
+    assert max(x.gamma for r in res for x in r.rounds) >= 18
+
+
 class _Adaptive:
     """A test-local controller (the select/update protocol): cycles through the
     arms, lengthens the draft after a fully accepted round and shortens it
