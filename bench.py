@@ -6,9 +6,10 @@ Default workload (``--workload e2e``): Llama-3-8B shape (32 layers, d_model
 128256), bf16 random weights N(0, 0.02), batch 32, context 32768 tokens of
 synthetic bf16 KV (N(0,1), 1% outlier channels x8) in 16-token pages with
 shuffled block tables, drafter arms int8 group-64 keep 1.0 and int4 group-32
-(fp16 scale/zero) keep 0.25 switched every 64 rounds (each switch
-requantizes the mirror), gamma chosen each round by the cost model (at most
-16), temperature 0.8 rejection sampling. A step is one decode round over the
+(fp16 scale/zero) keep 0.25 switched every 64 rounds, or half way through
+the timed rounds when fewer than 128 are timed (each switch requantizes the
+mirror), gamma chosen each round by the cost model (at most 20; 0 = a plain
+full-KV step), temperature 0.8 rejection sampling. A step is one decode round over the
 batch: gamma draft forwards against the mirror (replayed from a recorded HIP
 graph per mirror layout; ``--eager`` runs them op by op), one gamma+1-row
 verify forward against the full cache, acceptance, rollback and mirror
@@ -890,8 +891,9 @@ def run_gemm(args):
     SwiGLU epilogue, down 4096x14336), bf16 weights N(0, 0.02), at the row
     counts of a b=32 decode step (M = 32), a gamma-2 verify (96) and a gamma-8
     verify (288), rotating over 8 layers' weights (3.5 GB, so every call
-    streams its weights from HBM). Each call timed with HIP events on the
-    launch stream; algorithmic bytes: the weights once, x once, y once."""
+    streams its weights from HBM), stored tiled as the bf16 models store them
+    (``ops.TiledW``). Each call timed with HIP events on the launch stream;
+    algorithmic bytes: the weights once, x once, y once."""
     import torch
     from draftkv import ops
     dev = torch.device("cuda")
@@ -901,7 +903,7 @@ def run_gemm(args):
     nl = 8
     shapes = {"qkv": (nq, d, torch.bfloat16, False), "o": (d, d, torch.float32, False),
               "gate_up": (2 * ff, d, torch.bfloat16, True), "down": (d, ff, torch.bfloat16, False)}
-    W = {k: [torch.empty((n, kk), dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
+    W = {k: [ops.TiledW(torch.empty((n, kk), dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g))
              for _ in range(nl)] for k, (n, kk, _, _) in shapes.items()}
     res = {}
     for M in (32, 96, 288):

@@ -92,17 +92,39 @@ struct GemmArgs {
     int swiglu;          // rows of W interleave (gate_i, up_i); y[m][i] = silu(gate) * up, bf16, N / 2 columns
 };
 
-// One workgroup: 64*NW rows of W (16*NW per wave) against a tile of 16*MB
-// rows of x, over c_per consecutive K chunks. Per 128-k block the tile's x
+// W stored in tiles (DKV_GEMM_WTILED): 16 rows x 128 k per 4 KB tile, the
+// tiles of a 16-row fragment consecutive along k, and inside a tile the
+// MFMA A-operand order of the block's four 32-k steps: element (row 16 fn + c,
+// k 128 kb + 32 j + 8 q + e) at ((fn * K/128 + kb) * 4 + j) * 512 + (16 q + c) * 8 + e.
+// A wave's load of one step is then 1 KB contiguous (16 B per lane, lane
+// 16 q + c), and a fragment streams as one run; row-major W makes each load
+// 16 rows x 64 B. The arithmetic is the same either way.
+template <bool WT>
+__device__ __forceinline__ const uint16_t* w_lane_base(const uint16_t* w, int64_t frag_row0, int col, int q, int lane,
+                                                       int K) {
+    if constexpr (WT) return w + frag_row0 * K + 8 * lane;
+    else return w + (frag_row0 + col) * K + 8 * q;
+}
+// offset of step j of the block starting at k (elements, from the lane base)
+template <bool WT>
+__device__ __forceinline__ int64_t w_step_off(int k, int j) {
+    if constexpr (WT) return 16 * (int64_t)k + 512 * j;
+    else return k + 32 * j;
+}
+
+// One workgroup: WV waves, 16*NW*WV rows of W (16*NW per wave), against a
+// tile of 16*MB rows of x, over c_per consecutive K chunks. Per 128-k block the tile's x
 // is staged once in LDS (shared by the four waves); each lane streams its W
 // rows straight into registers PD - 1 blocks ahead (PD register sets in
 // rotation). MULTI: the chunks' sums are added in chunk order here (the same
 // additions, in the same order, as the reduce kernel applies to partials).
 // PARTIAL: chunks may end in a block of fewer than four 32-k steps (K not a
 // multiple of 128); otherwise every block is whole.
-template <int NW, int MB, bool MULTI, bool PARTIAL, int PD, bool XF32>
-__global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
+template <int NW, int MB, bool MULTI, bool PARTIAL, int PD, bool XF32, int WV, bool WT>
+__global__ void __launch_bounds__(64 * WV) gemm_bf16_kernel(GemmArgs a) {
     constexpr int TM = 16 * MB;
+    constexpr int NT = 64 * WV;                               // threads
+    constexpr int NXI = (16 * TM + NT - 1) / NT;             // x pieces (8 elements) per thread per block
     __shared__ __align__(16) uint16_t xs[2][TM][GX_ROW];
     // XCD-aware order: workgroup g runs on XCD g % 8; the m tiles of one unit
     // (a W row block and chunk range) take consecutive slots of one XCD, so
@@ -116,21 +138,23 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
     const int col = lane % 16, q = lane / 16;
-    const int n0 = nt * 64 * NW + 16 * NW * wave;
+    const int n0 = nt * 16 * NW * WV + 16 * NW * wave;
     const bool live = n0 < a.N;   // wave-uniform; NW == 2 only where N % 32 == 0
     const int K = a.K, KC = a.KC;
     const int nb = (KC + GKB - 1) / GKB, G = nb * a.c_per;
     const uint16_t* wrow[NW];
 #pragma unroll
-    for (int f = 0; f < NW; ++f) wrow[f] = a.w + (int64_t)(live ? n0 + 16 * f + col : col) * K + 8 * q;
+    for (int f = 0; f < NW; ++f) wrow[f] = w_lane_base<WT>(a.w, live ? n0 + 16 * f : 0, col, q, lane, K);
     // x piece i of this thread: tile row xr_row[i], k offset 8 xr_c[i] in the block. Tile rows past M
     // reread row M-1 (their outputs are dropped), so every load and LDS write is unconditional.
-    int64_t xsrc[MB];   // element offset of the piece's row in x
-    uint32_t xdst[MB];
-    int xc[MB];
+    // (pieces past the tile, when the thread count does not divide it, repeat
+    // the tile's last piece: the same load and the same LDS bytes)
+    int64_t xsrc[NXI];   // element offset of the piece's row in x
+    uint32_t xdst[NXI];
+    int xc[NXI];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int p = tid + 256 * i, r = p / 16;
+    for (int i = 0; i < NXI; ++i) {
+        const int p = min(tid + NT * i, 16 * TM - 1), r = p / 16;
         xc[i] = p % 16;
         xsrc[i] = (int64_t)(m0 + min(r, mrows - 1)) * K;
         xdst[i] = (uint32_t)(r * GX_ROW);
@@ -153,17 +177,17 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
         _Pragma("unroll") for (int f_ = 0; f_ < NW; ++f_) _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_)       \
-            DST[f_][j_] = *reinterpret_cast<const gu32x4_t*>(wrow[f_] + k_ + 32 * (PARTIAL ? min(j_, st_ - 1) : j_)); \
+            DST[f_][j_] = *reinterpret_cast<const gu32x4_t*>(wrow[f_] + w_step_off<WT>(k_, PARTIAL ? min(j_, st_ - 1) : j_)); \
     } while (0)
 #define DKV_LOAD_X(XD, GB)                                                                                      \
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
-        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_) XD[i_] =                                              \
+        _Pragma("unroll") for (int i_ = 0; i_ < NXI; ++i_) XD[i_] =                                             \
             load_x8<XF32>(a.x, xsrc[i_] + k_ + 8 * (PARTIAL ? min(xc[i_], 4 * st_ - 1) : xc[i_]));               \
     } while (0)
 #define DKV_STORE_X(XS, BUF)                                                                                    \
     do {                                                                                                        \
-        _Pragma("unroll") for (int i_ = 0; i_ < MB; ++i_)                                                        \
+        _Pragma("unroll") for (int i_ = 0; i_ < NXI; ++i_)                                                       \
             *reinterpret_cast<gu32x4_t*>(&xs[BUF][0][0] + xdst[i_] + 8 * xc[i_]) = x8_bf16<XF32>(XS[i_]);       \
     } while (0)
 
@@ -177,7 +201,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
     // multiplied. x is fetched as far ahead as W: loads complete in issue order, so waiting for
     // x(gb + 1) also waits for every W load issued before it.
     gu32x4_t wr[PD][NW][4];
-    XRaw<XF32> xr[PD][MB];
+    XRaw<XF32> xr[PD][NXI];
     DKV_LOAD_X(xr[0], 0);
     DKV_STORE_X(xr[0], 0);
 #pragma unroll
@@ -275,7 +299,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs a) {
 // first wave adds them in chunk order (then the bias) and writes y -- the
 // same additions as the other plans, with no partials in HBM and no second
 // kernel. Requires S % CW == 0 and chunks of whole 128-k blocks.
-template <int RW, int CW, int MB, bool XF32>
+template <int RW, int CW, int MB, bool XF32, bool WT>
 __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs a) {
     constexpr int PD = 4;
     extern __shared__ __align__(16) float red[];   // [S][RW][MB][64 lanes][4]
@@ -287,7 +311,7 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
     const bool live = n0 < a.N;   // wave-uniform
     const int K = a.K, KC = a.KC, S = a.S;
     const int nb = KC / GKB, G = nb * (S / CW);
-    const uint16_t* wrow = a.w + (int64_t)(live ? n0 + col : col) * K + 8 * q;
+    const uint16_t* wrow = w_lane_base<WT>(a.w, live ? n0 : 0, col, q, lane, K);
     int64_t xrow[MB];   // element offset of the lane's x row and lane group
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) xrow[mb] = (int64_t)min(16 * mb + col, a.M - 1) * K + 8 * q;
@@ -302,7 +326,7 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
         const int k_ = blk_k(GB);                                                                               \
         _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                                     \
             const int kj = k_ + 32 * j_;                                                                        \
-            WD[j_] = *reinterpret_cast<const gu32x4_t*>(wrow + kj);                                           \
+            WD[j_] = *reinterpret_cast<const gu32x4_t*>(wrow + w_step_off<WT>(k_, j_));                       \
             _Pragma("unroll") for (int m_ = 0; m_ < MB; ++m_) XD[m_][j_] = load_x8<XF32>(a.x, xrow[m_] + kj);  \
         }                                                                                                       \
     } while (0)
@@ -431,6 +455,7 @@ static int gemm_chunks(int N, int K) {
 // wave, x rows per tile, and whether the chunks are split across workgroups.
 struct GemmPlan {
     int nw, mb, m_tiles, n_tiles, c_per;
+    int wv;              // waves per workgroup (4, or 7 where that tiles N into whole rounds of 256 CUs)
     int small, rw, cw;   // gemm_bf16_small_kernel: RW fragments x CW chunk groups per workgroup
 };
 
@@ -438,6 +463,7 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     GemmPlan p;
     const int S = gemm_chunks(N, K);
     p.small = 0;
+    p.wv = 4;
     if (M <= 8 && S >= 4) {   // a few rows and a chunked K: split K inside the workgroup
         p.small = 1, p.nw = 1, p.mb = 1, p.m_tiles = 1, p.c_per = S;
         p.cw = 4, p.rw = 1;
@@ -453,6 +479,15 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     p.n_tiles = (N + 64 * p.nw - 1) / (64 * p.nw);
     // split the chunks over workgroups only when the tiles alone leave most of the chip idle
     p.c_per = (S > 1 && (int64_t)p.n_tiles * p.m_tiles < 128) ? 1 : S;
+    // 7-wave workgroups when they cut W into whole rounds of 256 tiles and 4-wave ones do not
+    // (the Llama-3-8B gate/up weight, 28672 rows: 448 tiles of 64 leave the CUs unevenly loaded,
+    // 256 of 112 give every CU one)
+    const int r7 = 16 * p.nw * 7;
+    if (p.c_per == S && p.mb <= 2 && K % GKB == 0 && N % r7 == 0 && (N / r7 * p.m_tiles) % 256 == 0 &&
+        (p.n_tiles * p.m_tiles) % 256 != 0) {
+        p.wv = 7;
+        p.n_tiles = N / r7;
+    }
     return p;
 }
 
@@ -474,29 +509,49 @@ extern "C" size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K) {
     return !p.small && p.c_per == 1 && S > 1 ? sizeof(float) * (size_t)S * M * N : 0;
 }
 
-template <int RW, int CW, int MB>
+template <int RW, int CW, int MB, bool WT>
 static void launch_small(const GemmArgs& a, int n_wg, hipStream_t st) {
     const size_t lds = sizeof(float) * 4 * WAVE * (size_t)a.S * RW * MB;
-    if (a.x_f32) hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, true>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
-    else hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, false>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
+    if (a.x_f32)
+        hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, true, WT>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
+    else
+        hipLaunchKernelGGL((gemm_bf16_small_kernel<RW, CW, MB, false, WT>), dim3(n_wg), dim3(64 * RW * CW), lds, st, a);
 }
 
-template <int NW, int MB, bool PARTIAL>
+template <int NW, int MB, bool PARTIAL, int WV, bool WT>
 static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr int PD = 3;   // register sets in rotation (4 measured no faster: fewer waves fit)
+    const dim3 blk(64 * WV);
     if (a.x_f32) {
-        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, true>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, true>), grid, dim3(256), 0, st, a);
+        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, true, WV, WT>), grid, blk, 0, st, a);
+        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, true, WV, WT>), grid, blk, 0, st, a);
     } else {
-        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, false>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, false>), grid, dim3(256), 0, st, a);
+        if (a.c_per > 1) hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, true, PARTIAL, PD, false, WV, WT>), grid, blk, 0, st, a);
+        else hipLaunchKernelGGL((gemm_bf16_kernel<NW, MB, false, PARTIAL, PD, false, WV, WT>), grid, blk, 0, st, a);
     }
 }
 
-template <int NW, int MB>
-static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
-    if (a.KC % GKB == 0) launch_gemm<NW, MB, false>(a, grid, st);
-    else launch_gemm<NW, MB, true>(a, grid, st);
+// the plan's kernel; tiled W always comes in whole 128-k blocks
+template <bool WT>
+static void launch_plan(const GemmPlan& p, const GemmArgs& a, dim3 grid, hipStream_t st) {
+    const bool whole = WT || a.KC % GKB == 0;
+    if (p.wv == 7) {   // one fragment per wave, an x tile of 16 or 32 rows, whole 128-k blocks (the plan's test)
+        if (p.mb == 2) launch_gemm<1, 2, false, 7, WT>(a, grid, st);
+        else launch_gemm<1, 1, false, 7, WT>(a, grid, st);
+    } else if (p.nw == 2 && p.mb == 4) {   // K % 128 == 0 with two fragments
+        launch_gemm<2, 4, false, 4, WT>(a, grid, st);
+    } else if (p.nw == 2) {
+        launch_gemm<2, 8, false, 4, WT>(a, grid, st);
+    } else if (p.mb == 1) {
+        if (whole) launch_gemm<1, 1, false, 4, WT>(a, grid, st);
+        else launch_gemm<1, 1, true, 4, false>(a, grid, st);
+    } else if (p.mb == 2) {
+        if (whole) launch_gemm<1, 2, false, 4, WT>(a, grid, st);
+        else launch_gemm<1, 2, true, 4, false>(a, grid, st);
+    } else {
+        if (whole) launch_gemm<1, 4, false, 4, WT>(a, grid, st);
+        else launch_gemm<1, 4, true, 4, false>(a, grid, st);
+    }
 }
 
 extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, const void* bias, int32_t M, int32_t N,
@@ -507,9 +562,11 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
     DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
     DKV_REQUIRE(x_dtype == DKV_BF16 || x_dtype == DKV_F32, "dkv_gemm_bf16: x must be bf16 or float32");
-    DKV_REQUIRE((flags & ~(DKV_GEMM_SWIGLU | DKV_GEMM_DEFER)) == 0, "dkv_gemm_bf16: unknown flags");
+    DKV_REQUIRE((flags & ~(DKV_GEMM_SWIGLU | DKV_GEMM_DEFER | DKV_GEMM_WTILED)) == 0, "dkv_gemm_bf16: unknown flags");
     const int swiglu = (flags & DKV_GEMM_SWIGLU) != 0;
     const int defer = (flags & DKV_GEMM_DEFER) != 0;
+    const bool wt = (flags & DKV_GEMM_WTILED) != 0;
+    DKV_REQUIRE(!wt || K % GKB == 0, "dkv_gemm_bf16: tiled W needs K a multiple of 128");
     DKV_REQUIRE(!defer || (!swiglu && !bias && y_dtype == DKV_BF16),
                 "dkv_gemm_bf16: deferred partials are for a bf16 y without bias or SwiGLU");
     DKV_REQUIRE(!swiglu || (y_dtype == DKV_BF16 && !bias),
@@ -540,17 +597,15 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
     hipStream_t st = as_stream(stream);
     if (p.small) {
         DKV_REQUIRE((int64_t)S * p.rw * p.mb * 4 * WAVE * sizeof(float) <= 64 * 1024, "dkv_gemm_bf16: too many K chunks");
-        launch_small<1, 4, 1>(a, p.n_tiles, st);   // S >= 4, a power of two; chunks of whole 128-k blocks
+        if (wt) launch_small<1, 4, 1, true>(a, p.n_tiles, st);   // S >= 4, a power of two; chunks of whole 128-k blocks
+        else launch_small<1, 4, 1, false>(a, p.n_tiles, st);
         return check_launch("dkv_gemm_bf16");
     }
     const int64_t nwg = (int64_t)(a.units + 7) / 8 * 8 * p.m_tiles;
     DKV_REQUIRE(nwg < (int64_t)1 << 31, "dkv_gemm_bf16: too many workgroups");
     const dim3 grid((unsigned)nwg);
-    if (p.nw == 2 && p.mb == 4) launch_gemm<2, 4, false>(a, grid, st);   // K % 128 == 0 with two fragments
-    else if (p.nw == 2) launch_gemm<2, 8, false>(a, grid, st);
-    else if (p.mb == 1) launch_gemm<1, 1>(a, grid, st);
-    else if (p.mb == 2) launch_gemm<1, 2>(a, grid, st);
-    else launch_gemm<1, 4>(a, grid, st);
+    if (wt) launch_plan<true>(p, a, grid, st);
+    else launch_plan<false>(p, a, grid, st);
     int rc = check_launch("dkv_gemm_bf16");
     if (rc || !need || defer) return rc;   // deferred: the consumer sums the partials
     const int64_t MN = (int64_t)M * N;   // a multiple of 16

@@ -14,7 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "libdraftkv_hip.so")
 
 DKV_F32, DKV_BF16 = 0, 1
-DKV_GEMM_SWIGLU, DKV_GEMM_DEFER = 1, 2
+DKV_GEMM_SWIGLU, DKV_GEMM_DEFER, DKV_GEMM_WTILED = 1, 2, 4
 _ERRORS = {-1: ValueError, -2: RuntimeError, -3: MemoryError, -4: MemoryError}
 
 

@@ -139,6 +139,21 @@ class Decoder:
         return ops.add_norm(h, self._linear(x, w, defer=True), bias, nw, nb, self.eps, self.norm == "layer",
                             self.act_dtype)
 
+    def _tile_weights(self) -> None:
+        """bf16 models: store every projection weight the bf16 GEMM takes in its
+        tiled form (``ops.TiledW``: 1 KB contiguous per load of W), and the LM
+        head too unless it is the (tied) embedding table. The arithmetic is
+        unchanged; ``TiledW.rows()`` gives a matrix back."""
+        if self.wdtype != torch.bfloat16 or self.device.type != "cuda":
+            return
+        for p in self.layers:
+            for name in ("wqkv", "wo", "w1", "w2"):
+                w = getattr(p, name)
+                if ops.tile_ok(w):
+                    setattr(p, name, ops.TiledW(w))
+        if self.head is not self.emb and ops.tile_ok(self.head):
+            self.head = ops.TiledW(self.head)
+
     def _interleave_gate_up(self) -> None:
         """bf16 SwiGLU models: reorder each fused [gate; up] weight to rows
         (gate_0, up_0, gate_1, up_1, ...), so the GEMM's epilogue holds both

@@ -117,6 +117,7 @@ class GPT2(Decoder):
         self.nfw, self.nfb = self._v(w[f"{pre}ln_f.weight"]), self._v(w[f"{pre}ln_f.bias"])
         self.head = self.emb                       # tied: logits = h @ wte.T (gpt2.py:213)
         self.head_layout = 1
+        self._tile_weights()
 
     @classmethod
     def from_dir(cls, d, **kw) -> "GPT2":                             # gpt2.py:169-174

@@ -82,6 +82,7 @@ class LlamaLike(Decoder):
         self.head = self.emb if head is None else self._w(head, 1)        # tied when absent
         self.head_layout = 1
         self._interleave_gate_up()
+        self._tile_weights()
 
     @classmethod
     def from_dir(cls, d, **kw) -> "LlamaLike":                          # llama.py:152-156

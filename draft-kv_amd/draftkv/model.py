@@ -67,6 +67,7 @@ class TinyTransformer(Decoder):
         self.nfw, self.nfb = self._v(np.ones(d_model, f32)), None
         self.head = self._w((rng.standard_normal((d_model, vocab_size)) * s).astype(f32), 0)
         self.head_layout = self.w_layout
+        self._tile_weights()
 
 
 def demo_model(seed: int = 1, **kw) -> TinyTransformer:            # model.py:143-156

@@ -12,7 +12,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import DKV_BF16, DKV_F32, DKV_GEMM_DEFER, Drafter, Paged, QCfg, check, lib
+from ._lib import DKV_BF16, DKV_F32, DKV_GEMM_DEFER, DKV_GEMM_SWIGLU, DKV_GEMM_WTILED, Drafter, Paged, QCfg, check, lib
 
 
 _get_device = getattr(torch._C, "_cuda_getDevice", None)
@@ -469,12 +469,64 @@ def gemm_f32(x: torch.Tensor, w: torch.Tensor, w_layout: int, bias: Optional[tor
     return out
 
 
-def gemm_bf16_ok(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None) -> bool:
+class TiledW:
+    """A bf16 weight [N, K] (N % 16 == 0, K % 128 == 0) stored for
+    dkv_gemm_bf16's DKV_GEMM_WTILED: 16-row x 128-k tiles of 4 KB, a 16-row
+    fragment's tiles consecutive along k, each tile in the MFMA A-operand
+    order of its four 32-k steps (element (16 fn + c, 128 kb + 32 j + 8 q + e)
+    at (fn * K/128 + kb) * 2048 + j * 512 + (16 q + c) * 8 + e). Every load
+    of W is then 1 KB contiguous. ``rows()`` gives the [N, K] matrix back."""
+
+    __slots__ = ("t", "shape")
+    dtype = torch.bfloat16
+
+    def __init__(self, w: torch.Tensor) -> None:
+        if not tile_ok(w):
+            raise ValueError(f"TiledW: needs a contiguous bf16 [N, K] with N % 16 == 0 and K % 128 == 0, "
+                             f"got {tuple(w.shape)} {w.dtype}")
+        N, K = w.shape
+        self.shape = (N, K)
+        self.t = w.view(N // 16, 16, K // 128, 4, 4, 8).permute(0, 2, 3, 4, 1, 5).contiguous()
+
+    def rows(self) -> torch.Tensor:
+        N, K = self.shape
+        return self.t.permute(0, 4, 1, 2, 3, 5).reshape(N, K)
+
+    @property
+    def device(self):
+        return self.t.device
+
+    @property
+    def is_cuda(self) -> bool:
+        return self.t.is_cuda
+
+    def numel(self) -> int:
+        return self.t.numel()
+
+    def element_size(self) -> int:
+        return 2
+
+    def data_ptr(self) -> int:
+        return self.t.data_ptr()
+
+    def dim(self) -> int:
+        return 2
+
+
+def tile_ok(w) -> bool:
+    return (isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_contiguous()
+            and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0 and w.shape[0] > 0)
+
+
+def gemm_bf16_ok(x: torch.Tensor, w, bias: Optional[torch.Tensor] = None) -> bool:
     """Whether dkv_gemm_bf16 takes this product (contiguous x [M, K], bf16 or
-    float32, and bf16 w [N, K], N % 16 == 0, K % 32 == 0, 16-byte aligned;
-    bias None or bf16 contiguous [N], 8-byte aligned)."""
-    ok = (x.dtype in (torch.bfloat16, torch.float32) and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2
-          and x.is_cuda and w.is_cuda and x.is_contiguous() and w.is_contiguous()
+    float32, and bf16 w [N, K] (a tensor or a ``TiledW``), N % 16 == 0,
+    K % 32 == 0, 16-byte aligned; bias None or bf16 contiguous [N], 8-byte
+    aligned)."""
+    if not isinstance(w, TiledW) and not (isinstance(w, torch.Tensor) and w.dim() == 2 and w.is_contiguous()):
+        return False
+    ok = (x.dtype in (torch.bfloat16, torch.float32) and w.dtype == torch.bfloat16 and x.dim() == 2
+          and x.is_cuda and w.is_cuda and x.is_contiguous()
           and x.shape[1] == w.shape[1] and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0
           and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
     if ok and bias is not None:
@@ -505,7 +557,7 @@ class Partials:
         return self.part.data_ptr()
 
 
-def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+def gemm_bf16(x: torch.Tensor, w, bias: Optional[torch.Tensor] = None,
               out_dtype=torch.bfloat16, swiglu: bool = False, defer: bool = False):
     """x [M, K] @ w[N, K]^T (+ bias), bf16 in (a float32 x is rounded to bf16
     as it is read), float32 accumulation, bf16 (or float32) out; a row's
@@ -525,13 +577,14 @@ def gemm_bf16(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = N
     S = lib().dkv_gemm_bf16_partials(M, N, K) if defer else 0
     nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)
     ws = _WS.get(x.device, nbytes) if nbytes else None
+    wflag = DKV_GEMM_WTILED if isinstance(w, TiledW) else 0
     if S > 0:
         check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), None, M, N, K, ws.data_ptr(),
-                                  _odt(out_dtype), DKV_GEMM_DEFER, ws.data_ptr(), ws.numel(), _stream()),
+                                  _odt(out_dtype), DKV_GEMM_DEFER | wflag, ws.data_ptr(), ws.numel(), _stream()),
               "dkv_gemm_bf16")
         return Partials(ws, S, (M, N))
     out = torch.empty((M, N // 2 if swiglu else N), dtype=out_dtype, device=x.device)
     check(lib().dkv_gemm_bf16(x.data_ptr(), _odt(x.dtype), w.data_ptr(), _ptr(bias), M, N, K, out.data_ptr(),
-                              _odt(out_dtype), 1 if swiglu else 0,
+                              _odt(out_dtype), (DKV_GEMM_SWIGLU if swiglu else 0) | wflag,
                               _ptr(ws), 0 if ws is None else ws.numel(), _stream()), "dkv_gemm_bf16")
     return out

@@ -312,6 +312,10 @@ int dkv_gemm_f32(const float* x, const float* w, int32_t w_layout, int32_t M, in
                               start of work and skip the reduce: y is not written, and the consumer
                               sums them (dkv_add_norm_partials, dkv_qkv_split_partials); otherwise
                               y is written as usual. bf16 y only, no bias, no SwiGLU */
+#define DKV_GEMM_WTILED 4  /* flags: w is stored in 16-row x 128-k tiles (K a multiple of 128): the
+                              4 KB tile (fn, kb) at (fn * K/128 + kb) * 2048 elements, holding
+                              element (16 fn + c, 128 kb + 32 j + 8 q + e) at j * 512 + (16 q + c) * 8 + e,
+                              so every load of W is 1 KB contiguous; same arithmetic and results */
 size_t dkv_gemm_bf16_workspace(int32_t M, int32_t N, int32_t K);
 /* the chunk count S of the partials dkv_gemm_bf16 writes for (M, N, K), or 0 when its plan
  * writes y directly (a function of the launch plan, not of the arithmetic) */

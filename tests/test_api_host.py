@@ -183,3 +183,30 @@ def test_growing_full_cache_reserve_matches_block_by_block():
         assert (a.tables == b.tables).all() and (a.table_len == b.table_len).all()
         assert all(p._stack == q._stack for p, q in zip(a.pools, b.pools))
         assert (a.d_tables.numpy() == b.d_tables.numpy()).all()
+
+
+def test_tiled_weight_layout_and_round_trip():
+    """ops.TiledW puts element (16 fn + c, 128 kb + 32 j + 8 q + e) of a bf16
+    [N, K] weight at (fn * K/128 + kb) * 2048 + j * 512 + (16 q + c) * 8 + e
+    (the MFMA A-operand order the tiled GEMM reads), and rows() gives the
+    matrix back; shapes it cannot tile are refused. Two weights whose
+    entries are their row and their column (exact in bf16) locate every
+    element."""
+    import itertools
+    import torch
+    from draftkv import ops
+    N, K = 48, 256
+    rows = torch.arange(N, dtype=torch.float32)[:, None].expand(N, K).contiguous().to(torch.bfloat16)
+    cols = torch.arange(K, dtype=torch.float32)[None, :].expand(N, K).contiguous().to(torch.bfloat16)
+    tr, tc = ops.TiledW(rows).t.reshape(-1), ops.TiledW(cols).t.reshape(-1)
+    assert tr.numel() == N * K
+    for fn, kb, j, q, c, e in itertools.product(range(N // 16), range(K // 128), range(4), range(4), range(16), range(8)):
+        off = ((fn * (K // 128) + kb) * 4 + j) * 512 + (16 * q + c) * 8 + e
+        assert int(tr[off]) == 16 * fn + c and int(tc[off]) == 128 * kb + 32 * j + 8 * q + e
+    w = torch.randn((N, K)).to(torch.bfloat16)
+    assert torch.equal(ops.TiledW(w).rows(), w)
+    for bad in (torch.zeros((24, 256), dtype=torch.bfloat16), torch.zeros((32, 192), dtype=torch.bfloat16),
+                torch.zeros((32, 256), dtype=torch.float32)):
+        assert not ops.tile_ok(bad)
+        with pytest.raises(ValueError):
+            ops.TiledW(bad)

@@ -127,7 +127,8 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
                                              (8, 4096, 14336, False), (17, 6144, 4096, False),
                                              (32, 4096, 4096, True), (33, 512, 14336, False),
                                              (96, 6144, 4096, True), (200, 1024, 2048, False), (64, 272, 96, True),
-                                             (544, 4096, 4096, False)])
+                                             (544, 4096, 4096, False), (32, 28672, 4096, True),
+                                             (96, 28672, 4096, False)])
 def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     """bf16 x @ W^T (+ b) against the float32 product of the same bf16 values
     (one rounding to bf16 apart), float32 output too, and every row equal to
@@ -136,7 +137,8 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     of 16 to 128 rows, several M tiles, K chunks split over workgroups
     (partials + ordered reduce) or summed inside one, the small-M kernel that
     splits K among the waves of a workgroup, 128-k blocks and the 32-k
-    tail."""
+    tail, and the 7-wave workgroups of the 28672-row gate/up weight (whose
+    rows must equal those of the 4-wave plan at M = 96)."""
     ops = _ops()
     g = torch.Generator(device=dev).manual_seed(M + N + K)
     x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
@@ -247,6 +249,38 @@ def test_qkv_split_on_deferred_partials_equals_gemm_then_split(dev, M, rope, bia
     got = ops.qkv_split(p, b, Hq, Hkv, D, pos, cs, n)
     for r, o in zip(ref, got):
         assert torch.equal(r, o)
+
+
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 4096, 4096, False), (6, 1024, 4096, True), (8, 4096, 14336, False),
+                                             (17, 6144, 4096, True), (32, 4096, 4096, False),
+                                             (32, 28672, 4096, False), (12, 28672, 4096, True),
+                                             (96, 6144, 4096, False), (200, 1024, 2048, True), (96, 4096, 14336, False)])
+def test_gemm_bf16_tiled_weights_equal_row_major(dev, M, N, K, with_bias):
+    """W stored in 16x128 tiles (ops.TiledW, DKV_GEMM_WTILED) gives bit for bit
+    the row-major product on every launch plan (small-M in-workgroup split, x
+    tiles of 16-128 rows, one or two fragments per wave, 7-wave workgroups,
+    partials + reduce or deferred to the consumer, float32 output, float32 x,
+    the SwiGLU epilogue)."""
+    ops = _ops()
+    g = torch.Generator(device=dev).manual_seed(M * 3 + N + K)
+    w = (0.05 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+    wt = ops.TiledW(w)
+    assert torch.equal(wt.rows(), w)
+    bias = (0.1 * torch.randn(N, generator=g, device=dev)).to(torch.bfloat16) if with_bias else None
+    x = torch.randn((M, K), generator=g, device=dev)
+    for xx in (x, x.to(torch.bfloat16)):
+        assert torch.equal(ops.gemm_bf16(xx, wt, bias), ops.gemm_bf16(xx, w, bias))
+        assert torch.equal(ops.gemm_bf16(xx, wt, bias, out_dtype=torch.float32),
+                           ops.gemm_bf16(xx, w, bias, out_dtype=torch.float32))
+    if not with_bias:   # the deferred partials (the op workspace holds one set at a time)
+        pr = ops.gemm_bf16(x, w, defer=True)
+        ref = pr.part.view(torch.float32)[: pr.n_part * M * N].clone() if isinstance(pr, ops.Partials) else pr
+        pt = ops.gemm_bf16(x, wt, defer=True)
+        assert isinstance(pt, ops.Partials) == isinstance(pr, ops.Partials)
+        got = pt.part.view(torch.float32)[: pt.n_part * M * N] if isinstance(pt, ops.Partials) else pt
+        assert torch.equal(got, ref)
+    if N % 32 == 0:
+        assert torch.equal(ops.gemm_bf16(x, wt, swiglu=True), ops.gemm_bf16(x, w, swiglu=True))
 
 
 def test_gemm_bf16_rejects_unsupported_operands(dev):
