@@ -20,7 +20,7 @@ ROWS = [1, 7, 32, 300]
 
 
 @pytest.mark.parametrize("rows", ROWS)
-@pytest.mark.parametrize("d", [64, 576, 768, 4096])
+@pytest.mark.parametrize("d", [64, 100, 576, 768, 4096, 8192])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 def test_add_rmsnorm_and_layernorm(dev, rows, d, xdt):
     ops = _ops()
