@@ -892,8 +892,9 @@ def run_gemm(args):
     counts of a b=32 decode step (M = 32), a gamma-2 verify (96) and a gamma-8
     verify (288), rotating over 8 layers' weights (3.5 GB, so every call
     streams its weights from HBM), stored tiled as the bf16 models store them
-    (``ops.TiledW``). Each call timed with HIP events on the launch stream;
-    algorithmic bytes: the weights once, x once, y once."""
+    (``ops.TiledW``). The 8 calls of a shape run back to back between one
+    pair of HIP events on the launch stream; algorithmic bytes: the weights
+    once, x once, y once."""
     import torch
     from draftkv import ops
     dev = torch.device("cuda")
@@ -908,21 +909,23 @@ def run_gemm(args):
     res = {}
     for M in (32, 96, 288):
         X = {k: torch.randn((M, kk), generator=g, device=dev).to(xd) for k, (n, kk, xd, _) in shapes.items()}
+        # one event pair around the nl calls of a shape (back to back, as in a
+        # forward; a pair around every call would add its markers' idle gaps)
         per = {}
         for rep in range(args.warmup + args.steps):
-            for i in range(nl):
-                for k, (n, kk, xd, sw) in shapes.items():
-                    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    s_ev.record()
+            for k, (n, kk, xd, sw) in shapes.items():
+                s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s_ev.record()
+                for i in range(nl):
                     ops.gemm_bf16(X[k], W[k][i], None, torch.bfloat16, swiglu=sw)
-                    e_ev.record()
-                    if rep >= args.warmup:
-                        per.setdefault(k, []).append((s_ev, e_ev))
+                e_ev.record()
+                if rep >= args.warmup:
+                    per.setdefault(k, []).append((s_ev, e_ev))
         torch.cuda.synchronize()
         row = {}
         tot_b = tot_us = 0.0
         for k, (n, kk, xd, sw) in shapes.items():
-            us = 1e3 * sum(a.elapsed_time(c) for a, c in per[k]) / len(per[k])
+            us = 1e3 * sum(a.elapsed_time(c) for a, c in per[k]) / (len(per[k]) * nl)
             nbytes = n * kk * 2 + M * kk * (4 if xd == torch.float32 else 2) + M * (n // 2 if sw else n) * 2
             row[k] = {"us": us, "GB/s": nbytes / (us * 1e-6) / 1e9, "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
             tot_b += nbytes
