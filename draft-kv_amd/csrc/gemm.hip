@@ -9,11 +9,14 @@
 // Every output is, per chunk, one in-order chain of
 // v_mfma_f32_16x16x32_bf16 over the chunk's 128-k blocks (block step j,
 // lane group q: k = 32j + 8q .. +8, the same for W and x), and the chunk
-// sums are added in chunk order, either inside the workgroup or by the
-// reduce kernel from per-chunk partials -- the same float additions in the
-// same order. So an output's arithmetic depends neither on M, nor on the
-// launch shape chosen for M, nor on the row's place in the batch: a verify
-// row equals the one-token decode row bit for bit.
+// sums are added in chunk order, either inside the workgroup, or from
+// per-chunk partials by the reduce kernel or by the kernel that consumes y
+// (DKV_GEMM_DEFER) -- the same float additions in the same order. So an
+// output's arithmetic depends neither on M, nor on the launch shape chosen
+// for M, nor on the row's place in the batch: a verify row equals the
+// one-token decode row bit for bit. W is row-major or tiled
+// (DKV_GEMM_WTILED); the layout changes which addresses a lane loads, not
+// what it multiplies.
 #include "dkv_common.h"
 
 #include <type_traits>
@@ -114,7 +117,7 @@ __device__ __forceinline__ int64_t w_step_off(int k, int j) {
 
 // One workgroup: WV waves, 16*NW*WV rows of W (16*NW per wave), against a
 // tile of 16*MB rows of x, over c_per consecutive K chunks. Per 128-k block the tile's x
-// is staged once in LDS (shared by the four waves); each lane streams its W
+// is staged once in LDS (shared by the waves); each lane streams its W
 // rows straight into registers PD - 1 blocks ahead (PD register sets in
 // rotation). MULTI: the chunks' sums are added in chunk order here (the same
 // additions, in the same order, as the reduce kernel applies to partials).
