@@ -510,11 +510,20 @@ class DecodeBatch:
         self.resolve_tokens()             # the read-back above waited for every earlier copy
         self._dev_pending = None
 
-        # -- bookkeeping, rollback, resync
-        h0 = time.perf_counter()
+        # -- rollback and resync first (queued on the device), then the host's
+        # bookkeeping, which runs while the device resyncs the mirror
+        seqs = np.flatnonzero(active)
         cut = flen.copy()
+        cut[seqs] = n[seqs] + host[seqs, 0]
+        if ph is not None:
+            ev["s0"] = ph.event()
+        full.truncate(cut)
+        self._sync(np.where(active, n - 1, full.lengths()))
+        if ph is not None:
+            ev["end"] = ph.event()
+        h0 = time.perf_counter()
         emitted_total = 0
-        for s in np.flatnonzero(active):
+        for s in seqs:
             a, nx, k = int(host[s, 0]), int(host[s, 1]), int(host[s, 2])
             emitted = [int(t) for t in host[s, 3: 3 + a]] + [nx]
             toks[s].extend(emitted)
@@ -522,18 +531,12 @@ class DecodeBatch:
             g = eng._g(s)
             g.bit_generator.state = states[s]
             g.bit_generator.advance(k)
-            cut[s] = n[s] + a
             eng.controller.update(cfg, gamma, a, int(n[s]), self.key)
             res[s].rounds.append(RoundLog(cfg, gamma, a, len(emitted), int(n[s])))
             res[s].draft_steps += gamma
             res[s].verify_passes += 1
         hs = time.perf_counter() - h0
-        if ph is not None:
-            ev["s0"] = ph.event()
-        full.truncate(cut)
-        self._sync(np.where(active, n - 1, full.lengths()))
         self.last_emitted = emitted_total
         if ph is not None:
-            ev["end"] = ph.event()
             ph.add(cfg, gamma, ev, emitted_total, hs)
         return True
