@@ -835,6 +835,290 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
     c.finish(part, s, h, Hq, G, n_splits, wid);
 }
 
+// ---- segment kernel (4-bit codes, D = 128, 4 query heads x 4 groups per KV
+// head): one block of 8 waves per (sequence, KV head) segment, used when the
+// segments alone fill the chip (batch x KV heads >= 256). The waves stream
+// their pages as the LDS-staged kernel does, but keep each page's logits in
+// registers instead of writing them to the workspace (33.5 MB of scattered
+// writes at b=32 ctx 32k cost the split-K pass a quarter of its time, mixed
+// into the read stream). After a block barrier the 8 partials meet in LDS --
+// the combine kernel's merge, in its order -- and each lane turns its logits
+// into probabilities with the final max and sum, summed over the KV head's 4
+// query heads across a lane quad: one float per row and KV head goes out, and
+// draft_mass_sum_kernel adds the KV heads' sums to the row scores.
+//
+// The logits buffer: lane (gcol, hcol, jj) keeps rows 4jj+gcol and
+// 16+4jj+gcol of head hcol (the 4 group columns of a head hold the same 8
+// rows and share them out), two floats per page, in VGPRs above the
+// compiler's allocation (amdgpu_num_vgpr caps it at SEG_VGPRS; the clobber of
+// v255 sizes the wave's allocation to 256), written and read with
+// s_set_gpr_idx at a wave-uniform index. Pages past SEG_TMAX spill to the
+// workspace.
+constexpr int SEG_WAVES = 8;
+constexpr int SEG_VGPRS = 176;                  // the compiler's registers
+constexpr int SEG_TMAX = (256 - SEG_VGPRS) / 2;  // pages per wave kept in registers
+#ifndef SEG_OLD
+#define SEG_OLD 10
+#endif
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// buffer registers v176 + i2, v177 + i2 <- (a, b)
+__device__ __forceinline__ void seg_put(int i2, float a, float b) {
+    asm volatile("s_set_gpr_idx_on %0, gpr_idx(DST)\n\t"
+                 "v_mov_b32 v176, %1\n\t"
+                 "v_mov_b32 v177, %2\n\t"
+                 "s_set_gpr_idx_off" ::"s"(i2),
+                 "v"(a), "v"(b)
+                 : "m0", "v255");
+}
+// (a, b) <- buffer registers v176 + i2, v177 + i2
+__device__ __forceinline__ void seg_get(int i2, float& a, float& b) {
+    asm volatile("s_set_gpr_idx_on %2, gpr_idx(SRC0)\n\t"
+                 "v_mov_b32 %0, v176\n\t"
+                 "v_mov_b32 %1, v177\n\t"
+                 "s_set_gpr_idx_off"
+                 : "=v"(a), "=v"(b)
+                 : "s"(i2)
+                 : "m0");
+}
+#pragma clang diagnostic pop
+
+// t where the lane's bit of mask is set, else f (one v_cndmask_b32; written out
+// so that a select between registers does not become an indexed stack load)
+__device__ __forceinline__ float lane_select(float f, float t, uint64_t mask) {
+    float r;
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(mask));
+    return r;
+}
+
+// lane-quad sum (lanes 4k..4k+3): the bitwise-same total in each lane
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
+    return v;
+}
+
+template <int MF, int LPP>
+__global__ void __launch_bounds__(64 * SEG_WAVES, 1) __attribute__((amdgpu_num_vgpr(SEG_VGPRS)))
+draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* __restrict__ q, int Hq, float scale,
+                      float* __restrict__ out, float* __restrict__ spill, float* __restrict__ pmass) {
+    constexpr int D = 128, CB = 4, G = 4;
+    using Core = SplitCore<D, CB, MF>;
+    using Regs = typename Core::Regs;
+    constexpr int NVL = D / 64;
+    constexpr int S = dma_stages(LPP);
+    constexpr int SLOT = LPP * 1024;
+    constexpr int PD = D + 2;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int h = blockIdx.y, s = blockIdx.z;
+    const int Hkv = m.n_kv_heads;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    const int np = (n + PAGE - 1) / PAGE;
+    // contiguous page runs; with at least 64 pages, waves 0-3 (the older
+    // wave of each SIMD, which wins issue by age) take SEG_OLD/16 of them
+    // (every wave keeps at least 4 pages for SEG_OLD <= 12)
+    const int A = min(SEG_WAVES, np);
+    const bool active = wave < A;
+    auto cut = [&](int w) -> int {
+        if (A < SEG_WAVES || np < 64) return (int)(((int64_t)w * np) / A);   // every wave >= 1 page
+        const int c = w <= 4 ? w * SEG_OLD : 4 * SEG_OLD + (w - 4) * (16 - SEG_OLD);   // in 64ths
+        return (int)(((int64_t)c * np) / 64);
+    };
+    const int pg0 = active ? cut(wave) : 0;
+    const int T = active ? cut(wave + 1) - pg0 : 0;
+    const bool tail = wave == A - 1 && n % PAGE != 0;
+    const bool keep = pmass != nullptr;
+    extern __shared__ __align__(16) char dma_smem[];
+    Core c;
+    if (active) {
+        const PageFmt f = page_fmt(cfg, D);
+        const uint32_t kmb = (uint32_t)(f.vc - f.km);
+        char* ring = dma_smem + (size_t)wave * S * SLOT;
+        int slot_in = 0, slot_out = 0;
+        const int col = lane % 16, jj = lane / 16;
+        uint32_t src[LPP];
+#pragma unroll
+        for (int i = 0; i < LPP; ++i) {
+            uint32_t o;
+            if (i < 2) {
+                o = (uint32_t)f.kc + i * 1024 + lane * 16;
+            } else if (i < 2 + NVL) {
+                o = (uint32_t)f.vc + (col * 4 + jj) * Regs::NV * 4 + (i - 2) * 16;
+            } else {
+                const uint32_t mo = (i - 2 - NVL) * 1024 + lane * 16;
+                o = mo < kmb ? (uint32_t)f.km + mo : (mo < 2 * kmb ? (uint32_t)f.vm + (mo - kmb) : (uint32_t)f.km);
+            }
+            src[i] = o;
+        }
+        auto issue = [&](int g) {
+            const uint8_t* pg = page_ptr(m, s, layer, h, pg0 + g);
+            const uint32_t dst = lds_addr(ring + slot_in);
+#pragma unroll
+            for (int i = 0; i < LPP; ++i) dma16(pg, src[i], dst + i * 1024);
+            slot_in = slot_in + SLOT == S * SLOT ? 0 : slot_in + SLOT;
+        };
+        for (int j = 0; j < S - 1; ++j)
+            if (j < T) issue(j);
+        c.init(q, s, h, Hq, G, cfg.group, lane, scale);
+        c.reset();
+        constexpr uint32_t mbase = (2 + NVL) * 1024;
+        const uint32_t o_k = (c.col * 4 + c.jj) * 16;
+        const uint32_t o_v = 2 * 1024 + lane * 16;
+        const uint32_t o_km = mbase + (c.gmeta * PAGE + 4 * c.jj) * f.metaB;
+        const uint32_t o_vm = mbase + kmb + (c.gmeta * PAGE + 8 * c.jj) * f.metaB;
+        auto operands = [&](Regs& r) {
+            const char* sl = ring + slot_out;
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                load_words(r.k[a], reinterpret_cast<const uint8_t*>(sl + a * 1024 + o_k));
+                load_words(r.km[a], reinterpret_cast<const uint8_t*>(sl + o_km + 16 * a * f.metaB));
+            }
+#pragma unroll
+            for (int x = 0; x < NVL; ++x) {
+                const uint4 w = *reinterpret_cast<const uint4*>(sl + x * 1024 + o_v);
+                r.v[4 * x] = w.x;
+                r.v[4 * x + 1] = w.y;
+                r.v[4 * x + 2] = w.z;
+                r.v[4 * x + 3] = w.w;
+            }
+            load_words(r.vm, reinterpret_cast<const uint8_t*>(sl + o_vm));
+            slot_out = slot_out + SLOT == S * SLOT ? 0 : slot_out + SLOT;
+        };
+        // a page's logits: the lane's two rows (x = gcol and gcol + 4 of its 8)
+        const uint64_t g1 = __ballot((c.gcol & 1) != 0), g2 = __ballot((c.gcol & 2) != 0);
+        float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
+        auto stash = [&](const float (&pv)[8], int p0) {
+            if (!keep) return;
+            const float a = lane_select(lane_select(pv[0], pv[1], g1), lane_select(pv[2], pv[3], g1), g2);
+            const float b = lane_select(lane_select(pv[4], pv[5], g1), lane_select(pv[6], pv[7], g1), g2);
+            const int g = __builtin_amdgcn_readfirstlane(p0 / PAGE - pg0);
+            if (g < SEG_TMAX) seg_put(2 * g, a, b);
+            else *reinterpret_cast<float2*>(spill_w + (int64_t)g * (2 * WAVE)) = make_float2(a, b);
+        };
+        // the LDS-staged kernel's page pipeline, with the logits kept instead
+        // of stored: the waits count loads only (spilled pages wait as if
+        // they were not there; a spill store only makes a wait longer)
+        Regs ra, rb;
+        float sa_[8], sb_[8];
+        vm_wait(LPP * min(S - 2, T - 1));
+        operands(ra);
+        c.qk(ra, sa_);
+        auto step = [&](int g, Regs& cur, float (&scur)[8], Regs& nxt, float (&snxt)[8]) {
+            vm_wait(LPP * max(0, min(S - 3, T - 2 - g)));
+            if (g + S - 1 < T) issue(g + S - 1);
+            operands(nxt);
+            float pv[8];
+            c.template rest_head<false>(scur, (pg0 + g) * PAGE, n, stash, pv);
+            f32x4_t acc_next[2];
+            c.qk_mfma(nxt, acc_next);
+            c.template rest_tail<false>(cur, pv, (pg0 + g) * PAGE, n);
+            c.qk_fold(nxt, acc_next, snxt);
+        };
+        auto last = [&](int g, const Regs& cur, const float (&scur)[8]) {
+            if (tail) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, stash);
+            else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, stash);
+        };
+        int g = 0;
+        for (; g + 2 < T; g += 2) {
+            step(g, ra, sa_, rb, sb_);
+            step(g + 1, rb, sb_, ra, sa_);
+        }
+        if (g + 1 < T) {
+            step(g, ra, sa_, rb, sb_);
+            last(g + 1, rb, sb_);
+        } else {
+            last(g, ra, sa_);
+        }
+    }
+    // ---- merge: the partials [head][wave][D+2] and the heads' (max, 1/sum)
+    // in the LDS the ring held (every page has landed and been read)
+    __syncthreads();
+    float* sp = reinterpret_cast<float*>(dma_smem);
+    float* sst = sp + G * SEG_WAVES * PD;
+    if (active) c.finish(sp, 0, 0, G, G, SEG_WAVES, wave);
+    __syncthreads();
+    {
+        const int hl = threadIdx.x / D, d = threadIdx.x % D;   // 512 threads = G x D outputs
+        const float* ph = sp + hl * SEG_WAVES * PD;
+        float mm = -INFINITY;
+        for (int w = 0; w < A; ++w) mm = fmaxf(mm, ph[w * PD + D]);
+        float l = 0.0f, o = 0.0f;
+        for (int w = 0; w < A; ++w) {
+            const float mc = ph[w * PD + D], lc = ph[w * PD + D + 1];
+            const float wt = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
+            l = fmaf(lc, wt, l);
+            o = fmaf(ph[w * PD + d], wt, o);
+        }
+        out[((int64_t)s * Hq + h * G + hl) * D + d] = (l > 0.0f) ? o / l : 0.0f;
+        if (d == 0) {
+            sst[2 * hl] = mm;
+            sst[2 * hl + 1] = l > 0.0f ? 1.0f / l : 0.0f;
+        }
+    }
+    if (!keep) return;
+    __syncthreads();
+    if (!active) return;
+    // ---- mass: p = exp(logit - max) / sum per kept value, summed over the
+    // quad of the KV head's 4 query heads (lanes hcol 0..3 of a group column)
+    {
+        const float mm = sst[2 * c.hcol], il = sst[2 * c.hcol + 1];
+        const uint64_t hb0 = __ballot((c.hcol & 1) != 0), hb1 = __ballot((c.hcol & 2) != 0);
+        const int row2 = (c.hcol >> 1) * PAGE + (c.hcol & 1) * 16 + 4 * c.jj + c.gcol;   // row in the page pair
+        float* pm = pmass + (int64_t)(s * Hkv + h) * m.cap + pg0 * PAGE + row2;
+        const float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
+        const int r_end = (pg0 + T) * PAGE <= n ? T * PAGE : n - pg0 * PAGE;   // the wave's live rows
+        // 8 pages at a time, so the reads, exps and quad sums of different
+        // pages overlap
+        constexpr int U = 8;
+        for (int g0 = 0; g0 < T; g0 += U) {
+            float a[U], b[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const int g = g0 + k;
+                if (g < T && g < SEG_TMAX) {
+                    seg_get(2 * g, a[k], b[k]);
+                } else if (g < T) {
+                    const float2 v = *reinterpret_cast<const float2*>(spill_w + (int64_t)g * (2 * WAVE));
+                    a[k] = v.x;
+                    b[k] = v.y;
+                } else {
+                    a[k] = b[k] = -INFINITY;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                a[k] = quad_sum(__expf(a[k] - mm) * il);
+                b[k] = quad_sum(__expf(b[k] - mm) * il);
+            }
+            // every lane of a quad holds both sums of its rows: lane hcol
+            // writes page g0 + k + (hcol >> 1), half (hcol & 1), so one store
+            // covers two pages (64 rows, 256 contiguous bytes)
+#pragma unroll
+            for (int k = 0; k < U; k += 2) {
+                const float lo = lane_select(a[k], b[k], hb0), hi = lane_select(a[k + 1], b[k + 1], hb0);
+                const float v = lane_select(lo, hi, hb1);
+                const int r = (g0 + k) * PAGE + row2;
+                if (r < r_end) pm[(g0 + k) * PAGE] = v;
+            }
+        }
+    }
+}
+
+// score[row] += sum over KV heads of the per-KV-head masses of the segment
+// kernel (KV heads in order)
+__global__ void __launch_bounds__(256) draft_mass_sum_kernel(dkv_drafter_t m, int layer,
+                                                             const float* __restrict__ pmass) {
+    const int s = blockIdx.y;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const float* p = pmass + (int64_t)s * m.n_kv_heads * m.cap + r;
+    float t = p[0];
+    for (int hk = 1; hk < m.n_kv_heads; ++hk) t += p[(int64_t)hk * m.cap];
+    m.score[row_index(m, s, layer) + r] += static_cast<double>(t);
+}
+
 // ---------------------------------------------------------------- combine + mass
 // Merge the partials of (seq, query head) and record the final (max, sum).
 // Partial slots [0, min(live units, n_splits, n_parts)) hold data, a unit
@@ -959,17 +1243,19 @@ static int n_splits_of(const dkv_drafter_t* m, int n_q_heads) {
 }
 
 // workspace sections, each starting on a 256-byte boundary: partials
-// [b][Hq][splits][D+2], stats [b][Hq][2], logits [b][Hq][cap] (with mass)
+// [b][Hq][splits][D+2], stats [b][Hq][2], logits [b][Hq][cap] and the segment
+// kernel's per-KV-head masses [b][Hkv][cap] (with mass)
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 struct DraftWork {
-    size_t stats_off, logits_off, bytes;
+    size_t stats_off, logits_off, pmass_off, bytes;
 };
 static DraftWork draft_work(const dkv_drafter_t& m, int n_q_heads, int want_mass) {
     const size_t b = m.batch, D = m.head_dim;
     DraftWork w;
     w.stats_off = align256(sizeof(float) * b * n_q_heads * n_splits_of(&m, n_q_heads) * (D + 2));
     w.logits_off = align256(w.stats_off + sizeof(float) * b * n_q_heads * 2);
-    w.bytes = want_mass ? w.logits_off + sizeof(float) * b * n_q_heads * (size_t)m.cap : w.logits_off;
+    w.pmass_off = align256(w.logits_off + sizeof(float) * b * n_q_heads * (size_t)m.cap);
+    w.bytes = want_mass ? w.pmass_off + sizeof(float) * b * m.n_kv_heads * (size_t)m.cap : w.logits_off;
     return w;
 }
 
@@ -1051,6 +1337,32 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
     int unit = rps;     // rows per unit of work that owns a partial slot
     const int tslot = timing_slot();
+    // One block of 8 waves per (sequence, KV head) segment when the segments
+    // alone fill the chip: split-K, merge and the per-KV-head mass in one
+    // kernel (4-bit codes, D = 128, 4 query heads and 4 groups per KV head,
+    // fp16 meta)
+    if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0 && cfg.bits <= 4 &&
+        m.head_dim == 128 && G == 4 && m.head_dim / cfg.group == 4 && cfg.meta_f16 &&
+        dma_lpp(page_fmt(cfg, 128), 128) == 5 && m.batch * m.n_kv_heads >= 256) {
+        auto kfn = draft_attn_seg_kernel<1, 5>;
+        const size_t lds = (size_t)SEG_WAVES * dma_stages(5) * 5 * 1024;
+        static size_t lds_done[16] = {};
+        if (!reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))
+            return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS");
+        float* pmass = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.pmass_off) : nullptr;
+        if (g_time_splitk) hipEventRecord(g_splitk_ev[0][tslot], st);
+        hipLaunchKernelGGL(kfn, dim3(1, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), lds, st, m, layer, cfg, q,
+                           n_q_heads, scale, out, logits, pmass);
+        if (g_time_splitk) {
+            hipEventRecord(g_splitk_ev[1][tslot], st);
+            if (g_timed < TIMING_PAIRS) ++g_timed;
+        }
+        int rc = check_launch("dkv_drafter_attention(segment)");
+        if (rc || !want_mass) return rc;
+        hipLaunchKernelGGL(draft_mass_sum_kernel, dim3((m.cap + 255) / 256, m.batch), dim3(256), 0, st, m, layer,
+                           pmass);
+        return check_launch("dkv_drafter_attention(mass)");
+    }
     if (g_time_splitk) hipEventRecord(g_splitk_ev[0][tslot], st);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {

@@ -40,6 +40,7 @@ B, CTX, HKV, HQ, D, L = 32, 32768, 8, 32, 128, 2
 LAYER = 1                              # the layer under test (layer 0 holds other rows)
 INT4 = Cfg(4, 0.25, group=32, meta="f16")
 INT8 = Cfg(8, 1.0, group=64, meta="f16")
+INT4H = Cfg(4, 0.5, group=32, meta="f16")    # ~16k rows: 64 pages per wave of the segment kernel
 LENS = np.array([CTX - 1 - 37 * s for s in range(B)], np.int64)
 _POOL = cf.ThreadPoolExecutor(8)       # the numpy oracle per sequence (it releases the GIL)
 
@@ -151,11 +152,13 @@ def test_requantize_both_arms_and_switches_bit_exact(dev, cache):
     assert g0["pos"].tolist() == list(range(int(LENS[5])))
 
 
-@pytest.mark.parametrize("cfg", [INT4, INT8], ids=["int4g32f16keep0.25", "int8g64f16keep1"])
+@pytest.mark.parametrize("cfg", [INT4, INT8, INT4H], ids=["int4g32f16keep0.25", "int8g64f16keep1", "int4g32f16keep0.5"])
 def test_drafter_attention_and_mass_match_oracle(dev, cache, cfg):
     """One query row per sequence over the mirror built at the benchmark
     shape: every sequence's output within tolerance of the oracle's, and the
-    attention mass added to every kept row's score."""
+    attention mass added to every kept row's score. The int4 arms run the
+    segment kernel (one block per sequence and KV head); at keep 0.5 its waves
+    hold more pages than their logit registers and spill the rest."""
     full, host = cache
     md = _mirror([cfg] * L, [cfg])
     md.sync_from(full, 0)
