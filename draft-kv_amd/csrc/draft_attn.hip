@@ -177,6 +177,12 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr float kTwo24 = 16777216.0f;            // 2^24
 constexpr float kTwoM24 = 1.0f / 16777216.0f;    // 2^-24
 
+#ifndef DKV_X16
+#define DKV_X16 1
+#endif
+// element e of a 4-bit operand carries 16x its code when DKV_X16 and e & 2
+__host__ __device__ constexpr bool x16_elem(int CB, int e) { return DKV_X16 && CB == 4 && (e & 2); }
+
 // 8 codes of one word (cb 4) or two words (cb 8) -> 8 f16 subnormals
 // code * 2^-24 (the interleaved word order of mirror_layout.h puts two codes
 // in the low bits of the two halves)
@@ -185,10 +191,21 @@ __device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w) {
     uint4 r;
     if (CB == 4) {
         const uint32_t x = w[0];
+#if DKV_X16
+        // codes at bits 4-7 of a half are subnormals too, 16x the value:
+        // elements e = 2, 3, 6, 7 come out scaled by 16 (the other operand
+        // carries 1/16 there), one AND per pair instead of a shift and an AND
+        const uint32_t y = x >> 8;
+        r.x = x & 0x000F000Fu;
+        r.y = x & 0x00F000F0u;
+        r.z = y & 0x000F000Fu;
+        r.w = y & 0x00F000F0u;
+#else
         r.x = x & 0x000F000Fu;
         r.y = (x >> 4) & 0x000F000Fu;
         r.z = (x >> 8) & 0x000F000Fu;
         r.w = (x >> 12) & 0x000F000Fu;
+#endif
     } else {
         r.x = w[0] & 0x00FF00FFu;
         r.y = (w[0] >> 8) & 0x00FF00FFu;
@@ -354,12 +371,13 @@ struct SplitCore {
                 const float4 w4 = qv[(8 * st + e) / 4];
                 const float raw = (e % 4 == 0) ? w4.x : (e % 4 == 1) ? w4.y : (e % 4 == 2) ? w4.z : w4.w;
                 const uint32_t keep = (cvalid && d / group == gcol) ? 0xFFFFFFFFu : 0u;
-                const float v = __uint_as_float(__float_as_uint(raw) & keep);
+                float v = __uint_as_float(__float_as_uint(raw) & keep);
+                if (x16_elem(CB, e)) v *= 0.0625f;   // exact: the code operand carries the 16
                 const _Float16 hi = (_Float16)v;
                 const _Float16 lo = (_Float16)(v - (float)hi);
                 qhi[st][e] = hi;
                 qlo[st][e] = lo;
-                qsum += (float)hi + (float)lo;
+                qsum += x16_elem(CB, e) ? ((float)hi + (float)lo) * 16.0f : (float)hi + (float)lo;
             }
         qsum += __shfl_xor(qsum, 16);
         qsum += __shfl_xor(qsum, 32);
@@ -493,7 +511,7 @@ struct SplitCore {
                 sc = ok ? sc : 0.0f;
                 lo = ok ? lo : 0.0f;
             }
-            const float x = pv[e] * sc;            // p, sc >= 0
+            const float x = pv[e] * (x16_elem(CB, e) ? sc * 0.0625f : sc);   // p, sc >= 0
             bhi[e] = (_Float16)x;
             blo[e] = (_Float16)(x - (float)bhi[e]);   // exact difference, rounded once
             zs = fmaf(pv[e], lo, zs);
