@@ -193,6 +193,16 @@ def splitk_bytes(rows_per_seq, n_kv_heads, d, bits, group, q_heads):
     return float(sum(rows_per_seq)) * per_row + len(rows_per_seq) * q_heads * d * 4
 
 
+def segment_path(arm, batch, n_kv_heads, d, q_heads) -> bool:
+    """Whether dkv_drafter_attention runs the segment kernel for this arm and
+    shape (one 8-wave block per sequence and KV head: 4-bit codes, head_dim
+    128, 4 query heads and 4 groups per KV head, fp16 meta, batch x KV heads
+    >= 256); it then writes the output and the mass itself, so its
+    algorithmic bytes are the whole call's."""
+    return (arm.bits <= 4 and d == 128 and q_heads == 4 * n_kv_heads and d // arm.group == 4
+            and arm.scale_fp16 and batch * n_kv_heads >= 256)
+
+
 def time_verify(full, n_q_heads: int, T: int, reps: int = 2):
     """Verify attention timed on the run's own full cache: T N(0,1) query rows
     per sequence at its last T positions, every layer, ``reps`` times, one
@@ -242,7 +252,8 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
         for layer in range(L):
             r = rows[:, layer].astype(np.float64)
             cb += reps * drafter_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
-            kb += reps * splitk_bytes(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
+            kfn = drafter_bytes if segment_path(arm, b, comp.n_kv_heads, comp.d_head, n_q_heads) else splitk_bytes
+            kb += reps * kfn(r, comp.n_kv_heads, comp.d_head, arm.bits, arm.group, n_q_heads)
         # whole calls back to back, then the split-K kernel of each call
         # (again back to back: one event pair per call, summed at the end)
         t = EventTimer(comp, "attend")
@@ -561,9 +572,10 @@ def run_e2e(args):
             c[0] += nbytes
             c[1] += s_ev.elapsed_time(e_ev) * 1e3
             c[2] += 1
-    log("drafter attention and its split-K kernel timed on the run's mirror, under each arm")
+    log("drafter attention and its dominant kernel timed on the run's mirror, under each arm")
     timed = time_drafter(comp, full, arms, Hq)
     main_arm = arms[1]
+    seg = segment_path(main_arm, b, Hkv, D, Hq)
     mb, mus, mn = timed[main_arm]["call"]
     kbytes, kus, kn = timed[main_arm]["splitk"]
     achieved = kbytes / (kus * 1e-6) / 1e9
@@ -661,10 +673,12 @@ def run_e2e(args):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": "profiles/attention_hbm_traffic_b32_ctx32k.md (FETCH_SIZE x 2.0 + "
                                        "WRITE_SIZE, copy-kernel calibrated)" if traffic else None,
-                     "kernel": f"drafter attention split-K kernel, {main_arm.label()} g{main_arm.group} "
-                               "(the dominant kernel of dkv_drafter_attention)",
+                     "kernel": f"drafter attention {'segment' if seg else 'split-K'} kernel, "
+                               f"{main_arm.label()} g{main_arm.group} (the dominant kernel of "
+                               "dkv_drafter_attention)",
                      "bytes_per_launch": kbytes / max(kn, 1), "us_per_launch": kus / max(kn, 1), "launches": kn,
-                     "call": {"what": "split-K + combine + mass", "bytes_per_call": mb / max(mn, 1),
+                     "call": {"what": "segment kernel + mass sum" if seg else
+                              "split-K + combine + mass", "bytes_per_call": mb / max(mn, 1),
                               "us_per_call": mus / max(mn, 1), "GB/s": mb / (mus * 1e-6) / 1e9,
                               "frac": mb / (mus * 1e-6) / 1e9 / HBM_PEAK_GBS, "calls": mn}},
         "kernels": {"verify_attention": {"us_per_call": v_us, "bytes_per_call": v_bytes,
