@@ -117,13 +117,17 @@ __device__ __forceinline__ int quant_code(float x, GroupMeta m, int bits) {
 // quant_code of 8 values of one group without a division on the common path.
 // With inv = rcp(scale) (hardware reciprocal, within 1 ulp) the product
 // q = RN(d * inv) lies within 2^-22 |Q| of the exact quotient Q = d / scale
-// (d = RN(x - lo)), and RN(Q) within 2^-24 |Q| of Q. So when q is farther
-// than 2^-20 |q| from every half-integer, rint(q) == rint(RN(Q)); for the
-// values that are not (rare) the correctly rounded division decides, behind
-// a wave-uniform branch. Same codes as quant_code for every input.
+// (d = RN(x - lo)), and RN(Q) within 2^-24 |Q| of Q. So when |q| <= levels + 1
+// and q is farther than (levels + 1) 2^-20 from every half-integer,
+// rint(q) == rint(RN(Q)); past levels + 1 (or below -1) the clamp to
+// [0, levels] gives the same code whichever way either rounds. The values
+// within that distance of a half-integer (rare) take the correctly rounded
+// division, behind a wave-uniform branch. Same codes as quant_code for every
+// input.
 __device__ __forceinline__ void quant_codes8(const float (&v)[8], GroupMeta m, int bits, uint32_t (&code)[8]) {
 #pragma clang fp contract(off)
     const float levels = static_cast<float>((1 << bits) - 1);
+    const float tie = 0.5f - (levels + 1.0f) * 9.5367431640625e-07f;   // 0.5 - (levels + 1) 2^-20, exact
     const float inv = __builtin_amdgcn_rcpf(m.scale);
     const bool bad = !(inv >= 1.17549435e-38f && inv <= 3.0e38f);   // a reciprocal out of the normal range
     float r[8];
@@ -133,7 +137,7 @@ __device__ __forceinline__ void quant_codes8(const float (&v)[8], GroupMeta m, i
     for (int e = 0; e < 8; ++e) {
         const float q = __fmul_rn(__fsub_rn(v[e], m.lo), inv);
         r[e] = rintf(q);
-        near[e] = bad || fmaf(fabsf(q), 9.5367431640625e-07f, fabsf(__fsub_rn(q, r[e]))) >= 0.5f;   // 2^-20
+        near[e] = bad || fabsf(__fsub_rn(q, r[e])) >= tie;
         any = any || near[e];
     }
     if (__any(any)) {
@@ -142,7 +146,7 @@ __device__ __forceinline__ void quant_codes8(const float (&v)[8], GroupMeta m, i
             if (near[e]) r[e] = rintf(__fdiv_rn(__fsub_rn(v[e], m.lo), m.scale));
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) code[e] = static_cast<uint32_t>(fminf(fmaxf(r[e], 0.0f), levels));
+    for (int e = 0; e < 8; ++e) code[e] = static_cast<uint32_t>(__builtin_amdgcn_fmed3f(r[e], 0.0f, levels));
 }
 
 __device__ __forceinline__ float dequant(int code, GroupMeta m) {
