@@ -273,9 +273,19 @@ __device__ __forceinline__ float meta_lo(const uint32_t* w, int k) {
     return __uint_as_float(w[2 * k + 1]);
 }
 
-// Column offsets of group g within a 16-lane row (see the kernel): the
-// subgroup of lane XORs generated by 15, 7 and 3, in butterfly order.
-__constant__ int kColXor[8] = {0, 15, 7, 8, 3, 12, 4, 11};
+// an optional callback left out
+struct NoHook {
+    template <class... A>
+    __device__ __forceinline__ void operator()(A&&...) const {}
+};
+
+// Column offset of group g within a 16-lane row (see the kernel): the
+// subgroup of lane XORs generated by 15, 7 and 3, in butterfly order
+// {0, 15, 7, 8, 3, 12, 4, 11}. A function, so that an unrolled loop folds it
+// to immediates instead of loading a table.
+__device__ __forceinline__ constexpr int col_xor(int g) {
+    return (g & 1 ? 15 : 0) ^ (g & 2 ? 7 : 0) ^ (g & 4 ? 3 : 0);
+}
 
 template <bool B>
 using bool_c = std::integral_constant<bool, B>;
@@ -333,32 +343,48 @@ struct SplitCore {
 
     __device__ __forceinline__ void init(const float* __restrict__ q, int s, int h, int Hq, int G, int grp, int lane,
                                          float scale) {
+        init_at(q + ((int64_t)s * Hq + h * G) * D, G, grp, lane, scale);
+    }
+
+    // qh: the KV head's G query heads, [G][D] floats (global memory or LDS)
+    __device__ __forceinline__ void init_at(const float* __restrict__ qh, int G, int grp, int lane, float scale) {
+        init_lanes(G, grp, lane);
+        init_q(qh, scale);
+    }
+
+    // the lane's place: column, lane group, and the (group, head) its column holds
+    __device__ __forceinline__ void init_lanes(int G, int grp, int lane) {
         col = lane % 16;
         jj = lane / 16;
         group = grp;
         NG = D / grp;
-        // column col = hcol ^ kColXor[gcol]: the NG columns of a head form an
+        // column col = hcol ^ col_xor(gcol): the NG columns of a head form an
         // orbit of the lane involutions row_mirror (^15), row_half_mirror (^7)
         // and quad reverse (^3), so their sum is a butterfly of DPP adds that
         // leaves the bitwise-same total in every column of the head
         gcol = 0;
         hcol = 0;
         cvalid = false;
-        for (int g = 0; g < NG; ++g) {
-            const int hh = col ^ kColXor[g];
-            if (hh < G) {
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int hh = col ^ col_xor(g);
+            if (g < NG && hh < G) {
                 gcol = g;
                 hcol = hh;
                 cvalid = true;
             }
         }
         gmeta = min(gcol, NG - 1);
+    }
+
+    // Q^T of the lane's column in f16 hi + lo, and the column's q sum
+    __device__ __forceinline__ void init_q(const float* __restrict__ qh, float scale) {
         // Q^T columns (group, head) in f16 hi + lo, and the column's q sum: the
         // lane's DL channels as DL/4 vector loads, all in flight at once (hq is a
         // valid head for every lane); the group mask is a bit mask, so the loads
         // stay unconditional
-        const int hq = h * G + hcol;
-        const float4* qr = reinterpret_cast<const float4*>(q + ((int64_t)s * Hq + hq) * D + DL * jj);
+        const float4* qr = reinterpret_cast<const float4*>(qh + hcol * D + DL * jj);
+        const int d_lo = cvalid ? gcol * group : D, d_hi = d_lo + group;   // the column's group of channels
         float4 qv[DL / 4];
 #pragma unroll
         for (int x = 0; x < DL / 4; ++x) qv[x] = qr[x];
@@ -370,7 +396,7 @@ struct SplitCore {
                 const int d = DL * jj + 8 * st + e;
                 const float4 w4 = qv[(8 * st + e) / 4];
                 const float raw = (e % 4 == 0) ? w4.x : (e % 4 == 1) ? w4.y : (e % 4 == 2) ? w4.z : w4.w;
-                const uint32_t keep = (cvalid && d / group == gcol) ? 0xFFFFFFFFu : 0u;
+                const uint32_t keep = (d >= d_lo && d < d_hi) ? 0xFFFFFFFFu : 0u;
                 float v = __uint_as_float(__float_as_uint(raw) & keep);
                 if (x16_elem(CB, e)) v *= 0.0625f;   // exact: the code operand carries the 16
                 const _Float16 hi = (_Float16)v;
@@ -447,18 +473,23 @@ struct SplitCore {
     }
 
     // The rest of a page on its scores: scale, mask, hand over the logits,
-    // online softmax, PV.
-    template <bool TAIL, class Sink>
-    __device__ __forceinline__ void rest(const Regs& cur, const float (&sv)[8], int p0, int r_end, Sink&& sink) {
+    // online softmax, PV. The optional hooks: resc(alpha, p0) when the
+    // reference max moves (alpha = exp(old - new) per lane, before page p0's
+    // probabilities), post(pv, p0) with the page's probabilities exp(logit -
+    // reference).
+    template <bool TAIL, class Sink, class Resc = NoHook, class Post = NoHook>
+    __device__ __forceinline__ void rest(const Regs& cur, const float (&sv)[8], int p0, int r_end, Sink&& sink,
+                                         Resc&& resc = Resc{}, Post&& post = Post{}) {
         float pv[8];
-        rest_head<TAIL>(sv, p0, r_end, sink, pv);
-        rest_tail<TAIL>(cur, pv, p0, r_end);
+        rest_head<TAIL>(sv, p0, r_end, sink, pv, resc);
+        rest_tail<TAIL>(cur, pv, p0, r_end, post);
     }
 
     // scale, mask the tail, hand over the logits, the column max and the lazy
     // rescale; pv gets the scaled logits
-    template <bool TAIL, class Sink>
-    __device__ __forceinline__ void rest_head(const float (&sv)[8], int p0, int r_end, Sink&& sink, float (&pv)[8]) {
+    template <bool TAIL, class Sink, class Resc = NoHook>
+    __device__ __forceinline__ void rest_head(const float (&sv)[8], int p0, int r_end, Sink&& sink, float (&pv)[8],
+                                              Resc&& resc = Resc{}) {
         float mx = -INFINITY;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
@@ -480,17 +511,20 @@ struct SplitCore {
             zsum *= alpha;
 #pragma unroll
             for (int t = 0; t < NDT; ++t) acc[t] *= alpha;
+            resc(alpha, p0);
             m_run = m_new;
         }
     }
 
     // probabilities, row sums and the PV product of the page
-    template <bool TAIL>
-    __device__ __forceinline__ void rest_tail(const Regs& cur, float (&pv)[8], int p0, int r_end) {
+    template <bool TAIL, class Post = NoHook>
+    __device__ __forceinline__ void rest_tail(const Regs& cur, float (&pv)[8], int p0, int r_end,
+                                              Post&& post = Post{}) {
         // m_run is finite from the first page on (every split starts with a
         // live row), so masked rows give exp(-inf) = 0 with no test
 #pragma unroll
         for (int x = 0; x < 8; ++x) pv[x] = __expf(pv[x] - m_run);
+        post(pv, p0);
         float sum = pv[0];
 #pragma unroll
         for (int x = 1; x < 8; ++x) sum += pv[x];
@@ -976,9 +1010,19 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             for (int i = 0; i < LPP; ++i) dma16(pg, src[i], dst + i * 1024);
             slot_in = slot_in + SLOT == S * SLOT ? 0 : slot_in + SLOT;
         };
+        // the KV head's G x D floats of q (2 KB) go into the ring's last slot,
+        // which no page uses before the first step, ahead of the pages: the
+        // wait for q then leaves the pages in flight
+        char* qs = ring + (S - 1) * SLOT;
+        const float* qg = q + ((int64_t)s * Hq + h * G) * D;
+        static_assert(G * D * 4 == 2048 && S >= 2, "q takes two 1 KB loads into a free slot");
+        dma16(qg, lane * 16, lds_addr(qs));
+        dma16(qg, 1024 + lane * 16, lds_addr(qs) + 1024);
         for (int j = 0; j < S - 1; ++j)
             if (j < T) issue(j);
-        c.init(q, s, h, Hq, G, cfg.group, lane, scale);
+        c.init_lanes(G, cfg.group, lane);
+        vm_wait(LPP * min(S - 1, T));
+        c.init_q(reinterpret_cast<const float*>(qs), scale);
         c.reset();
         constexpr uint32_t mbase = (2 + NVL) * 1024;
         const uint32_t o_k = (c.col * 4 + c.jj) * 16;
@@ -1003,7 +1047,8 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             load_words(r.vm, reinterpret_cast<const uint8_t*>(sl + o_vm));
             slot_out = slot_out + SLOT == S * SLOT ? 0 : slot_out + SLOT;
         };
-        // a page's logits: the lane's two rows (x = gcol and gcol + 4 of its 8)
+        // a page's probabilities exp(logit - reference): the lane's two rows
+        // (x = gcol and gcol + 4 of its 8)
         const uint64_t g1 = __ballot((c.gcol & 1) != 0), g2 = __ballot((c.gcol & 2) != 0);
         float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
         auto stash = [&](const float (&pv)[8], int p0) {
@@ -1013,6 +1058,22 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             const int g = __builtin_amdgcn_readfirstlane(p0 / PAGE - pg0);
             if (g < SEG_TMAX) seg_put(2 * g, a, b);
             else *reinterpret_cast<float2*>(spill_w + (int64_t)g * (2 * WAVE)) = make_float2(a, b);
+        };
+        // the reference moved before page p0 (rare: a column's max grew by
+        // more than 6): the pages kept so far take the factor too
+        auto restash = [&](float alpha, int p0) {
+            if (!keep) return;
+            const int gc = __builtin_amdgcn_readfirstlane(p0 / PAGE - pg0);
+            for (int k = 0; k < min(gc, SEG_TMAX); ++k) {
+                float a, b;
+                seg_get(2 * k, a, b);
+                seg_put(2 * k, a * alpha, b * alpha);
+            }
+            for (int k = SEG_TMAX; k < gc; ++k) {
+                float2* pk = reinterpret_cast<float2*>(spill_w + (int64_t)k * (2 * WAVE));
+                const float2 v = *pk;
+                *pk = make_float2(v.x * alpha, v.y * alpha);
+            }
         };
         // the LDS-staged kernel's page pipeline, with the logits kept instead
         // of stored: the waits count loads only (spilled pages wait as if
@@ -1027,15 +1088,15 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             if (g + S - 1 < T) issue(g + S - 1);
             operands(nxt);
             float pv[8];
-            c.template rest_head<false>(scur, (pg0 + g) * PAGE, n, stash, pv);
+            c.template rest_head<false>(scur, (pg0 + g) * PAGE, n, NoHook{}, pv, restash);
             f32x4_t acc_next[2];
             c.qk_mfma(nxt, acc_next);
-            c.template rest_tail<false>(cur, pv, (pg0 + g) * PAGE, n);
+            c.template rest_tail<false>(cur, pv, (pg0 + g) * PAGE, n, stash);
             c.qk_fold(nxt, acc_next, snxt);
         };
         auto last = [&](int g, const Regs& cur, const float (&scur)[8]) {
-            if (tail) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, stash);
-            else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, stash);
+            if (tail) c.template rest<true>(cur, scur, (pg0 + g) * PAGE, n, NoHook{}, restash, stash);
+            else c.template rest<false>(cur, scur, (pg0 + g) * PAGE, n, NoHook{}, restash, stash);
         };
         int g = 0;
         for (; g + 2 < T; g += 2) {
@@ -1078,15 +1139,17 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
     __syncthreads();
     if (!active) return;
     // ---- mass: p = exp(logit - max) / sum per kept value, summed over the
-    // quad of the KV head's 4 query heads (lanes hcol 0..3 of a group column)
+    // quad of the KV head's 4 query heads (lanes hcol 0..3 of a group column);
+    // the kept values are exp(logit - the wave's reference), so p is a kept
+    // value times exp(reference - max) / sum
     {
-        const float mm = sst[2 * c.hcol], il = sst[2 * c.hcol + 1];
+        const float fac = __expf(c.m_run - sst[2 * c.hcol]) * sst[2 * c.hcol + 1];
         const uint64_t hb0 = __ballot((c.hcol & 1) != 0), hb1 = __ballot((c.hcol & 2) != 0);
         const int row2 = (c.hcol >> 1) * PAGE + (c.hcol & 1) * 16 + 4 * c.jj + c.gcol;   // row in the page pair
         float* pm = pmass + (int64_t)(s * Hkv + h) * m.cap + pg0 * PAGE + row2;
         const float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
         const int r_end = (pg0 + T) * PAGE <= n ? T * PAGE : n - pg0 * PAGE;   // the wave's live rows
-        // 8 pages at a time, so the reads, exps and quad sums of different
+        // 8 pages at a time, so the reads, products and quad sums of different
         // pages overlap
         constexpr int U = 8;
         for (int g0 = 0; g0 < T; g0 += U) {
@@ -1101,13 +1164,13 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                     a[k] = v.x;
                     b[k] = v.y;
                 } else {
-                    a[k] = b[k] = -INFINITY;
+                    a[k] = b[k] = 0.0f;
                 }
             }
 #pragma unroll
             for (int k = 0; k < U; ++k) {
-                a[k] = quad_sum(__expf(a[k] - mm) * il);
-                b[k] = quad_sum(__expf(b[k] - mm) * il);
+                a[k] = quad_sum(a[k] * fac);
+                b[k] = quad_sum(b[k] * fac);
             }
             // every lane of a quad holds both sums of its rows: lane hcol
             // writes page g0 + k + (hcol >> 1), half (hcol & 1), so one store
