@@ -568,9 +568,10 @@ struct SplitCore {
         zsum += __shfl_xor(zsum, 32);
         if (!cvalid) return;
         float* pp = part + (((int64_t)s * Hq + h * G + hcol) * n_splits + split) * (D + 2);
+        const int t_lo = gcol * (group / 16), t_hi = t_lo + group / 16;   // the tiles of the column's group
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-            if ((16 * t) / group != gcol) continue;   // this column's group covers tile t
+            if (t < t_lo || t >= t_hi) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) pp[16 * t + 4 * jj + r] = acc[t][r] * kTwo24 + zsum;
         }
@@ -934,6 +935,43 @@ __device__ __forceinline__ void seg_get(int i2, float& a, float& b) {
                  : "s"(i2)
                  : "m0");
 }
+// 8 pages: (a[k], b[k]) <- buffer registers v176 + i2 + 2k, v177 + i2 + 2k
+__device__ __forceinline__ void seg_get8(int i2, float (&a)[8], float (&b)[8]) {
+    asm volatile("s_set_gpr_idx_on %16, gpr_idx(SRC0)\n\t"
+                 "v_mov_b32 %0, v176\n\tv_mov_b32 %1, v177\n\tv_mov_b32 %2, v178\n\tv_mov_b32 %3, v179\n\t"
+                 "v_mov_b32 %4, v180\n\tv_mov_b32 %5, v181\n\tv_mov_b32 %6, v182\n\tv_mov_b32 %7, v183\n\t"
+                 "v_mov_b32 %8, v184\n\tv_mov_b32 %9, v185\n\tv_mov_b32 %10, v186\n\tv_mov_b32 %11, v187\n\t"
+                 "v_mov_b32 %12, v188\n\tv_mov_b32 %13, v189\n\tv_mov_b32 %14, v190\n\tv_mov_b32 %15, v191\n\t"
+                 "s_set_gpr_idx_off"
+                 : "=v"(a[0]), "=v"(b[0]), "=v"(a[1]), "=v"(b[1]), "=v"(a[2]), "=v"(b[2]), "=v"(a[3]), "=v"(b[3]),
+                   "=v"(a[4]), "=v"(b[4]), "=v"(a[5]), "=v"(b[5]), "=v"(a[6]), "=v"(b[6]), "=v"(a[7]), "=v"(b[7])
+                 : "s"(i2)
+                 : "m0");
+}
+
+// lane-quad sums (lanes 4k..4k+3) of 16 values, the bitwise-same total in
+// each lane: one fused v_add_f32_dpp per value and step (quad_perm [1,0,3,2]
+// then [2,3,0,1]); the s_nop covers the two wait states a DPP read needs
+// after a VALU write, and every later add reads a register written at least
+// two instructions before it.
+#define DKV_QADD16(CTRL)                                                                                         \
+    "v_add_f32_dpp %0, %0, %0 " CTRL " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %1, %1, %1 " CTRL           \
+    " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %2, %2, %2 " CTRL " row_mask:0xf bank_mask:0xf\n\t"            \
+    "v_add_f32_dpp %3, %3, %3 " CTRL " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %4, %4, %4 " CTRL           \
+    " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %5, %5, %5 " CTRL " row_mask:0xf bank_mask:0xf\n\t"            \
+    "v_add_f32_dpp %6, %6, %6 " CTRL " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %7, %7, %7 " CTRL           \
+    " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %8, %8, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"            \
+    "v_add_f32_dpp %9, %9, %9 " CTRL " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %10, %10, %10 " CTRL        \
+    " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %11, %11, %11 " CTRL " row_mask:0xf bank_mask:0xf\n\t"         \
+    "v_add_f32_dpp %12, %12, %12 " CTRL " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %13, %13, %13 " CTRL     \
+    " row_mask:0xf bank_mask:0xf\n\tv_add_f32_dpp %14, %14, %14 " CTRL " row_mask:0xf bank_mask:0xf\n\t"         \
+    "v_add_f32_dpp %15, %15, %15 " CTRL " row_mask:0xf bank_mask:0xf\n\t"
+__device__ __forceinline__ void quad_sum16(float (&a)[8], float (&b)[8]) {
+    asm volatile("s_nop 1\n\t" DKV_QADD16("quad_perm:[1,0,3,2]") DKV_QADD16("quad_perm:[2,3,0,1]")
+                 : "+v"(a[0]), "+v"(b[0]), "+v"(a[1]), "+v"(b[1]), "+v"(a[2]), "+v"(b[2]), "+v"(a[3]), "+v"(b[3]),
+                   "+v"(a[4]), "+v"(b[4]), "+v"(a[5]), "+v"(b[5]), "+v"(a[6]), "+v"(b[6]), "+v"(a[7]), "+v"(b[7]));
+}
+#undef DKV_QADD16
 #pragma clang diagnostic pop
 
 // t where the lane's bit of mask is set, else f (one v_cndmask_b32; written out
@@ -1129,7 +1167,7 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             l = fmaf(lc, wt, l);
             o = fmaf(ph[w * PD + d], wt, o);
         }
-        out[((int64_t)s * Hq + h * G + hl) * D + d] = (l > 0.0f) ? o / l : 0.0f;
+        __builtin_nontemporal_store((l > 0.0f) ? o / l : 0.0f, &out[((int64_t)s * Hq + h * G + hl) * D + d]);
         if (d == 0) {
             sst[2 * hl] = mm;
             sst[2 * hl + 1] = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1150,9 +1188,36 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
         const float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
         const int r_end = (pg0 + T) * PAGE <= n ? T * PAGE : n - pg0 * PAGE;   // the wave's live rows
         // 8 pages at a time, so the reads, products and quad sums of different
-        // pages overlap
+        // pages overlap. Every lane of a quad ends with both sums of its rows:
+        // lane hcol writes page g0 + k + (hcol >> 1), half (hcol & 1), so one
+        // store covers two pages (64 rows, 256 contiguous bytes); non-temporal,
+        // as the output's (written once, read once by the mass sum: measured
+        // 1 us faster per call at b=32 ctx 32k)
         constexpr int U = 8;
-        for (int g0 = 0; g0 < T; g0 += U) {
+        auto emit = [&](int g0, float (&a)[U], float (&b)[U], bool whole) {
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                a[k] *= fac;
+                b[k] *= fac;
+            }
+            quad_sum16(a, b);
+#pragma unroll
+            for (int k = 0; k < U; k += 2) {
+                const float lo = lane_select(a[k], b[k], hb0), hi = lane_select(a[k + 1], b[k + 1], hb0);
+                const float v = lane_select(lo, hi, hb1);
+                if (whole || (g0 + k) * PAGE + row2 < r_end) __builtin_nontemporal_store(v, &pm[(g0 + k) * PAGE]);
+            }
+        };
+        // whole chunks in registers: one indexed read of 16 registers, and
+        // with every row of the chunk live, no row test
+        const int Tr = min(T, SEG_TMAX);
+        int g0 = 0;
+        for (; g0 + U <= Tr; g0 += U) {
+            float a[U], b[U];
+            seg_get8(2 * g0, a, b);
+            emit(g0, a, b, (g0 + U) * PAGE <= r_end);
+        }
+        for (; g0 < T; g0 += U) {
             float a[U], b[U];
 #pragma unroll
             for (int k = 0; k < U; ++k) {
@@ -1167,21 +1232,7 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                     a[k] = b[k] = 0.0f;
                 }
             }
-#pragma unroll
-            for (int k = 0; k < U; ++k) {
-                a[k] = quad_sum(a[k] * fac);
-                b[k] = quad_sum(b[k] * fac);
-            }
-            // every lane of a quad holds both sums of its rows: lane hcol
-            // writes page g0 + k + (hcol >> 1), half (hcol & 1), so one store
-            // covers two pages (64 rows, 256 contiguous bytes)
-#pragma unroll
-            for (int k = 0; k < U; k += 2) {
-                const float lo = lane_select(a[k], b[k], hb0), hi = lane_select(a[k + 1], b[k + 1], hb0);
-                const float v = lane_select(lo, hi, hb1);
-                const int r = (g0 + k) * PAGE + row2;
-                if (r < r_end) pm[(g0 + k) * PAGE] = v;
-            }
+            emit(g0, a, b, false);
         }
     }
 }
@@ -1342,7 +1393,10 @@ static DraftWork draft_work(const dkv_drafter_t& m, int n_q_heads, int want_mass
 
 // Measurement hook: when on, dkv_drafter_attention records a pair of HIP
 // events around its split-K kernel on the launch stream, into the next of
-// TIMING_PAIRS slots (the last slot is reused once they run out).
+// TIMING_PAIRS slots (the last slot is reused once they run out). The events
+// skip the system-scope fence: they only order device work on the stream,
+// and the fence alone adds ~1.7 us to every timed launch (and slows the
+// launches around it).
 constexpr int TIMING_PAIRS = 1024;
 static bool g_time_splitk = false;
 static int g_timed = 0;   // pairs recorded since timing was switched on
@@ -1353,7 +1407,8 @@ static int timing_slot() { return g_timed < TIMING_PAIRS ? g_timed : TIMING_PAIR
 extern "C" int dkv_drafter_kernel_timing(int32_t on) {
     if (on && !g_splitk_ev[0][0]) {
         for (int i = 0; i < TIMING_PAIRS; ++i)
-            if (hipEventCreate(&g_splitk_ev[0][i]) != hipSuccess || hipEventCreate(&g_splitk_ev[1][i]) != hipSuccess)
+            if (hipEventCreateWithFlags(&g_splitk_ev[0][i], hipEventDisableSystemFence) != hipSuccess ||
+                hipEventCreateWithFlags(&g_splitk_ev[1][i], hipEventDisableSystemFence) != hipSuccess)
                 return fail(DKV_ELAUNCH, "dkv_drafter_kernel_timing: cannot create events");
     }
     if (on) g_timed = 0;

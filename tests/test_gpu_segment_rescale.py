@@ -1,0 +1,104 @@
+"""The drafter's int4 segment kernel (one block per sequence and KV head, its
+waves keeping each kept row's probability in registers until the block's
+softmax is final) on logits that keep growing along the sequence, so that
+the running maximum of every wave moves many times: each move rescales the
+probabilities kept so far, in registers and, past the register budget, in
+the spill buffer.
+
+Shape: the Llama-3-8B attention heads (32 query heads, 8 KV heads,
+head_dim 128), batch 32, ~12k rows per sequence kept in full (int4, group
+32, fp16 meta): 375 pages per (sequence, KV head), so the older waves hold
+58 pages, 18 of them spilled. Channel 5 of every key carries a ramp that
+the queries weight heavily: the logits climb ~400 along a sequence, ~60
+across an older wave's run, about ten moves of its maximum.
+
+Attention: 2e-3 relative / 1e-3 absolute against the float32 oracle;
+attention mass: 5e-4 relative / 1e-7 absolute. The top rows' logits reach
+~360 here, and float32 logits of that size carry ~1e-4 of absolute error on
+either side (the kernel's two-f16 query split keeps ~22 bits, the oracle
+rounds its float32 products), which moves their probabilities by as much
+relative -- at the benchmark's logit sizes the mass bound is 1e-4.
+"""
+
+import concurrent.futures as cf
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import attend, row_mass
+from oracle.config import Cfg
+from oracle.quant import quantize_codes
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 2e-3, 1e-3
+MASS_RTOL = 5e-4
+B, CTX, HKV, HQ, D = 32, 12000, 8, 32, 128
+ARM = Cfg(4, 1.0, group=32, meta="f16")
+LENS = np.array([CTX - 37 * s for s in range(B)], np.int64)
+_POOL = cf.ThreadPoolExecutor(8)
+
+
+@pytest.fixture(scope="module")
+def ramp(dev):
+    """A one-layer bf16 paged cache: N(0,1) K/V, with K channel 5 = 566 t/T
+    at row t. Returns the device cache and the host copy (bf16)."""
+    import draftkv
+    maxt = CTX + 64
+    full = draftkv.PagedKVCache(1, HKV, D, 16, maxt // 16, "bf16", batch=B, max_tokens=maxt)
+    full.reserve(LENS)
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    cnt = torch.tensor(LENS, dtype=torch.int32, device=dev)
+    st0 = torch.zeros(B, dtype=torch.int32, device=dev)
+    k = torch.randn((B, CTX, HKV, D), generator=g, device=dev, dtype=torch.float32)
+    k[..., 5] = (566.0 / CTX) * torch.arange(CTX, device=dev, dtype=torch.float32)[None, :, None]
+    k = k.bfloat16()
+    v = torch.randn((B, CTX, HKV, D), generator=g, device=dev, dtype=torch.float32).bfloat16()
+    full.append_layer(0, k, v, st0, cnt)
+    full.commit(LENS)
+    host = (k.cpu(), v.cpu())
+    del k, v
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    yield full, host
+    del full
+    torch.cuda.empty_cache()
+
+
+def test_segment_kernel_rescales_kept_probabilities(dev, ramp):
+    """Output and mass of every sequence match the oracle although every
+    wave's reference maximum moves again and again, also after its spill
+    point."""
+    import draftkv
+    full, host = ramp
+    md = draftkv.CompressedKVCache(1, [draftkv.CompressionConfig(4, 1.0, group=32, scale_fp16=True)],
+                                   batch=B, cap=CTX + 64)
+    md.sync_from(full, 0)
+    rng = np.random.default_rng(22)
+    q = rng.standard_normal((B, HQ, D)).astype(np.float32)
+    q[:, :, 5] = 8.0
+    out = md.attend(0, torch.from_numpy(q).to(dev), want_mass=True).cpu().numpy()
+    gs = {s: md.read_codes(0, s) for s in range(B)}
+    scale = 1.0 / np.sqrt(D)
+
+    def one(s):
+        n = int(LENS[s])
+        g = gs[s]
+        assert g["pos"].tolist() == list(range(n))
+        kr = host[0][s, :n].float().numpy()
+        vr = host[1][s, :n].float().numpy()
+        kq = quantize_codes(kr, ARM.bits, ARM.group, ARM.meta)
+        vq = quantize_codes(vr, ARM.bits, ARM.group, ARM.meta)
+        # the test's premise: the logits climb by far more than the kernel's
+        # rescale threshold within every wave's run of pages
+        lg = np.einsum("hd,khd->hk", q[s][::HQ // HKV], kq[3]) * scale
+        assert lg[:, -32:].max() - lg[:, :32].max() > 300.0
+        ref, _, mp = attend(q[s][None], kq[3], vq[3], np.arange(n), np.array([n]), HQ // HKV)
+        np.testing.assert_allclose(out[s], ref[0], rtol=RTOL, atol=ATOL, err_msg=f"seq {s}")
+        np.testing.assert_allclose(g["score"], row_mass(mp).astype(np.float64), rtol=MASS_RTOL, atol=1e-7,
+                                   err_msg=f"seq {s} mass")
+        return s
+
+    assert sorted(_POOL.map(one, range(B))) == list(range(B))
