@@ -935,17 +935,20 @@ __device__ __forceinline__ void seg_get(int i2, float& a, float& b) {
                  : "s"(i2)
                  : "m0");
 }
-// 8 pages: (a[k], b[k]) <- buffer registers v176 + i2 + 2k, v177 + i2 + 2k
-__device__ __forceinline__ void seg_get8(int i2, float (&a)[8], float (&b)[8]) {
+// 8 pages scaled: (a[k], b[k]) <- f * buffer registers v176 + i2 + 2k,
+// v177 + i2 + 2k (the index applies to the products' first operand only)
+__device__ __forceinline__ void seg_get8_mul(int i2, float f, float (&a)[8], float (&b)[8]) {
     asm volatile("s_set_gpr_idx_on %16, gpr_idx(SRC0)\n\t"
-                 "v_mov_b32 %0, v176\n\tv_mov_b32 %1, v177\n\tv_mov_b32 %2, v178\n\tv_mov_b32 %3, v179\n\t"
-                 "v_mov_b32 %4, v180\n\tv_mov_b32 %5, v181\n\tv_mov_b32 %6, v182\n\tv_mov_b32 %7, v183\n\t"
-                 "v_mov_b32 %8, v184\n\tv_mov_b32 %9, v185\n\tv_mov_b32 %10, v186\n\tv_mov_b32 %11, v187\n\t"
-                 "v_mov_b32 %12, v188\n\tv_mov_b32 %13, v189\n\tv_mov_b32 %14, v190\n\tv_mov_b32 %15, v191\n\t"
+                 "v_mul_f32 %0, v176, %17\n\tv_mul_f32 %1, v177, %17\n\tv_mul_f32 %2, v178, %17\n\t"
+                 "v_mul_f32 %3, v179, %17\n\tv_mul_f32 %4, v180, %17\n\tv_mul_f32 %5, v181, %17\n\t"
+                 "v_mul_f32 %6, v182, %17\n\tv_mul_f32 %7, v183, %17\n\tv_mul_f32 %8, v184, %17\n\t"
+                 "v_mul_f32 %9, v185, %17\n\tv_mul_f32 %10, v186, %17\n\tv_mul_f32 %11, v187, %17\n\t"
+                 "v_mul_f32 %12, v188, %17\n\tv_mul_f32 %13, v189, %17\n\tv_mul_f32 %14, v190, %17\n\t"
+                 "v_mul_f32 %15, v191, %17\n\t"
                  "s_set_gpr_idx_off"
                  : "=v"(a[0]), "=v"(b[0]), "=v"(a[1]), "=v"(b[1]), "=v"(a[2]), "=v"(b[2]), "=v"(a[3]), "=v"(b[3]),
                    "=v"(a[4]), "=v"(b[4]), "=v"(a[5]), "=v"(b[5]), "=v"(a[6]), "=v"(b[6]), "=v"(a[7]), "=v"(b[7])
-                 : "s"(i2)
+                 : "s"(i2), "v"(f)
                  : "m0");
 }
 
@@ -1153,15 +1156,26 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
     __syncthreads();
     float* sp = reinterpret_cast<float*>(dma_smem);
     float* sst = sp + G * SEG_WAVES * PD;
-    if (active) c.finish(sp, 0, 0, G, G, SEG_WAVES, wave);
+    if (active) {
+        c.finish(sp, 0, 0, G, G, SEG_WAVES, wave);
+    } else {
+        // a wave without pages (segments under 8 pages): a neutral partial
+        // (max -inf, sum 0, zeros), so the merge runs over every wave
+        for (int i = lane; i < G * PD; i += WAVE)
+            sp[((i / PD) * SEG_WAVES + wave) * PD + i % PD] = (i % PD == D) ? -INFINITY : 0.0f;
+    }
     __syncthreads();
     {
+        // all the waves' loads at once (the loops unroll), then the sums in
+        // wave order
         const int hl = threadIdx.x / D, d = threadIdx.x % D;   // 512 threads = G x D outputs
         const float* ph = sp + hl * SEG_WAVES * PD;
         float mm = -INFINITY;
-        for (int w = 0; w < A; ++w) mm = fmaxf(mm, ph[w * PD + D]);
+#pragma unroll
+        for (int w = 0; w < SEG_WAVES; ++w) mm = fmaxf(mm, ph[w * PD + D]);
         float l = 0.0f, o = 0.0f;
-        for (int w = 0; w < A; ++w) {
+#pragma unroll
+        for (int w = 0; w < SEG_WAVES; ++w) {
             const float mc = ph[w * PD + D], lc = ph[w * PD + D + 1];
             const float wt = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
             l = fmaf(lc, wt, l);
@@ -1195,11 +1209,6 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
         // 1 us faster per call at b=32 ctx 32k)
         constexpr int U = 8;
         auto emit = [&](int g0, float (&a)[U], float (&b)[U], bool whole) {
-#pragma unroll
-            for (int k = 0; k < U; ++k) {
-                a[k] *= fac;
-                b[k] *= fac;
-            }
             quad_sum16(a, b);
 #pragma unroll
             for (int k = 0; k < U; k += 2) {
@@ -1208,13 +1217,13 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                 if (whole || (g0 + k) * PAGE + row2 < r_end) __builtin_nontemporal_store(v, &pm[(g0 + k) * PAGE]);
             }
         };
-        // whole chunks in registers: one indexed read of 16 registers, and
+        // whole chunks in registers: 16 products with indexed operands, and
         // with every row of the chunk live, no row test
         const int Tr = min(T, SEG_TMAX);
         int g0 = 0;
         for (; g0 + U <= Tr; g0 += U) {
             float a[U], b[U];
-            seg_get8(2 * g0, a, b);
+            seg_get8_mul(2 * g0, fac, a, b);
             emit(g0, a, b, (g0 + U) * PAGE <= r_end);
         }
         for (; g0 < T; g0 += U) {
@@ -1231,6 +1240,8 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                 } else {
                     a[k] = b[k] = 0.0f;
                 }
+                a[k] *= fac;
+                b[k] *= fac;
             }
             emit(g0, a, b, false);
         }
