@@ -28,6 +28,8 @@
 // The accumulator lanes of the QK product already hold the 8 rows of one
 // column that the PV B operand needs, so probabilities never move between
 // lanes; the V page layout (mirror_layout.h) is the PV A operand.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "mirror_layout.h"
@@ -1415,6 +1417,20 @@ static hipEvent_t g_splitk_ev[2][TIMING_PAIRS] = {};
 
 static int timing_slot() { return g_timed < TIMING_PAIRS ? g_timed : TIMING_PAIRS - 1; }
 
+// Launch the split-K kernel, timed when the hook is on: the events ride on
+// the kernel's own dispatch (hipExtLaunchKernel), so they bracket its
+// execution without marker packets of their own around it.
+template <typename... KArgs, typename... Args>
+static void launch_splitk(void (*kfn)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+    if (g_time_splitk) {
+        const int i = timing_slot();
+        hipExtLaunchKernelGGL(kfn, grid, block, (uint32_t)lds, st, g_splitk_ev[0][i], g_splitk_ev[1][i], 0, args...);
+        if (g_timed < TIMING_PAIRS) ++g_timed;
+    } else {
+        hipLaunchKernelGGL(kfn, grid, block, lds, st, args...);
+    }
+}
+
 extern "C" int dkv_drafter_kernel_timing(int32_t on) {
     if (on && !g_splitk_ev[0][0]) {
         for (int i = 0; i < TIMING_PAIRS; ++i)
@@ -1483,7 +1499,6 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     hipStream_t st = as_stream(stream);
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
     int unit = rps;     // rows per unit of work that owns a partial slot
-    const int tslot = timing_slot();
     // One block of 8 waves per (sequence, KV head) segment when the segments
     // alone fill the chip: split-K, merge and the per-KV-head mass in one
     // kernel (4-bit codes, D = 128, 4 query heads and 4 groups per KV head,
@@ -1497,20 +1512,14 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         if (!reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))
             return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS");
         float* pmass = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.pmass_off) : nullptr;
-        if (g_time_splitk) hipEventRecord(g_splitk_ev[0][tslot], st);
-        hipLaunchKernelGGL(kfn, dim3(1, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), lds, st, m, layer, cfg, q,
-                           n_q_heads, scale, out, logits, pmass);
-        if (g_time_splitk) {
-            hipEventRecord(g_splitk_ev[1][tslot], st);
-            if (g_timed < TIMING_PAIRS) ++g_timed;
-        }
+        launch_splitk(kfn, dim3(1, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), lds, st, m, (int)layer, cfg, q,
+                      (int)n_q_heads, scale, out, logits, pmass);
         int rc = check_launch("dkv_drafter_attention(segment)");
         if (rc || !want_mass) return rc;
         hipLaunchKernelGGL(draft_mass_sum_kernel, dim3((m.cap + 255) / 256, m.batch), dim3(256), 0, st, m, layer,
                            pmass);
         return check_launch("dkv_drafter_attention(mass)");
     }
-    if (g_time_splitk) hipEventRecord(g_splitk_ev[0][tslot], st);
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
         // blocks of 4 waves; each wave walks splits blockIdx.x*4 + wave, +
@@ -1537,8 +1546,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         static size_t lds_done[16] = {};                                                                         \
         if (!reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))                                      \
             return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS"); \
-        hipLaunchKernelGGL(kfn, grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, scale, rps, ns, part,      \
-                           logits);                                                                               \
+        launch_splitk(kfn, grid, dim3(256), lds, st, m, (int)layer, cfg, q, (int)n_q_heads, scale, rps, ns, part, \
+                      logits);                                                                                    \
     } while (0)
 #define DKV_DMA2(MM, LP)              \
     do {                              \
@@ -1562,9 +1571,9 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         } else {
             const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
             const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + 8 * WAVE);
-#define DKV_LAUNCH(DD, CC, MM)                                                                                      \
-    hipLaunchKernelGGL((draft_attn_mfma_kernel<DD, CC, MM>), grid, dim3(256), lds, st, m, layer, cfg, q, n_q_heads, \
-                       scale, rps, ns, part, logits)
+#define DKV_LAUNCH(DD, CC, MM)                                                                                 \
+    launch_splitk(draft_attn_mfma_kernel<DD, CC, MM>, grid, dim3(256), lds, st, m, (int)layer, cfg, q,          \
+                  (int)n_q_heads, scale, rps, ns, part, logits)
             switch (key) {
                 case 0: DKV_LAUNCH(64, 4, 0); break;
                 case 1: DKV_LAUNCH(64, 4, 1); break;
@@ -1576,12 +1585,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
 #undef DKV_LAUNCH
         }
     } else {
-        hipLaunchKernelGGL(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st,
-                           m, layer, cfg, q, n_q_heads, scale, rps, ns, part, logits);
-    }
-    if (g_time_splitk) {
-        hipEventRecord(g_splitk_ev[1][tslot], st);
-        if (g_timed < TIMING_PAIRS) ++g_timed;
+        launch_splitk(draft_attn_kernel, dim3(ns, m.n_kv_heads, m.batch), dim3(256), smem_bytes(m.head_dim), st, m,
+                      (int)layer, cfg, q, (int)n_q_heads, scale, rps, ns, part, logits);
     }
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
