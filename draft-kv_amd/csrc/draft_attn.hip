@@ -1251,17 +1251,43 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
 }
 
 // score[row] += sum over KV heads of the per-KV-head masses of the segment
-// kernel (KV heads in order)
+// kernel (KV heads in order), 4 rows per thread: float4 reads of the masses,
+// double2 read-modify-writes of the scores
+constexpr int MSUM_ROWS = 4;
 __global__ void __launch_bounds__(256) draft_mass_sum_kernel(dkv_drafter_t m, int layer,
                                                              const float* __restrict__ pmass) {
     const int s = blockIdx.y;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = (blockIdx.x * blockDim.x + threadIdx.x) * MSUM_ROWS;
     if (r >= n) return;
     const float* p = pmass + (int64_t)s * m.n_kv_heads * m.cap + r;
-    float t = p[0];
-    for (int hk = 1; hk < m.n_kv_heads; ++hk) t += p[(int64_t)hk * m.cap];
-    m.score[row_index(m, s, layer) + r] += static_cast<double>(t);
+    double* sc = m.score + row_index(m, s, layer) + r;
+    // (cap and r are multiples of 4, so p and sc are 16-byte aligned when
+    // the workspace and the scores are)
+    if (r + MSUM_ROWS <= n && ((reinterpret_cast<uintptr_t>(sc) | reinterpret_cast<uintptr_t>(p)) & 15) == 0) {
+        float4 t = *reinterpret_cast<const float4*>(p);
+        for (int hk = 1; hk < m.n_kv_heads; ++hk) {
+            const float4 v = *reinterpret_cast<const float4*>(p + (int64_t)hk * m.cap);
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+        }
+        double2* d2 = reinterpret_cast<double2*>(sc);
+        double2 a = d2[0], b = d2[1];
+        a.x += static_cast<double>(t.x);
+        a.y += static_cast<double>(t.y);
+        b.x += static_cast<double>(t.z);
+        b.y += static_cast<double>(t.w);
+        d2[0] = a;
+        d2[1] = b;
+        return;
+    }
+    for (int k = 0; k < MSUM_ROWS && r + k < n; ++k) {
+        float t = p[k];
+        for (int hk = 1; hk < m.n_kv_heads; ++hk) t += p[(int64_t)hk * m.cap + k];
+        sc[k] += static_cast<double>(t);
+    }
 }
 
 // ---------------------------------------------------------------- combine + mass
@@ -1516,8 +1542,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
                       (int)n_q_heads, scale, out, logits, pmass);
         int rc = check_launch("dkv_drafter_attention(segment)");
         if (rc || !want_mass) return rc;
-        hipLaunchKernelGGL(draft_mass_sum_kernel, dim3((m.cap + 255) / 256, m.batch), dim3(256), 0, st, m, layer,
-                           pmass);
+        hipLaunchKernelGGL(draft_mass_sum_kernel, dim3((m.cap + 256 * MSUM_ROWS - 1) / (256 * MSUM_ROWS), m.batch),
+                           dim3(256), 0, st, m, layer, pmass);
         return check_launch("dkv_drafter_attention(mass)");
     }
     // the fast path reads q rows with 16-byte vector loads
