@@ -938,7 +938,8 @@ __device__ __forceinline__ void seg_get(int i2, float& a, float& b) {
                  : "m0");
 }
 // 8 pages scaled: (a[k], b[k]) <- f * buffer registers v176 + i2 + 2k,
-// v177 + i2 + 2k (the index applies to the products' first operand only)
+// v177 + i2 + 2k (the index applies to the products' first operand only;
+// the outputs are early-clobber, as f is read after the first is written)
 __device__ __forceinline__ void seg_get8_mul(int i2, float f, float (&a)[8], float (&b)[8]) {
     asm volatile("s_set_gpr_idx_on %16, gpr_idx(SRC0)\n\t"
                  "v_mul_f32 %0, v176, %17\n\tv_mul_f32 %1, v177, %17\n\tv_mul_f32 %2, v178, %17\n\t"
@@ -948,8 +949,9 @@ __device__ __forceinline__ void seg_get8_mul(int i2, float f, float (&a)[8], flo
                  "v_mul_f32 %12, v188, %17\n\tv_mul_f32 %13, v189, %17\n\tv_mul_f32 %14, v190, %17\n\t"
                  "v_mul_f32 %15, v191, %17\n\t"
                  "s_set_gpr_idx_off"
-                 : "=v"(a[0]), "=v"(b[0]), "=v"(a[1]), "=v"(b[1]), "=v"(a[2]), "=v"(b[2]), "=v"(a[3]), "=v"(b[3]),
-                   "=v"(a[4]), "=v"(b[4]), "=v"(a[5]), "=v"(b[5]), "=v"(a[6]), "=v"(b[6]), "=v"(a[7]), "=v"(b[7])
+                 : "=&v"(a[0]), "=&v"(b[0]), "=&v"(a[1]), "=&v"(b[1]), "=&v"(a[2]), "=&v"(b[2]), "=&v"(a[3]),
+                   "=&v"(b[3]), "=&v"(a[4]), "=&v"(b[4]), "=&v"(a[5]), "=&v"(b[5]), "=&v"(a[6]), "=&v"(b[6]),
+                   "=&v"(a[7]), "=&v"(b[7])
                  : "s"(i2), "v"(f)
                  : "m0");
 }
@@ -984,6 +986,14 @@ __device__ __forceinline__ void quad_sum16(float (&a)[8], float (&b)[8]) {
 __device__ __forceinline__ float lane_select(float f, float t, uint64_t mask) {
     float r;
     asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(mask));
+    return r;
+}
+// the same on operands that may come straight from a transcendental (v_exp):
+// a VALU read of its result needs one wait state, which the compiler inserts
+// before its own instructions but not before inline asm
+__device__ __forceinline__ float lane_select_tr(float f, float t, uint64_t mask) {
+    float r;
+    asm("s_nop 0\n\tv_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(mask));
     return r;
 }
 
@@ -1096,8 +1106,8 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
         float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
         auto stash = [&](const float (&pv)[8], int p0) {
             if (!keep) return;
-            const float a = lane_select(lane_select(pv[0], pv[1], g1), lane_select(pv[2], pv[3], g1), g2);
-            const float b = lane_select(lane_select(pv[4], pv[5], g1), lane_select(pv[6], pv[7], g1), g2);
+            const float a = lane_select(lane_select_tr(pv[0], pv[1], g1), lane_select_tr(pv[2], pv[3], g1), g2);
+            const float b = lane_select(lane_select_tr(pv[4], pv[5], g1), lane_select_tr(pv[6], pv[7], g1), g2);
             const int g = __builtin_amdgcn_readfirstlane(p0 / PAGE - pg0);
             if (g < SEG_TMAX) seg_put(2 * g, a, b);
             else *reinterpret_cast<float2*>(spill_w + (int64_t)g * (2 * WAVE)) = make_float2(a, b);
