@@ -169,8 +169,9 @@ int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer, dkv_qcfg_t
                           void* work, size_t work_bytes, dkv_stream_t stream);
 
 /* Measurement hook (no counterpart in the reference; for benchmarks that
- * time the dominant kernel alone): when on, dkv_drafter_attention records
- * a pair of HIP events around its split-K kernel on its launch stream, one
+ * time the dominant kernel alone): when on, dkv_drafter_attention times
+ * its split-K (or segment) kernel with a pair of HIP events carried by that
+ * kernel's own launch (hipExtLaunchKernel) on its launch stream, one
  * pair per call for the first 1024 calls after switching on (later calls
  * reuse the last pair). dkv_drafter_kernel_last_ms waits for the last pair
  * and returns its elapsed milliseconds (-1 when there is none);
