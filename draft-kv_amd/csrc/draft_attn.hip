@@ -893,22 +893,24 @@ __global__ void __launch_bounds__(256, 2) draft_attn_dma_kernel(dkv_drafter_t m,
 // ---- segment kernel (4-bit codes, D = 128, 4 query heads x 4 groups per KV
 // head): one block of 8 waves per (sequence, KV head) segment, used when the
 // segments alone fill the chip (batch x KV heads >= 256). The waves stream
-// their pages as the LDS-staged kernel does, but keep each page's logits in
-// registers instead of writing them to the workspace (33.5 MB of scattered
-// writes at b=32 ctx 32k cost the split-K pass a quarter of its time, mixed
-// into the read stream). After a block barrier the 8 partials meet in LDS --
-// the combine kernel's merge, in its order -- and each lane turns its logits
-// into probabilities with the final max and sum, summed over the KV head's 4
-// query heads across a lane quad: one float per row and KV head goes out, and
-// draft_mass_sum_kernel adds the KV heads' sums to the row scores.
+// their pages as the LDS-staged kernel does, but keep each page's
+// probabilities in registers instead of writing logits to the workspace
+// (33.5 MB of scattered writes at b=32 ctx 32k cost the split-K pass a
+// quarter of its time, mixed into the read stream). After a block barrier
+// the 8 partials meet in LDS -- the combine kernel's merge, in its order --
+// and each lane scales its kept probabilities to the final max and sum and
+// sums them over the KV head's 4 query heads across a lane quad: one float
+// per row and KV head goes out, and draft_mass_sum_kernel adds the KV heads'
+// sums to the row scores.
 //
-// The logits buffer: lane (gcol, hcol, jj) keeps rows 4jj+gcol and
+// The kept values: lane (gcol, hcol, jj) keeps rows 4jj+gcol and
 // 16+4jj+gcol of head hcol (the 4 group columns of a head hold the same 8
-// rows and share them out), two floats per page, in VGPRs above the
-// compiler's allocation (amdgpu_num_vgpr caps it at SEG_VGPRS; the clobber of
-// v255 sizes the wave's allocation to 256), written and read with
-// s_set_gpr_idx at a wave-uniform index. Pages past SEG_TMAX spill to the
-// workspace.
+// rows and share them out), two floats per page, exp(logit - the wave's
+// running reference), rescaled with the accumulator when the reference
+// moves. They sit in VGPRs above the compiler's allocation (amdgpu_num_vgpr
+// caps it at SEG_VGPRS; the clobber of v255 sizes the wave's allocation to
+// 256), written and read with s_set_gpr_idx at a wave-uniform index. Pages
+// past SEG_TMAX spill to the workspace.
 constexpr int SEG_WAVES = 8;
 constexpr int SEG_VGPRS = 176;                  // the compiler's registers
 constexpr int SEG_TMAX = (256 - SEG_VGPRS) / 2;  // pages per wave kept in registers
@@ -995,13 +997,6 @@ __device__ __forceinline__ float lane_select_tr(float f, float t, uint64_t mask)
     float r;
     asm("s_nop 0\n\tv_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(mask));
     return r;
-}
-
-// lane-quad sum (lanes 4k..4k+3): the bitwise-same total in each lane
-__device__ __forceinline__ float quad_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
-    return v;
 }
 
 template <int MF, int LPP>
@@ -1128,9 +1123,10 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                 *pk = make_float2(v.x * alpha, v.y * alpha);
             }
         };
-        // the LDS-staged kernel's page pipeline, with the logits kept instead
-        // of stored: the waits count loads only (spilled pages wait as if
-        // they were not there; a spill store only makes a wait longer)
+        // the LDS-staged kernel's page pipeline, with the probabilities kept
+        // instead of logits stored: the waits count loads only (spilled pages
+        // wait as if they were not there; a spill store or a rescale's
+        // read-modify-write only makes a wait longer)
         Regs ra, rb;
         float sa_[8], sb_[8];
         vm_wait(LPP * min(S - 2, T - 1));
