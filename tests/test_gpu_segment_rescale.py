@@ -18,6 +18,10 @@ attention mass: 5e-4 relative / 1e-7 absolute. The top rows' logits reach
 either side (the kernel's two-f16 query split keeps ~22 bits, the oracle
 rounds its float32 products), which moves their probabilities by as much
 relative -- at the benchmark's logit sizes the mass bound is 1e-4.
+
+A second case runs the same shape on ragged sequences of 1 to 7777 rows, for
+the kernel's small cases: waves with no pages, the even page split under 64
+pages, one- and two-page waves and partial last pages (mass rtol 1e-4).
 """
 
 import concurrent.futures as cf
@@ -99,6 +103,65 @@ def test_segment_kernel_rescales_kept_probabilities(dev, ramp):
         np.testing.assert_allclose(out[s], ref[0], rtol=RTOL, atol=ATOL, err_msg=f"seq {s}")
         np.testing.assert_allclose(g["score"], row_mass(mp).astype(np.float64), rtol=MASS_RTOL, atol=1e-7,
                                    err_msg=f"seq {s} mass")
+        return s
+
+    assert sorted(_POOL.map(one, range(B))) == list(range(B))
+
+
+# ragged segments: the segment kernel's small cases
+SHORT = np.array([1, 2, 5, 31, 32, 33, 63, 64, 65, 100, 224, 255, 256, 257, 300, 511, 512, 513, 1000, 1023,
+                  1024, 1025, 2047, 2048, 2049, 2500, 3000, 4095, 4096, 5000, 6000, 7777], np.int64)
+
+
+@pytest.fixture(scope="module")
+def ragged(dev):
+    """A one-layer bf16 paged cache of N(0,1) K/V with one sequence length
+    per entry of SHORT (batch 32). Returns the device cache and the host copy."""
+    import draftkv
+    T = int(SHORT.max())
+    maxt = T + 64
+    full = draftkv.PagedKVCache(1, HKV, D, 16, maxt // 16 + 1, "bf16", batch=B, max_tokens=maxt)
+    full.reserve(SHORT)
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    cnt = torch.tensor(SHORT, dtype=torch.int32, device=dev)
+    st0 = torch.zeros(B, dtype=torch.int32, device=dev)
+    k = torch.randn((B, T, HKV, D), generator=g, device=dev, dtype=torch.float32).bfloat16()
+    v = torch.randn((B, T, HKV, D), generator=g, device=dev, dtype=torch.float32).bfloat16()
+    full.append_layer(0, k, v, st0, cnt)
+    full.commit(SHORT)
+    host = (k.cpu(), v.cpu())
+    del k, v
+    torch.cuda.synchronize()
+    yield full, host
+    del full
+    torch.cuda.empty_cache()
+
+
+def test_segment_kernel_short_and_ragged_segments(dev, ragged):
+    """Sequences of 1 to 7777 kept rows in one batch of 32: waves without
+    pages (segments under 8 pages), the even split under 64 pages, one- and
+    two-page waves, partial last pages. Output and mass against the oracle."""
+    import draftkv
+    full, host = ragged
+    md = draftkv.CompressedKVCache(1, [draftkv.CompressionConfig(4, 1.0, group=32, scale_fp16=True)],
+                                   batch=B, cap=int(SHORT.max()) + 64)
+    md.sync_from(full, 0)
+    rng = np.random.default_rng(32)
+    q = (rng.standard_normal((B, HQ, D)) * 2.0).astype(np.float32)
+    out = md.attend(0, torch.from_numpy(q).to(dev), want_mass=True).cpu().numpy()
+    gs = {s: md.read_codes(0, s) for s in range(B)}
+
+    def one(s):
+        n = int(SHORT[s])
+        g = gs[s]
+        assert g["pos"].tolist() == list(range(n))
+        kq = quantize_codes(host[0][s, :n].float().numpy(), ARM.bits, ARM.group, ARM.meta)
+        vq = quantize_codes(host[1][s, :n].float().numpy(), ARM.bits, ARM.group, ARM.meta)
+        ref, _, mp = attend(q[s][None], kq[3], vq[3], np.arange(n), np.array([n]), HQ // HKV)
+        np.testing.assert_allclose(out[s], ref[0], rtol=RTOL, atol=ATOL, err_msg=f"seq {s} (n={n})")
+        np.testing.assert_allclose(g["score"], row_mass(mp).astype(np.float64), rtol=1e-4, atol=1e-7,
+                                   err_msg=f"seq {s} (n={n}) mass")
         return s
 
     assert sorted(_POOL.map(one, range(B))) == list(range(B))
