@@ -27,6 +27,17 @@ typedef __bf16 gbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float gf32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t gu32x4_t __attribute__((ext_vector_type(4)));   // a native vector: copies stay in registers
 
+// One 16-byte W load. NT: non-temporal, for workgroups that stream their W
+// rows through every K chunk (the long streams: measured 5-7% faster for the
+// Llama-3-8B gate/up weight at M = 32 and 96); the short per-chunk streams of
+// the split plans measured 12-17% slower that way (their loads wait on
+// latency, not bandwidth), so they keep the default policy.
+template <bool NT>
+__device__ __forceinline__ gu32x4_t load_w(const uint16_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const gu32x4_t*>(p));
+    return *reinterpret_cast<const gu32x4_t*>(p);
+}
+
 constexpr int GKB = 128;            // k per block: four 32-k MFMA steps
 constexpr int GX_ROW = GKB + 8;
      // LDS row of a staged x block (bf16), padded against bank conflicts
@@ -180,7 +191,7 @@ __global__ void __launch_bounds__(64 * WV) gemm_bf16_kernel(GemmArgs a) {
     do {                                                                                                        \
         const int k_ = blk_k(GB), st_ = blk_steps(GB);                                                         \
         _Pragma("unroll") for (int f_ = 0; f_ < NW; ++f_) _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_)       \
-            DST[f_][j_] = *reinterpret_cast<const gu32x4_t*>(wrow[f_] + w_step_off<WT>(k_, PARTIAL ? min(j_, st_ - 1) : j_)); \
+            DST[f_][j_] = load_w<MULTI>(wrow[f_] + w_step_off<WT>(k_, PARTIAL ? min(j_, st_ - 1) : j_));        \
     } while (0)
 #define DKV_LOAD_X(XD, GB)                                                                                      \
     do {                                                                                                        \
