@@ -13,6 +13,7 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 
@@ -44,12 +45,63 @@ def compile_one(src: str) -> str:
     return obj
 
 
+SEG_KERNEL = "_ZN3dkv21draft_attn_seg_kernel"
+_REG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
+
+
+def check_segment_registers() -> None:
+    """The segment kernel (csrc/draft_attn.hip) keeps its probabilities in
+    the VGPRs from SEG_VGPRS up, above what it lets the compiler allocate
+    (amdgpu_num_vgpr(SEG_VGPRS)). The compiler treats that attribute as a
+    target, not a bound -- one build took v176-v177 for code unpacking and
+    overwrote a wave's first page -- so the built code is checked: outside
+    inline asm no instruction of the kernel may name a register at or above
+    SEG_VGPRS, it uses no scratch, and its wave holds 256 VGPRs. Raises
+    RuntimeError otherwise."""
+    src = os.path.join(CSRC, "draft_attn.hip")
+    m = re.search(r"constexpr int SEG_VGPRS = (\d+);", open(src).read())
+    if not m:
+        raise RuntimeError("SEG_VGPRS not found in draft_attn.hip")
+    first = int(m.group(1))
+    asm = os.path.join(OBJ_DIR, "draft_attn.device.s")
+    cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-S", src, "-o", asm]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src}:\n{r.stdout}\n{r.stderr}")
+    lines = open(asm).read().split("\n")
+    starts = [i for i, l in enumerate(lines) if re.match(SEG_KERNEL + r"\S*:", l)]
+    if not starts:
+        raise RuntimeError("segment kernel not found in the device code")
+    for st in starts:
+        name = lines[st].split(":")[0]
+        in_asm = False
+        for i in range(st + 1, len(lines)):
+            t = lines[i].strip()
+            if t.startswith(".Lfunc_end"):
+                break
+            if t.startswith(";;#ASMSTART"):
+                in_asm = True
+            elif t.startswith(";;#ASMEND"):
+                in_asm = False
+            elif not in_asm and t and not t.startswith((";", ".")):
+                for g in _REG.finditer(t.split(";")[0]):
+                    hi = int(g.group(3) if g.group(3) else g.group(2))
+                    if hi >= first:
+                        raise RuntimeError(f"{name}: compiler-allocated register at or above v{first} "
+                                           f"(line {i + 1}: {t}); the kept probabilities live there")
+        desc = "\n".join(lines[next(i for i, l in enumerate(lines) if l.strip() == f".amdhsa_kernel {name}"):][:60])
+        if ".amdhsa_private_segment_fixed_size 0" not in desc or ".amdhsa_next_free_vgpr 256" not in desc:
+            raise RuntimeError(f"{name}: expected no scratch and 256 VGPRs per wave")
+
+
 def build(jobs: int = 8) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + 1))) as ex:
+        seg = ex.submit(check_segment_registers)
         objs = list(ex.map(compile_one, srcs))
+        seg.result()
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
