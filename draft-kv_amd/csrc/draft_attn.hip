@@ -1216,23 +1216,26 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
         // as the output's (written once, read once by the mass sum: measured
         // 1 us faster per call at b=32 ctx 32k)
         constexpr int U = 8;
-        auto emit = [&](int g0, float (&a)[U], float (&b)[U], bool whole) {
+        // WHOLE (a compile-time flag): every row of the chunk is live, so the
+        // stores need no row test
+        auto emit = [&](int g0, float (&a)[U], float (&b)[U], auto whole) {
             quad_sum16(a, b);
 #pragma unroll
             for (int k = 0; k < U; k += 2) {
                 const float lo = lane_select(a[k], b[k], hb0), hi = lane_select(a[k + 1], b[k + 1], hb0);
                 const float v = lane_select(lo, hi, hb1);
-                if (whole || (g0 + k) * PAGE + row2 < r_end) __builtin_nontemporal_store(v, &pm[(g0 + k) * PAGE]);
+                if (decltype(whole)::value || (g0 + k) * PAGE + row2 < r_end)
+                    __builtin_nontemporal_store(v, &pm[(g0 + k) * PAGE]);
             }
         };
-        // whole chunks in registers: 16 products with indexed operands, and
-        // with every row of the chunk live, no row test
+        // chunks in registers: 16 products with indexed operands
         const int Tr = min(T, SEG_TMAX);
         int g0 = 0;
         for (; g0 + U <= Tr; g0 += U) {
             float a[U], b[U];
             seg_get8_mul(2 * g0, fac, a, b);
-            emit(g0, a, b, (g0 + U) * PAGE <= r_end);
+            if ((g0 + U) * PAGE <= r_end) emit(g0, a, b, bool_c<true>{});
+            else emit(g0, a, b, bool_c<false>{});
         }
         for (; g0 < T; g0 += U) {
             float a[U], b[U];
@@ -1251,7 +1254,7 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
                 a[k] *= fac;
                 b[k] *= fac;
             }
-            emit(g0, a, b, false);
+            emit(g0, a, b, bool_c<false>{});
         }
     }
 }
