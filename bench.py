@@ -232,7 +232,8 @@ def time_drafter(comp, full, arms, n_q_heads: int, reps: int = 4) -> dict:
     each arm in turn: every layer, ``reps`` times, with N(0,1) queries and the
     attention mass on (as in the draft steps). HIP events on the launch
     stream time each whole call and, through the library's timing hook, its
-    split-K kernel alone. Returns {arm: {"call": [bytes, us, calls],
+    segment (or split-K) kernel alone, with the events carried by that
+    kernel's own launch. Returns {arm: {"call": [bytes, us, calls],
     "splitk": [bytes, us, calls]}}."""
     import numpy as np
     import torch
