@@ -156,7 +156,8 @@ class CompressedKVCache:
         self.n_kv_heads, self.d_head, self.cap = H, D, cap
         self.page_stride = self._page_stride(self.cfgs)
         b, L, dev = self.batch, self.n_layers, self.device
-        self.pages = torch.empty((b, L, H, cap // self.PAGE, self.page_stride), dtype=torch.uint8, device=dev)
+        # layer-major segments (the C ABI's layout): one layer's pages are contiguous
+        self.pages = torch.empty((L, b, H, cap // self.PAGE, self.page_stride), dtype=torch.uint8, device=dev)
         self.pos = torch.full((b, L, cap), -1, dtype=torch.int32, device=dev)
         self.score = torch.zeros((b, L, cap), dtype=torch.float64, device=dev)
         self.n_rows = torch.zeros((b, L), dtype=torch.int32, device=dev)

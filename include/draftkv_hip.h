@@ -49,8 +49,9 @@ typedef struct {
 /* Compressed drafter mirror -- reference draftkv/compress.py:95-241.
  * Per (seq, layer, kv_head) a dense segment of `cap` row slots (cap a
  * multiple of 32) stored as cap/32 pages of 32 rows; rows 0..n_rows-1 are
- * live (eviction and truncation compact it). Page p of a segment starts at
- *     pages + (((seq*n_layers + layer)*n_kv_heads + head) * (cap/32) + p) * page_stride
+ * live (eviction and truncation compact it). Segments are layer-major; page
+ * p of a segment starts at
+ *     pages + (((layer*batch + seq)*n_kv_heads + head) * (cap/32) + p) * page_stride
  * and holds K codes, K (scale, lo) pairs, V codes and V pairs of its rows in
  * the layout described in draft-kv_amd/csrc/mirror_layout.h (4-bit codes for
  * bits <= 4, bytes for 8 bits, raw float32 for 16 bits -- the reference
