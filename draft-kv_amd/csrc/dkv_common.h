@@ -160,13 +160,6 @@ __device__ __forceinline__ float dequant(int code, GroupMeta m) {
 __host__ __device__ inline int n_groups(int d, int group) { return (d + group - 1) / group; }
 
 // ------------------------------------------------------------ mirror addressing
-// Segments are layer-major: one layer's (sequence, KV head) segments are
-// contiguous, so a drafter call streams one compact range (32 layers of the
-// Llama-3-8B mirror at b=32: 59 us per segment-kernel launch layer-major
-// against 63 us sequence-major, every process)
-__host__ __device__ inline int64_t seg_index(const dkv_drafter_t& m, int s, int L, int h) {
-    return ((int64_t)L * m.batch + s) * m.n_kv_heads + h;
-}
 
 __host__ __device__ inline int64_t row_index(const dkv_drafter_t& m, int s, int L) {
     return (int64_t)(s * m.n_layers + L) * m.cap;

@@ -98,9 +98,22 @@ __host__ __device__ inline int64_t v_meta_off(const PageFmt& f, int i, int g) {
     return f.vm + ((int64_t)g * PAGE + j * 8 + e) * f.metaB;
 }
 
-// page p of segment (s, L, h)
+// page p of segment (s, L, h). A layer's pages form one range in which the
+// segments' pages are interleaved in chunks of PAGE_CHUNK: chunk c of every
+// segment (segments in (seq, head) order), then chunk c + 1, ...; the last
+// npg % PAGE_CHUNK pages of each segment follow the whole chunks. A drafter
+// call's waves, walking their pages in step, then read from one moving
+// window of the layer (Llama-3-8B mirror at b=32, int4 keep 0.25, 32
+// layers: segment kernel 60.3 -> 56.9 us; the int8 drafter unchanged).
+constexpr int PAGE_CHUNK = 8;
 __host__ __device__ inline uint8_t* page_ptr(const dkv_drafter_t& m, int s, int L, int h, int p) {
-    return static_cast<uint8_t*>(m.pages) + (seg_index(m, s, L, h) * (m.cap / PAGE) + p) * m.page_stride;
+    const int64_t nseg = (int64_t)m.batch * m.n_kv_heads, npg = m.cap / PAGE;
+    const int64_t nf = npg / PAGE_CHUNK, rem = npg - nf * PAGE_CHUNK;
+    const int64_t seg = (int64_t)s * m.n_kv_heads + h, base = (int64_t)L * npg * nseg;
+    const int64_t slot = p < nf * PAGE_CHUNK
+                             ? base + ((int64_t)(p / PAGE_CHUNK) * nseg + seg) * PAGE_CHUNK + p % PAGE_CHUNK
+                             : base + nf * PAGE_CHUNK * nseg + seg * rem + (p - nf * PAGE_CHUNK);
+    return static_cast<uint8_t*>(m.pages) + slot * m.page_stride;
 }
 
 // ---------------------------------------------------------------- device access

@@ -156,8 +156,9 @@ class CompressedKVCache:
         self.n_kv_heads, self.d_head, self.cap = H, D, cap
         self.page_stride = self._page_stride(self.cfgs)
         b, L, dev = self.batch, self.n_layers, self.device
-        # layer-major segments (the C ABI's layout): one layer's pages are contiguous
-        self.pages = torch.empty((L, b, H, cap // self.PAGE, self.page_stride), dtype=torch.uint8, device=dev)
+        # one row of page_stride bytes per page slot; page_slots() maps (layer,
+        # sequence, head, page) to its slot (the C ABI's layout)
+        self.pages = torch.empty((L * b * H * (cap // self.PAGE), self.page_stride), dtype=torch.uint8, device=dev)
         self.pos = torch.full((b, L, cap), -1, dtype=torch.int32, device=dev)
         self.score = torch.zeros((b, L, cap), dtype=torch.float64, device=dev)
         self.n_rows = torch.zeros((b, L), dtype=torch.int32, device=dev)
@@ -171,12 +172,35 @@ class CompressedKVCache:
         if cap <= self.cap and stride <= self.page_stride:
             return
         old_pages, old_pos, old_score, ocap, ostride = self.pages, self.pos, self.score, self.cap, self.page_stride
+        old_slots = self.page_slots(ocap)
         n_rows = self.n_rows
         self._alloc(self.n_kv_heads, self.d_head, max(cap, self.cap))
         self.n_rows = n_rows
-        self.pages[:, :, :, : ocap // self.PAGE, :ostride].copy_(old_pages)
+        new_slots = self.page_slots(self.cap)[:, :, : ocap // self.PAGE]
+        for L in range(self.n_layers):   # a layer at a time: the gather's temporary stays small
+            self.pages[new_slots[L].reshape(-1), :ostride] = old_pages[old_slots[L].reshape(-1)]
         self.pos[..., :ocap].copy_(old_pos)
         self.score[..., :ocap].copy_(old_score)
+
+    PAGE_CHUNK = 8   # pages per interleaved chunk (csrc/mirror_layout.h)
+
+    def page_slots(self, cap: int) -> torch.Tensor:
+        """Page slot of every (layer, sequence x KV head, page) at row capacity
+        ``cap``, shape (n_layers, batch * n_kv_heads, cap / 32): a layer's
+        pages are one range in which the segments interleave in chunks of
+        PAGE_CHUNK pages, the last cap/32 % PAGE_CHUNK pages of each segment
+        after the whole chunks (page_ptr in csrc/mirror_layout.h)."""
+        L, nseg, npg, ch = self.n_layers, self.batch * self.n_kv_heads, cap // self.PAGE, self.PAGE_CHUNK
+        nf = npg // ch
+        rem = npg - nf * ch
+        kw = dict(device=self.device, dtype=torch.int64)
+        lay = torch.arange(L, **kw).view(L, 1, 1)
+        seg = torch.arange(nseg, **kw).view(1, nseg, 1)
+        p = torch.arange(npg, **kw).view(1, 1, npg)
+        base = lay * npg * nseg
+        whole = base + ((p // ch) * nseg + seg) * ch + p % ch
+        tail = base + nf * ch * nseg + seg * rem + (p - nf * ch)
+        return torch.where(p < nf * ch, whole, tail)
 
     def desc(self) -> Drafter:
         return Drafter(self.pages.data_ptr(), self.pos.data_ptr(), self.score.data_ptr(), self.n_rows.data_ptr(),

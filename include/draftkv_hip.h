@@ -49,9 +49,13 @@ typedef struct {
 /* Compressed drafter mirror -- reference draftkv/compress.py:95-241.
  * Per (seq, layer, kv_head) a dense segment of `cap` row slots (cap a
  * multiple of 32) stored as cap/32 pages of 32 rows; rows 0..n_rows-1 are
- * live (eviction and truncation compact it). Segments are layer-major; page
- * p of a segment starts at
- *     pages + (((layer*batch + seq)*n_kv_heads + head) * (cap/32) + p) * page_stride
+ * live (eviction and truncation compact it). A layer's pages are one range
+ * in which the segments interleave in chunks of 8 pages; with npg = cap/32,
+ * nseg = batch*n_kv_heads, nf = npg/8, rem = npg - 8*nf and
+ * seg = seq*n_kv_heads + head, page p of a segment is slot
+ *     layer*npg*nseg + ((p/8)*nseg + seg)*8 + p%8          (p < 8*nf)
+ *     layer*npg*nseg + 8*nf*nseg + seg*rem + (p - 8*nf)    (otherwise)
+ * starting at pages + slot * page_stride
  * and holds K codes, K (scale, lo) pairs, V codes and V pairs of its rows in
  * the layout described in draft-kv_amd/csrc/mirror_layout.h (4-bit codes for
  * bits <= 4, bytes for 8 bits, raw float32 for 16 bits -- the reference
