@@ -49,15 +49,77 @@ SEG_KERNEL = "_ZN3dkv21draft_attn_seg_kernel"
 _REG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
 
 
+def _operands(ins: str) -> list[str]:
+    """The operand fields of one instruction line (mnemonic dropped, comment
+    and trailing modifiers such as ``row_mask:0xf`` kept in the last field)."""
+    parts = ins.split(None, 1)
+    return [] if len(parts) < 2 else [o.strip() for o in parts[1].split(",")]
+
+
+def scan_segment_asm(lines: list[str], first: int) -> None:
+    """Check the assembly of the segment kernel(s) in ``lines``: no register
+    at or above v``first`` anywhere, except as the literal indexed operand of
+    an ``s_set_gpr_idx_on`` session inside inline asm (the destination under
+    gpr_idx(DST), the first source under gpr_idx(SRC0)) -- the compiler also
+    allocates the other operands of the asm blocks, so those are checked
+    too. Each kernel must use no scratch and hold 256 VGPRs per wave.
+    Raises RuntimeError on the first violation."""
+    starts = [i for i, l in enumerate(lines) if re.match(SEG_KERNEL + r"\S*:", l)]
+    if not starts:
+        raise RuntimeError("segment kernel not found in the device code")
+    for st in starts:
+        name = lines[st].split(":")[0]
+        in_asm, mode = False, None
+        for i in range(st + 1, len(lines)):
+            t = lines[i].strip()
+            if t.startswith(".Lfunc_end"):
+                break
+            if t.startswith(";;#ASMSTART"):
+                in_asm, mode = True, None
+                continue
+            if t.startswith(";;#ASMEND"):
+                if mode is not None:
+                    raise RuntimeError(f"{name}: an asm block ends inside an s_set_gpr_idx session "
+                                       f"(line {i + 1})")
+                in_asm = False
+                continue
+            if not t or t.startswith((";", ".")):
+                continue
+            ins = t.split(";")[0].strip()
+            op = ins.split(None, 1)[0]
+            if op == "s_set_gpr_idx_on":
+                if not in_asm:
+                    raise RuntimeError(f"{name}: s_set_gpr_idx_on outside inline asm (line {i + 1})")
+                m = re.search(r"gpr_idx\((\w+)\)", ins)
+                mode = m.group(1) if m else "?"
+                if mode not in ("DST", "SRC0"):
+                    raise RuntimeError(f"{name}: unexpected gpr_idx mode (line {i + 1}: {t})")
+                continue
+            if op == "s_set_gpr_idx_off":
+                mode = None
+                continue
+            for k, fld in enumerate(_operands(ins)):
+                for g in _REG.finditer(fld):
+                    hi = int(g.group(3) if g.group(3) else g.group(2))
+                    if hi < first:
+                        continue
+                    indexed = (in_asm and g.group(3) is not None and fld == f"v{hi}" and op.startswith("v_")
+                               and ((mode == "DST" and k == 0) or (mode == "SRC0" and k == 1)))
+                    if not indexed:
+                        raise RuntimeError(f"{name}: register at or above v{first} outside an indexed operand "
+                                           f"(line {i + 1}: {t}); the kept probabilities live there")
+        desc = "\n".join(lines[next(i for i, l in enumerate(lines) if l.strip() == f".amdhsa_kernel {name}"):][:60])
+        if ".amdhsa_private_segment_fixed_size 0" not in desc or ".amdhsa_next_free_vgpr 256" not in desc:
+            raise RuntimeError(f"{name}: expected no scratch and 256 VGPRs per wave")
+
+
 def check_segment_registers() -> None:
     """The segment kernel (csrc/draft_attn.hip) keeps its probabilities in
     the VGPRs from SEG_VGPRS up, above what it lets the compiler allocate
     (amdgpu_num_vgpr(SEG_VGPRS)). The compiler treats that attribute as a
     target, not a bound -- one build took v176-v177 for code unpacking and
-    overwrote a wave's first page -- so the built code is checked: outside
-    inline asm no instruction of the kernel may name a register at or above
-    SEG_VGPRS, it uses no scratch, and its wave holds 256 VGPRs. Raises
-    RuntimeError otherwise."""
+    overwrote a wave's first page -- so the built code is checked by
+    ``scan_segment_asm``. Raises RuntimeError on a violation."""
     src = os.path.join(CSRC, "draft_attn.hip")
     m = re.search(r"constexpr int SEG_VGPRS = (\d+);", open(src).read())
     if not m:
@@ -68,30 +130,7 @@ def check_segment_registers() -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed on {src}:\n{r.stdout}\n{r.stderr}")
-    lines = open(asm).read().split("\n")
-    starts = [i for i, l in enumerate(lines) if re.match(SEG_KERNEL + r"\S*:", l)]
-    if not starts:
-        raise RuntimeError("segment kernel not found in the device code")
-    for st in starts:
-        name = lines[st].split(":")[0]
-        in_asm = False
-        for i in range(st + 1, len(lines)):
-            t = lines[i].strip()
-            if t.startswith(".Lfunc_end"):
-                break
-            if t.startswith(";;#ASMSTART"):
-                in_asm = True
-            elif t.startswith(";;#ASMEND"):
-                in_asm = False
-            elif not in_asm and t and not t.startswith((";", ".")):
-                for g in _REG.finditer(t.split(";")[0]):
-                    hi = int(g.group(3) if g.group(3) else g.group(2))
-                    if hi >= first:
-                        raise RuntimeError(f"{name}: compiler-allocated register at or above v{first} "
-                                           f"(line {i + 1}: {t}); the kept probabilities live there")
-        desc = "\n".join(lines[next(i for i, l in enumerate(lines) if l.strip() == f".amdhsa_kernel {name}"):][:60])
-        if ".amdhsa_private_segment_fixed_size 0" not in desc or ".amdhsa_next_free_vgpr 256" not in desc:
-            raise RuntimeError(f"{name}: expected no scratch and 256 VGPRs per wave")
+    scan_segment_asm(open(asm).read().split("\n"), first)
 
 
 def build(jobs: int = 8) -> str:

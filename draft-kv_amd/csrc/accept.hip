@@ -128,13 +128,14 @@ __device__ __forceinline__ double prob(float x, const RowNorm& r, float T) {
 }
 
 // One block per sequence, one wave per row (rows w, w + DECIDE_WAVES, ...):
-// each wave merges its row's chunk statistics. Then the lanes of wave 0
-// evaluate the accept test's p and q of every drafted position at once (the
-// scattered reads in flight together), and lane 0 walks the tests in order --
-// the same decisions, in the same order, as one lane reading as it goes.
+// each wave merges its row's chunk statistics into the row's norm. Then wave
+// 0 takes the drafted positions 64 at a time: its lanes fetch the accept
+// test's inputs of 64 positions at once (the argmax, or p and q of the
+// drafted token: the scattered reads in flight together), and lane 0 walks
+// those tests in order -- the same decisions, in the same order, as one lane
+// reading as it goes -- until one fails. Any gamma.
 constexpr int DECIDE_WAVES = 16;
 constexpr int PICK_MAX_CHUNKS = 1024;   // vocab up to 4M
-constexpr int DECIDE_MAX_GAMMA = 64;
 __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float* __restrict__ target,
                                                                      const float* __restrict__ draft,
                                                                      const int32_t* __restrict__ draft_tokens,
@@ -150,8 +151,8 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
     const ChunkStat* st = stats + (int64_t)s * R * n_chunks;
     const int n_rows = samp ? R : gamma + 1;
     RowNorm* nr = norms + (int64_t)s * R;
-    __shared__ RowNorm snr[2 * DECIDE_MAX_GAMMA + 1];
-    __shared__ double sp[DECIDE_MAX_GAMMA], sq[DECIDE_MAX_GAMMA];
+    __shared__ double sp[WAVE], sq[WAVE];
+    __shared__ int sarg[WAVE];
     for (int r = w; r < n_rows; r += DECIDE_WAVES) {
         const ChunkStat* sr = st + (int64_t)r * n_chunks;
         float mx = -INFINITY;
@@ -178,51 +179,60 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
             rn.S = wave_sum_d(S);
             rn.iS = 1.0 / rn.S;
         }
-        if (lane == 0) {
-            nr[r] = rn;
-            snr[r] = rn;
-        }
+        if (lane == 0) nr[r] = rn;
     }
-    __syncthreads();
+    __syncthreads();   // the norms written by every wave are visible to wave 0
     if (w != 0) return;
-    // p and q of the drafted token at every position (lane i: position i)
-    if (samp) {
-        for (int i = lane; i < gamma; i += WAVE) {
-            const int d = draft_tokens[(int64_t)s * gamma + i];
-            double p = 0.0, q = 0.0;
-            if (d >= 0 && d < vocab) {
-                p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], snr[i], T);
-                q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], snr[gamma + 1 + i], T);
-            }
-            sp[i] = p;
-            sq[i] = q;
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane != 0) return;
-    int acc = 0, used = 0;
     const double* us = u + (int64_t)s * (gamma + 1);
-    for (int i = 0; i < gamma; ++i) {
-        const int d = draft_tokens[(int64_t)s * gamma + i];
-        bool ok;
-        if (d < 0 || d >= vocab) {
-            ok = false;              // not a token of this vocabulary: never read past the row
-            if (T > 0.0f) ++used;
-        } else if (T <= 0.0f) {
-            ok = snr[i].arg == d;
-        } else {
-            const double ratio = sq[i] > 0.0 ? sp[i] / sq[i] : 0.0;
-            ok = us[used] < fmin(1.0, ratio);
-            ++used;
+    int acc = 0, used = 0;
+    bool stop = false;
+    for (int base = 0; base < gamma && !stop; base += WAVE) {
+        const int i = base + lane;
+        if (i < gamma) {   // lane: the inputs of position i's test
+            const int d = draft_tokens[(int64_t)s * gamma + i];
+            if (samp) {
+                double p = 0.0, q = 0.0;
+                if (d >= 0 && d < vocab) {
+                    p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], nr[i], T);
+                    q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], nr[gamma + 1 + i], T);
+                }
+                sp[lane] = p;
+                sq[lane] = q;
+            } else {
+                sarg[lane] = nr[i].arg;
+            }
         }
-        if (!ok) break;
-        ++acc;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {
+            for (int j = base; j < min(gamma, base + WAVE); ++j) {
+                const int d = draft_tokens[(int64_t)s * gamma + j];
+                bool ok;
+                if (d < 0 || d >= vocab) {
+                    ok = false;              // not a token of this vocabulary: never read past the row
+                    if (samp) ++used;
+                } else if (!samp) {
+                    ok = sarg[j - base] == d;
+                } else {
+                    const double ratio = sq[j - base] > 0.0 ? sp[j - base] / sq[j - base] : 0.0;
+                    ok = us[used] < fmin(1.0, ratio);
+                    ++used;
+                }
+                if (!ok) {
+                    stop = true;
+                    break;
+                }
+                ++acc;
+            }
+        }
+        stop = __shfl(stop ? 1 : 0, 0) != 0;
+        __builtin_amdgcn_wave_barrier();   // lane 0 is done with this block before the lanes refill it
     }
+    if (lane != 0) return;
     SeqState ss{0, acc, 0.0};
-    if (T <= 0.0f) {
-        next_token[s] = snr[acc].arg;
+    if (!samp) {
+        next_token[s] = nr[acc].arg;
         if (acc == gamma) ++used;   // the bonus draw is taken even though p is one-hot
     } else {
         ss.mode = (acc == gamma) ? 1 : 2;
@@ -405,7 +415,6 @@ extern "C" int dkv_accept(const float* target, const float* draft, const int32_t
                           dkv_stream_t stream) {
     DKV_REQUIRE(target && accepted && next_token && n_uniforms && u, "dkv_accept: NULL argument");
     DKV_REQUIRE(batch > 0 && gamma >= 0 && vocab > 0, "dkv_accept: bad sizes");
-    DKV_REQUIRE(gamma <= DECIDE_MAX_GAMMA, "dkv_accept: gamma must be at most 64");
     DKV_REQUIRE(chunks_of(vocab) <= PICK_MAX_CHUNKS, "dkv_accept: vocab too large");
     DKV_REQUIRE(gamma == 0 || draft_tokens, "dkv_accept: draft_tokens is NULL");
     DKV_REQUIRE(temperature <= 0.0f || gamma == 0 || draft, "dkv_accept: draft logits needed when T > 0");

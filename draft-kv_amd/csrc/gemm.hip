@@ -44,11 +44,19 @@ constexpr int GX_ROW = GKB + 8;
 
 __device__ __forceinline__ gbf16x8_t as_bf16x8(gu32x4_t v) { return __builtin_bit_cast(gbf16x8_t, v); }
 
-__device__ __forceinline__ float4 bias4(const uint16_t* b, int64_t n) {
+// bias of outputs n .. n+3 (n % 4 == 0, so one 8-byte load where all four
+// exist); zero past N
+__device__ __forceinline__ float4 bias4(const uint16_t* b, int64_t n, int N) {
     if (!b) return make_float4(0.f, 0.f, 0.f, 0.f);
-    const uint2 v = *reinterpret_cast<const uint2*>(b + n);
-    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
-                       __uint_as_float(v.y & 0xffff0000u));
+    if (n + 3 < N) {
+        const uint2 v = *reinterpret_cast<const uint2*>(b + n);
+        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+    }
+    float t[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = n + e < N ? __uint_as_float((uint32_t)b[n + e] << 16) : 0.0f;
+    return make_float4(t[0], t[1], t[2], t[3]);
 }
 
 __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
@@ -89,6 +97,26 @@ __device__ __forceinline__ gu32x4_t x8_bf16(const XRaw<XF32>& r) {
     else return r;
 }
 
+// y[m][n .. n+3] = t for a row-major y of N columns: one vector store when
+// N % 4 == 0 (the row, and so the four outputs, are aligned; n < N then
+// implies n + 3 < N), else element by element up to column N - 1
+__device__ __forceinline__ void store_y4(void* y, int y_f32, int64_t m, int n, int N, const gf32x4_t& t) {
+    const int64_t o = m * N + n;
+    if ((N & 3) == 0) {
+        if (y_f32) *reinterpret_cast<float4*>(static_cast<float*>(y) + o) = make_float4(t[0], t[1], t[2], t[3]);
+        else
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + o) =
+                make_uint2(bf16_pair_rne(t[0], t[1]), bf16_pair_rne(t[2], t[3]));
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (n + e >= N) break;
+        if (y_f32) static_cast<float*>(y)[o + e] = t[e];
+        else static_cast<uint16_t*>(y)[o + e] = f32_to_bf16_rne(t[e]);
+    }
+}
+
 struct GemmArgs {
     const void* x;       // [M, K], bf16 or float32 (x_f32)
     int x_f32;
@@ -113,11 +141,13 @@ struct GemmArgs {
 // A wave's load of one step is then 1 KB contiguous (16 B per lane, lane
 // 16 q + c), and a fragment streams as one run; row-major W makes each load
 // 16 rows x 64 B. The arithmetic is the same either way.
+// Row-major W may end inside a fragment (N % 16 != 0): its lanes past row N-1
+// reread row N-1, whose products land in outputs that are never stored.
 template <bool WT>
 __device__ __forceinline__ const uint16_t* w_lane_base(const uint16_t* w, int64_t frag_row0, int col, int q, int lane,
-                                                       int K) {
+                                                       int K, int N) {
     if constexpr (WT) return w + frag_row0 * K + 8 * lane;
-    else return w + (frag_row0 + col) * K + 8 * q;
+    else return w + min(frag_row0 + col, (int64_t)N - 1) * K + 8 * q;
 }
 // offset of step j of the block starting at k (elements, from the lane base)
 template <bool WT>
@@ -158,7 +188,7 @@ __global__ void __launch_bounds__(64 * WV) gemm_bf16_kernel(GemmArgs a) {
     const int nb = (KC + GKB - 1) / GKB, G = nb * a.c_per;
     const uint16_t* wrow[NW];
 #pragma unroll
-    for (int f = 0; f < NW; ++f) wrow[f] = w_lane_base<WT>(a.w, live ? n0 + 16 * f : 0, col, q, lane, K);
+    for (int f = 0; f < NW; ++f) wrow[f] = w_lane_base<WT>(a.w, live ? n0 + 16 * f : 0, col, q, lane, K, a.N);
     // x piece i of this thread: tile row xr_row[i], k offset 8 xr_c[i] in the block. Tile rows past M
     // reread row M-1 (their outputs are dropped), so every load and LDS write is unconditional.
     // (pieces past the tile, when the thread count does not divide it, repeat
@@ -284,24 +314,22 @@ __global__ void __launch_bounds__(64 * WV) gemm_bf16_kernel(GemmArgs a) {
             if constexpr (MULTI) t = tot[f][mb];
             else t = acc[f][mb];
             const int n = n0 + 16 * f + 4 * q;
+            if (n >= a.N) continue;   // a fragment past the end of W (N % 16 != 0)
             const int64_t o = (int64_t)m * a.N + n;
             if (!to_part && a.bias) {
-                const float4 bv = bias4(a.bias, n);
+                const float4 bv = bias4(a.bias, n, a.N);
                 t[0] = t[0] + bv.x;
                 t[1] = t[1] + bv.y;
                 t[2] = t[2] + bv.z;
                 t[3] = t[3] + bv.w;
             }
-            if (to_part) {
+            if (to_part) {   // partials only where N % 16 == 0
                 *reinterpret_cast<float4*>(a.part + (int64_t)c0 * a.M * a.N + o) = make_float4(t[0], t[1], t[2], t[3]);
             } else if (a.swiglu) {   // rows n .. n+3 are (gate, up) of outputs n/2 and n/2 + 1
                 *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (int64_t)m * (a.N / 2) + n / 2) =
                     swiglu_pair(t[0], t[1], t[2], t[3]);
-            } else if (a.y_f32) {
-                *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
             } else {
-                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + o) =
-                    make_uint2(bf16_pair_rne(t[0], t[1]), bf16_pair_rne(t[2], t[3]));
+                store_y4(a.y, a.y_f32, m, n, a.N, t);
             }
         }
 }
@@ -325,7 +353,7 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
     const bool live = n0 < a.N;   // wave-uniform
     const int K = a.K, KC = a.KC, S = a.S;
     const int nb = KC / GKB, G = nb * (S / CW);
-    const uint16_t* wrow = w_lane_base<WT>(a.w, live ? n0 : 0, col, q, lane, K);
+    const uint16_t* wrow = w_lane_base<WT>(a.w, live ? n0 : 0, col, q, lane, K, a.N);
     int64_t xrow[MB];   // element offset of the lane's x row and lane group
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) xrow[mb] = (int64_t)min(16 * mb + col, a.M - 1) * K + 8 * q;
@@ -405,24 +433,20 @@ __global__ void __launch_bounds__(64 * RW * CW) gemm_bf16_small_kernel(GemmArgs 
 #pragma unroll
             for (int e = 0; e < 4; ++e) t[e] = t[e] + u[e];
         }
-        if (m >= a.M) continue;
         const int n = n0 + 4 * q;
+        if (m >= a.M || n >= a.N) continue;
         if (a.bias) {
-            const float4 bv = bias4(a.bias, n);
+            const float4 bv = bias4(a.bias, n, a.N);
             t[0] = t[0] + bv.x;
             t[1] = t[1] + bv.y;
             t[2] = t[2] + bv.z;
             t[3] = t[3] + bv.w;
         }
-        const int64_t o = (int64_t)m * a.N + n;
         if (a.swiglu) {
             *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (int64_t)m * (a.N / 2) + n / 2) =
                 swiglu_pair(t[0], t[1], t[2], t[3]);
-        } else if (a.y_f32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(t[0], t[1], t[2], t[3]);
         } else {
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + o) =
-                make_uint2(bf16_pair_rne(t[0], t[1]), bf16_pair_rne(t[2], t[3]));
+            store_y4(a.y, a.y_f32, m, n, a.N, t);
         }
     }
 }
@@ -441,8 +465,8 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restric
         t.z += u.z;
         t.w += u.w;
     }
-    if (bias) {   // the four outputs share a row (N % 16 == 0)
-        const float4 bv = bias4(bias, i % N);
+    if (bias) {   // the four outputs share a row (partials only where N % 16 == 0)
+        const float4 bv = bias4(bias, i % N, N);
         t.x += bv.x;
         t.y += bv.y;
         t.z += bv.z;
@@ -481,7 +505,7 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     if (M <= 8 && S >= 4) {   // a few rows and a chunked K: split K inside the workgroup
         p.small = 1, p.nw = 1, p.mb = 1, p.m_tiles = 1, p.c_per = S;
         p.cw = 4, p.rw = 1;
-        p.n_tiles = N / 16;
+        p.n_tiles = (N + 15) / 16;
         return p;
     }
     // from M = 33 on, two W fragments per wave (each x fragment read from LDS feeds two MFMAs) wherever
@@ -492,7 +516,8 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     p.m_tiles = (M + 16 * p.mb - 1) / (16 * p.mb);
     p.n_tiles = (N + 64 * p.nw - 1) / (64 * p.nw);
     // split the chunks over workgroups only when the tiles alone leave most of the chip idle
-    p.c_per = (S > 1 && (int64_t)p.n_tiles * p.m_tiles < 128) ? 1 : S;
+    // (partials need whole 16-row fragments: N % 16 == 0)
+    p.c_per = (S > 1 && (int64_t)p.n_tiles * p.m_tiles < 128 && N % 16 == 0) ? 1 : S;
     // 7-wave workgroups when they cut W into whole rounds of 256 tiles and 4-wave ones do not
     // (the Llama-3-8B gate/up weight, 28672 rows: 448 tiles of 64 leave the CUs unevenly loaded,
     // 256 of 112 give every CU one)
@@ -573,14 +598,15 @@ extern "C" int dkv_gemm_bf16(const void* x, int32_t x_dtype, const void* w, cons
                              dkv_stream_t stream) {
     DKV_REQUIRE(x && w && y, "dkv_gemm_bf16: NULL argument");
     DKV_REQUIRE(M >= 0 && N > 0 && K > 0, "dkv_gemm_bf16: bad sizes");
-    DKV_REQUIRE(N % 16 == 0 && K % 32 == 0, "dkv_gemm_bf16: N must be a multiple of 16 and K of 32");
+    DKV_REQUIRE(K % 32 == 0, "dkv_gemm_bf16: K must be a multiple of 32");
     DKV_REQUIRE(y_dtype == DKV_BF16 || y_dtype == DKV_F32, "dkv_gemm_bf16: y must be bf16 or float32");
     DKV_REQUIRE(x_dtype == DKV_BF16 || x_dtype == DKV_F32, "dkv_gemm_bf16: x must be bf16 or float32");
     DKV_REQUIRE((flags & ~(DKV_GEMM_SWIGLU | DKV_GEMM_DEFER | DKV_GEMM_WTILED)) == 0, "dkv_gemm_bf16: unknown flags");
     const int swiglu = (flags & DKV_GEMM_SWIGLU) != 0;
     const int defer = (flags & DKV_GEMM_DEFER) != 0;
     const bool wt = (flags & DKV_GEMM_WTILED) != 0;
-    DKV_REQUIRE(!wt || K % GKB == 0, "dkv_gemm_bf16: tiled W needs K a multiple of 128");
+    DKV_REQUIRE(!wt || (K % GKB == 0 && N % 16 == 0), "dkv_gemm_bf16: tiled W needs K % 128 == 0 and N % 16 == 0");
+    DKV_REQUIRE(!swiglu || N % 16 == 0, "dkv_gemm_bf16: the SwiGLU epilogue needs N a multiple of 16");
     DKV_REQUIRE(!defer || (!swiglu && !bias && y_dtype == DKV_BF16),
                 "dkv_gemm_bf16: deferred partials are for a bf16 y without bias or SwiGLU");
     DKV_REQUIRE(!swiglu || (y_dtype == DKV_BF16 && !bias),

@@ -11,9 +11,11 @@ optional projection biases, and the LM head (own matrix / tied embedding).
   reduction per output), so a row's logits do not depend on how many rows
   share the pass -- the verify pass and one-token decoding agree bit for bit,
   which is what makes greedy self-speculative decoding exactly lossless.
-* bfloat16 weights: the projections run as bf16 GEMMs on the matrix cores
-  (``torch.nn.functional.linear``); norms, RoPE, activations and residual adds
-  stay in the HIP kernels with float32 activations.
+* bfloat16 weights: the projections and the head run as the library's bf16
+  MFMA GEMM (``dkv_gemm_bf16``, K chunks fixed by the shape, so a row's result
+  does not depend on the batch either); norms, RoPE, activations and residual
+  adds stay in the HIP kernels with float32 activations. There is no other
+  backend: a product the library GEMM does not take raises.
 
 Attention and the K/V writes go to the cache the forward is handed: the
 device-paged full cache (``PagedKVCache`` / ``FullKVCache``) or the drafter
@@ -28,7 +30,6 @@ from typing import Optional, Sequence
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from . import ops
 from .compress import CompressedKVCache, FullKVCache
@@ -88,9 +89,12 @@ class Decoder:
     def w_layout(self) -> int:
         return 1 if self.wdtype == torch.bfloat16 else self.layout
 
-    def new_cache(self, batch: int = 1, max_tokens: int = 1 << 20) -> FullKVCache:
+    def new_cache(self, batch: int = 1, max_tokens: int = 1 << 20, chunk_keys: Optional[int] = None) -> FullKVCache:
+        """The full cache for ``batch`` sequences of up to ``max_tokens`` rows;
+        ``chunk_keys`` fixes the attention kernel's key chunk (by default
+        chosen from the shape, ``paged.auto_chunk_keys``)."""
         return FullKVCache(self.n_layers, self.n_kv_heads, self.d_head, dtype=self.kv_dtype, batch=batch,
-                           max_tokens=max_tokens, device=self.device)
+                           max_tokens=max_tokens, device=self.device, chunk_keys=chunk_keys)
 
     # ------------------------------------------------------------ RoPE table
     def _cos_sin(self, need: int):
@@ -121,14 +125,13 @@ class Decoder:
 
     @staticmethod
     def _linear(x: torch.Tensor, w: torch.Tensor, bias=None, out_dtype=torch.bfloat16, defer: bool = False):
-        """bf16 x @ W^T (+ b) (W as [N, K]): the library's batch-invariant
-        GEMM when it takes the shapes, else torch's. ``defer``: the caller
-        takes ``ops.Partials`` (qkv_split, add_norm), so the GEMM may leave
-        its per-chunk partials to it instead of reducing them itself."""
-        if ops.gemm_bf16_ok(x, w, bias):
-            return ops.gemm_bf16(x, w, bias, out_dtype, defer=defer)
-        y = F.linear(x.to(w.dtype), w, bias)
-        return y if out_dtype == torch.bfloat16 else y.to(out_dtype)
+        """bf16 x @ W^T (+ b) (W as [N, K]) by the library's batch-invariant
+        GEMM (any N; K a multiple of 32). ``defer``: the caller takes
+        ``ops.Partials`` (qkv_split, add_norm), so the GEMM may leave its
+        per-chunk partials to it instead of reducing them itself. Raises
+        ValueError for a product the GEMM does not take (a second backend
+        would break the batch invariance greedy losslessness rests on)."""
+        return ops.gemm_bf16(x, w, bias, out_dtype, defer=defer)
 
     def _residual(self, h: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias, nw, nb) -> torch.Tensor:
         """h += x @ W (+ bias), then return the next norm of h (weights nw, nb).
@@ -144,7 +147,16 @@ class Decoder:
         tiled form (``ops.TiledW``: 1 KB contiguous per load of W), and the LM
         head too unless it is the (tied) embedding table. The arithmetic is
         unchanged; ``TiledW.rows()`` gives a matrix back."""
-        if self.wdtype != torch.bfloat16 or self.device.type != "cuda":
+        if self.wdtype != torch.bfloat16:
+            return
+        for i, p in enumerate(self.layers):   # the bf16 GEMM's k step is 32
+            for name in ("wqkv", "wo", "w1", "w2"):
+                if getattr(p, name).shape[1] % 32:
+                    raise ValueError(f"bf16 weights: layer {i} {name} has input width {getattr(p, name).shape[1]}, "
+                                     "not a multiple of 32 (the bf16 GEMM's k step)")
+        if self.head.shape[1] % 32:
+            raise ValueError(f"bf16 weights: the head's input width {self.head.shape[1]} is not a multiple of 32")
+        if self.device.type != "cuda":
             return
         for p in self.layers:
             for name in ("wqkv", "wo", "w1", "w2"):
@@ -157,8 +169,13 @@ class Decoder:
     def _interleave_gate_up(self) -> None:
         """bf16 SwiGLU models: reorder each fused [gate; up] weight to rows
         (gate_0, up_0, gate_1, up_1, ...), so the GEMM's epilogue holds both
-        halves of a pair and writes silu(gate) * up directly."""
+        halves of a pair and writes silu(gate) * up directly (when the width
+        is a multiple of 8, so the fused weight's rows come in whole 16-row
+        fragments; else the GEMM writes [gate | up] and the SwiGLU kernel
+        combines them)."""
         if self.mlp != "swiglu" or self.wdtype != torch.bfloat16:
+            return
+        if self.layers and self.layers[0].w1.shape[0] % 16:
             return
         for p in self.layers:
             ff2, k = p.w1.shape
@@ -168,10 +185,7 @@ class Decoder:
     def _mlp_inner(self, x: torch.Tensor, p: Layer) -> torch.Tensor:
         if self.mlp == "swiglu":
             if getattr(self, "gate_up_interleaved", False):
-                if ops.gemm_bf16_ok(x, p.w1):
-                    return ops.gemm_bf16(x, p.w1, swiglu=True)
-                y = F.linear(x.to(p.w1.dtype), p.w1)
-                return ops.silu_mul(torch.cat([y[:, 0::2], y[:, 1::2]], 1), self.act_dtype)
+                return ops.gemm_bf16(x, p.w1, swiglu=True)
             return ops.silu_mul(self._proj(x, p.w1), self.act_dtype)
         if self.mlp == "gelu":
             return ops.bias_gelu(self._proj(x, p.w1), p.b1, self.act_dtype)

@@ -32,7 +32,7 @@ import torch
 
 from . import ops
 from .compress import CompressedKVCache
-from .paged import PagedKVCache
+from .paged import PagedKVCache, auto_chunk_keys
 from .graphs import DraftStepGraph, FullStepGraph, full_graph_key, graph_key
 from .config import CompressionConfig
 from .controller import Controller, FixedPolicy
@@ -101,14 +101,21 @@ class DraftKVEngine:
             g = self._rngs[s] = np.random.default_rng(self.seed + s)
         return g
 
-    def _new_full(self, batch: int, max_tokens: int):
+    def _new_full(self, batch: int, max_tokens: int, span: Optional[int] = None):
+        """The full cache of one call: ``max_tokens`` rows per sequence, and the
+        attention key chunk chosen from ``span`` (longest prompt + new tokens;
+        default max_tokens), which plain and speculative decoding of the same
+        request share -- their rows then merge the same chunk partials in the
+        same order, so the greedy outputs stay identical whatever room each
+        path reserves."""
         if self.full_cache_factory is not None:
             c = self.full_cache_factory()
             if getattr(c, "batch", 1) != batch:
                 raise ValueError(f"full_cache_factory made a cache for {getattr(c, 'batch', 1)} sequences, "
                                  f"need {batch}")
             return c
-        return self.model.new_cache(batch=batch, max_tokens=max_tokens)
+        ck = auto_chunk_keys(batch, self.model.n_kv_heads, max_tokens if span is None else span)
+        return self.model.new_cache(batch=batch, max_tokens=max_tokens, chunk_keys=ck)
 
     def _prefill(self, prompts, full) -> None:
         lens = np.array([len(p) for p in prompts], np.int64)
@@ -144,7 +151,8 @@ class DraftKVEngine:
         model = self.model
         toks = self._check_prompts(prompts, model.vocab_size)
         b = len(toks)
-        full = self._new_full(b, max(len(t) for t in toks) + max_new_tokens + 16)
+        span = max(len(t) for t in toks) + max_new_tokens
+        full = self._new_full(b, span + 16, span)
         self.last_full = full
         self._prefill(toks, full)
         dev = model.device
@@ -175,7 +183,8 @@ class DraftKVEngine:
         exactly the reference's cap ``min(gamma, budget - 1)``)."""
         toks = self._check_prompts(prompts, self.model.vocab_size)
         plen = np.array([len(t) for t in toks], np.int64)
-        full = self._new_full(len(toks), rows_needed(plen, max_new_tokens, self.controller))
+        full = self._new_full(len(toks), rows_needed(plen, max_new_tokens, self.controller),
+                              int(plen.max()) + max_new_tokens)
         self._prefill(toks, full)
         batch = DecodeBatch(self, toks, full, max_new_tokens, temperature, context_key)
         while batch.step():

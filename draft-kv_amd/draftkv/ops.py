@@ -520,14 +520,14 @@ def tile_ok(w) -> bool:
 
 def gemm_bf16_ok(x: torch.Tensor, w, bias: Optional[torch.Tensor] = None) -> bool:
     """Whether dkv_gemm_bf16 takes this product (contiguous x [M, K], bf16 or
-    float32, and bf16 w [N, K] (a tensor or a ``TiledW``), N % 16 == 0,
+    float32, and bf16 w [N, K] (a tensor or a ``TiledW``), any N,
     K % 32 == 0, 16-byte aligned; bias None or bf16 contiguous [N], 8-byte
     aligned)."""
     if not isinstance(w, TiledW) and not (isinstance(w, torch.Tensor) and w.dim() == 2 and w.is_contiguous()):
         return False
     ok = (x.dtype in (torch.bfloat16, torch.float32) and w.dtype == torch.bfloat16 and x.dim() == 2
           and x.is_cuda and w.is_cuda and x.is_contiguous()
-          and x.shape[1] == w.shape[1] and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0
+          and x.shape[1] == w.shape[1] and w.shape[0] > 0 and w.shape[1] % 32 == 0
           and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
     if ok and bias is not None:
         ok = (bias.dtype == torch.bfloat16 and bias.is_cuda and bias.dim() == 1 and bias.is_contiguous()
@@ -571,8 +571,8 @@ def gemm_bf16(x: torch.Tensor, w, bias: Optional[torch.Tensor] = None,
                          + ("" if bias is None else f", bias {tuple(bias.shape)} {bias.dtype}"))
     M, K = x.shape
     N = w.shape[0]
-    if swiglu and (bias is not None or out_dtype != torch.bfloat16):
-        raise ValueError("gemm_bf16: the SwiGLU epilogue writes bf16 and takes no bias")
+    if swiglu and (bias is not None or out_dtype != torch.bfloat16 or N % 16):
+        raise ValueError("gemm_bf16: the SwiGLU epilogue writes bf16, takes no bias and needs N % 16 == 0")
     defer = defer and not swiglu and bias is None and out_dtype == torch.bfloat16 and M > 0
     S = lib().dkv_gemm_bf16_partials(M, N, K) if defer else 0
     nbytes = lib().dkv_gemm_bf16_workspace(M, N, K)

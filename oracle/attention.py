@@ -48,3 +48,27 @@ def row_mass(mass_probs: np.ndarray) -> np.ndarray:
     """What ``note_attention`` adds to each row's score (compress.py:148): the
     float32 sum over (queries, heads)."""
     return mass_probs.sum(axis=(0, 1))
+
+
+def attend_blas(q, ck, cv, cpos, pos, n_rep: int = 1):
+    """``attend``'s output through matrix products instead of ``einsum`` (no
+    GQA repeat: each KV head's query rows are multiplied as one block), for
+    benchmark-size checks where the einsum loops take minutes. Same
+    promotion: scores in float64 when q or the keys are float64, else float32
+    then float64 after the division by sqrt(D); softmax in float64; float32
+    probabilities times V. Only the order of the float32 additions differs
+    from ``attend`` (within float32 rounding of it, checked on the CPU).
+    Returns out (T, H, D)."""
+    T, H, D = q.shape
+    Tk, Hkv = ck.shape[0], ck.shape[1]
+    if H != Hkv * n_rep:
+        raise ValueError("query heads must be n_rep times the KV heads")
+    qg = np.ascontiguousarray(q.reshape(T, Hkv, n_rep, D).transpose(1, 0, 2, 3).reshape(Hkv, T * n_rep, D))
+    s = np.matmul(qg, np.ascontiguousarray(ck.transpose(1, 2, 0)))          # (Hkv, T*n_rep, Tk)
+    s = s.reshape(Hkv, T, n_rep, Tk).transpose(1, 0, 2, 3).reshape(T, H, Tk) / np.sqrt(D)
+    masked = np.asarray(cpos)[None, :] > np.asarray(pos)[:, None]
+    s = np.where(masked[:, None, :], -np.inf, s)
+    probs = softmax64(s, axis=-1).astype(np.float32)
+    pg = np.ascontiguousarray(probs.reshape(T, Hkv, n_rep, Tk).transpose(1, 0, 2, 3).reshape(Hkv, T * n_rep, Tk))
+    out = np.matmul(pg, np.ascontiguousarray(cv.transpose(1, 0, 2)))       # (Hkv, T*n_rep, D)
+    return out.reshape(Hkv, T, n_rep, D).transpose(1, 0, 2, 3).reshape(T, H, D)

@@ -6,6 +6,11 @@
 
 Each ``forward(tokens, cache, start_pos)`` appends K/V to ``cache`` and reads
 it back exactly as the reference does, so it runs against either oracle cache.
+``GPT2`` and ``LlamaLike`` take an optional ``act_round`` (e.g. ``bf16_round``)
+that models a bf16 forward's storage points -- every matrix product's inputs
+and result, and the K/V rows cached -- in otherwise unchanged arithmetic; it
+measures how far bf16 storage alone moves the logits. Without it the forward
+is the reference's.
 The weight initialisers consume ``np.random.default_rng(seed)`` in the
 reference's order, so a given seed yields the reference's weights.
 """
@@ -38,6 +43,21 @@ def silu(x):                                  # llama.py:102-103
 def rotate_half(x):                           # llama.py:106-109
     h = x.shape[-1] // 2
     return np.concatenate([-x[..., h:], x[..., :h]], axis=-1)
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round to the nearest bfloat16 value, ties to even (the top 16 bits of a
+    float32 after adding 0x7FFF plus the lowest kept bit); float32 result.
+    Inputs in float64 are first rounded to float32. Used by the forwards'
+    ``act_round`` to model a bf16 device forward's storage points; the
+    reference itself has no bf16 arithmetic."""
+    u = np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def _keep(x):
+    return x
 
 
 def sinusoidal(n: int, d: int) -> np.ndarray:   # model.py:86-94
@@ -110,7 +130,8 @@ def demo_model(seed: int = 1, **kw) -> TinyTransformer:     # model.py:143-156
 class GPT2:
     """gpt2.py:130-213 (LayerNorm, fused QKV Conv1D ``x @ W``, GELU-tanh, tied head)."""
 
-    def __init__(self, weights: dict, config: dict):
+    def __init__(self, weights: dict, config: dict, act_round=None):
+        self.r = act_round or _keep     # applied to every matrix product's input and output, and K/V
         self.n_layers = config["n_layer"]
         self.n_heads = config["n_head"]
         self.n_kv_heads = self.n_heads
@@ -139,19 +160,36 @@ class GPT2:
         pos = np.arange(start_pos, start_pos + T)
         h = self.wte[tokens] + self.wpe[pos]
         H, D = self.n_heads, self.d_head
+        r = self.r
+        if r is _keep:
+            for L, p in enumerate(self.blocks):
+                x = layer_norm(h, p["ln1w"], p["ln1b"], self.eps)
+                qkv = x @ p["qkvw"] + p["qkvb"]
+                q, k, v = np.split(qkv, 3, axis=-1)
+                q, k, v = q.reshape(T, H, D), k.reshape(T, H, D), v.reshape(T, H, D)
+                cache.append(L, k, v, pos)
+                ck, cv, cpos = cache.read(L)
+                attn, _, mp = attend(q, ck, cv, cpos, pos)
+                cache.note_attention(L, mp)
+                h = h + attn.reshape(T, H * D) @ p["ow"] + p["ob"]
+                x = layer_norm(h, p["ln2w"], p["ln2b"], self.eps)
+                h = h + gelu_new(x @ p["fcw"] + p["fcb"]) @ p["pw"] + p["pb"]
+            h = layer_norm(h, self.lnfw, self.lnfb, self.eps)
+            return (h @ self.wte.T).astype(np.float32)
+        # the same forward with every product's operands and result passed through r
         for L, p in enumerate(self.blocks):
-            x = layer_norm(h, p["ln1w"], p["ln1b"], self.eps)
-            qkv = x @ p["qkvw"] + p["qkvb"]
+            x = r(layer_norm(h, p["ln1w"], p["ln1b"], self.eps))
+            qkv = r(x @ p["qkvw"]) + p["qkvb"]
             q, k, v = np.split(qkv, 3, axis=-1)
-            q, k, v = q.reshape(T, H, D), k.reshape(T, H, D), v.reshape(T, H, D)
+            q, k, v = q.reshape(T, H, D), r(k.reshape(T, H, D)), r(v.reshape(T, H, D))
             cache.append(L, k, v, pos)
             ck, cv, cpos = cache.read(L)
             attn, _, mp = attend(q, ck, cv, cpos, pos)
             cache.note_attention(L, mp)
-            h = h + attn.reshape(T, H * D) @ p["ow"] + p["ob"]
-            x = layer_norm(h, p["ln2w"], p["ln2b"], self.eps)
-            h = h + gelu_new(x @ p["fcw"] + p["fcb"]) @ p["pw"] + p["pb"]
-        h = layer_norm(h, self.lnfw, self.lnfb, self.eps)
+            h = h + r(r(attn.reshape(T, H * D)) @ p["ow"]) + p["ob"]
+            x = r(layer_norm(h, p["ln2w"], p["ln2b"], self.eps))
+            h = h + r(r(gelu_new(r(x @ p["fcw"]) + p["fcb"])) @ p["pw"]) + p["pb"]
+        h = r(layer_norm(h, self.lnfw, self.lnfb, self.eps))
         return (h @ self.wte.T).astype(np.float32)
 
 
@@ -188,8 +226,9 @@ def gpt2_random_weights(cfg: dict, seed: int = 0, std: float = 0.02) -> dict:
 class LlamaLike:
     """llama.py:112-225 (RMSNorm, RoPE with float64 tables, GQA by repeat, SwiGLU)."""
 
-    def __init__(self, weights: dict, config: dict):
+    def __init__(self, weights: dict, config: dict, act_round=None):
         c = config
+        self.r = act_round or _keep     # applied to every matrix product's input and output, and K/V
         self.n_layers = c["num_hidden_layers"]
         self.d_model = c["hidden_size"]
         self.n_heads = c["num_attention_heads"]
@@ -231,6 +270,8 @@ class LlamaLike:
         H, KV, D = self.n_heads, self.n_kv_heads, self.d_head
         cos, sin = self.rope(pos)
         cos, sin = cos[:, None, :], sin[:, None, :]
+        if self.r is not _keep:
+            return self._forward_rounded(h, cache, pos, cos, sin)
         for L, p in enumerate(self.layers):
             x = rms_norm(h, p["n1"], self.eps)
             q, k, v = x @ p["q"].T, x @ p["k"].T, x @ p["v"].T
@@ -247,6 +288,31 @@ class LlamaLike:
             x = rms_norm(h, p["n2"], self.eps)
             h = h + (silu(x @ p["gate"].T) * (x @ p["up"].T)) @ p["down"].T
         h = rms_norm(h, self.final_norm, self.eps)
+        return (h @ self.head.T).astype(np.float32)
+
+
+    def _forward_rounded(self, h, cache, pos, cos, sin):
+        """``forward`` with every matrix product's operands and result, and the
+        K/V rows appended, passed through ``self.r``."""
+        r, T = self.r, h.shape[0]
+        H, KV, D = self.n_heads, self.n_kv_heads, self.d_head
+        for L, p in enumerate(self.layers):
+            x = r(rms_norm(h, p["n1"], self.eps))
+            q, k, v = r(x @ p["q"].T), r(x @ p["k"].T), r(x @ p["v"].T)
+            if p["qb"] is not None:
+                q, k, v = q + p["qb"], k + p["kb"], v + p["vb"]
+            q, k, v = q.reshape(T, H, D), k.reshape(T, KV, D), v.reshape(T, KV, D)
+            q = q * cos + rotate_half(q) * sin
+            k = r(k * cos + rotate_half(k) * sin)
+            v = r(v)
+            cache.append(L, k, v, pos)
+            ck, cv, cpos = cache.read(L)
+            attn, _, mp = attend(q, ck, cv, cpos, pos, self.n_rep)
+            cache.note_attention(L, mp)
+            h = h + r(r(attn.reshape(T, H * D)) @ p["o"].T) + (p["ob"] if p["ob"] is not None else 0.0)
+            x = r(rms_norm(h, p["n2"], self.eps))
+            h = h + r(r(silu(r(x @ p["gate"].T)) * r(x @ p["up"].T)) @ p["down"].T)
+        h = r(rms_norm(h, self.final_norm, self.eps))
         return (h @ self.head.T).astype(np.float32)
 
 

@@ -7,7 +7,7 @@ The reference samples with ``rng.choice(V, p=p/s)``. numpy's Generator
 implements that as ``searchsorted(cdf, rng.random(), side="right")`` with
 ``cdf = cumsum(p); cdf /= cdf[-1]`` -- one 64-bit draw per call, also when p
 is one-hot. ``sample_u`` takes that uniform explicitly so the oracle and the
-HIP accept kernel can be fed the same draw; ``tests/test_oracle_sampling.py``
+HIP accept kernel can be fed the same draw; ``tests/test_oracle_engine.py``
 pins the equivalence by running numpy.
 """
 

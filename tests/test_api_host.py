@@ -210,3 +210,50 @@ def test_tiled_weight_layout_and_round_trip():
         assert not ops.tile_ok(bad)
         with pytest.raises(ValueError):
             ops.TiledW(bad)
+
+
+class _Made(Exception):
+    pass
+
+
+class _StubModel:
+    """Just enough of a model for the engine to size a full cache: records
+    new_cache's arguments and stops there (no device needed)."""
+
+    vocab_size, n_kv_heads = 1000, 8
+
+    def __init__(self):
+        self.calls = []
+
+    def new_cache(self, **kw):
+        self.calls.append(kw)
+        raise _Made
+
+
+@pytest.mark.parametrize("plen,n_new,gamma", [(22000, 1024, 20), (22000, 1024, None), (4000, 300, 8),
+                                              (130000, 256, 16)])
+def test_baseline_and_speculative_caches_share_the_key_chunk(plen, n_new, gamma):
+    """Plain and speculative decoding of one request size their full caches
+    differently (16 rows of slack vs the longest draft), but the attention
+    key chunk -- which fixes how a row's chunk partials are merged -- comes
+    from what both share, so greedy speculative output can equal the
+    baseline bit for bit."""
+    from draftkv import DraftKVEngine, FixedPolicy
+    from draftkv.paged import auto_chunk_keys
+
+    class NoBound:
+        def select(self, ctx, key=None):
+            return CompressionConfig(4, 0.5), 20
+
+        def update(self, *a, **k):
+            pass
+
+    m = _StubModel()
+    ctrl = FixedPolicy(CompressionConfig(4, 0.5), gamma) if gamma is not None else NoBound()
+    eng = DraftKVEngine(m, ctrl)
+    prompts = [[1] * plen] * 32
+    for call in (lambda: eng.generate_baseline_batch(prompts, n_new), lambda: eng.generate_batch(prompts, n_new)):
+        with pytest.raises(_Made):
+            call()
+    base, spec = m.calls
+    assert base["chunk_keys"] == spec["chunk_keys"] == auto_chunk_keys(32, 8, plen + n_new)

@@ -17,6 +17,12 @@ build, an arm switch, a draft step with eviction by the accumulated mass,
 and the rollback resync. Attention: 2e-3 relative / 1e-3 absolute against
 the float32 oracle; attention mass: 1e-4 relative.
 
+The verify pass (gamma + 1 query rows per sequence over
+the full bf16 cache) is checked at the same shape with the cache's own key
+chunk (8192 keys: four chunk partials merged per row) for T = 1, 9 and 17
+rows, which run the MFMA kernel with 1, 4 and 8 waves; and at batch 1 with
+262144 positions (2048-key chunks, 128 partials per row) for T = 17.
+
 The oracle quantizes only the kept rows of a build: its quantizer works row
 by row (compress.py:38-43), so that equals quantizing every row and then
 evicting (checked on the CPU in test_oracle_caches.py).
@@ -29,7 +35,7 @@ import pytest
 import torch
 
 from oracle import caches as oc
-from oracle.attention import attend, row_mass
+from oracle.attention import attend, attend_blas, row_mass
 from oracle.config import Cfg, budget, closed_form_kept
 from oracle.quant import quantize_codes
 
@@ -232,3 +238,70 @@ def test_draft_step_eviction_and_resync_match_oracle(dev, cache):
 
     kept = list(_POOL.map(one, range(B)))
     assert md.rows()[:, LAYER].tolist() == kept
+
+
+@pytest.mark.parametrize("T", [1, 9, 17])
+def test_verify_attention_matches_oracle(dev, cache, T):
+    """T query rows per sequence at positions n-T .. n-1 over keys 0 .. own
+    position of the benchmark cache (ragged ~32k rows, shuffled 16-token bf16
+    pages), with the key chunk the cache picks for its shape: every sequence
+    within 2e-3 / 1e-3 of the oracle (llama.py:202-218 via engine.py:184-185).
+    T = 1, 9, 17 make 1, 3, 5 sixteen-row query tiles, so the kernel runs with
+    1, 4 and 8 waves per workgroup."""
+    full, host = cache
+    assert full.chunk_keys == 8192
+    rng = np.random.default_rng(20 + T)
+    q = rng.standard_normal((B, T, HQ, D)).astype(np.float32)
+    start = torch.tensor(LENS - T, dtype=torch.int32, device=dev)
+    out = full.attend(LAYER, torch.from_numpy(q).to(dev), start, int(LENS.max())).cpu().numpy()
+
+    def one(s):
+        n = int(LENS[s])
+        k, v = host[0][s, :n].float().numpy(), host[1][s, :n].float().numpy()
+        ref = attend_blas(q[s], k, v, np.arange(n), np.arange(n - T, n), HQ // HKV)
+        np.testing.assert_allclose(out[s], ref, rtol=RTOL, atol=ATOL, err_msg=f"T {T} seq {s}")
+        return s
+
+    assert sorted(_POOL.map(one, range(B))) == list(range(B))
+
+
+def test_verify_attention_long_context_matches_oracle(dev):
+    """Batch 1 with 262144 positions (the long-context workload) in
+    shuffled 16-token bf16 pages: the cache's key chunk is 2048, so each of
+    the 17 query rows merges up to 128 chunk partials. Every row and head
+    within 2e-3 / 1e-3 of the oracle."""
+    import draftkv
+    ctx, T = 262144, 17
+    maxt = ctx + 64
+    full = draftkv.PagedKVCache(1, HKV, D, 16, maxt // 16, "bf16", batch=1, max_tokens=maxt)
+    assert full.chunk_keys == 2048
+    rng = np.random.default_rng(5)
+    rng.shuffle(full.pools[0]._stack)
+    full.reserve([ctx])
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    kv = []
+    for _ in range(2):
+        x = torch.randn((1, ctx, HKV, D), generator=g, device=dev, dtype=torch.float32)
+        x[..., [5, 77]] *= 8.0
+        kv.append(x.bfloat16())
+        del x
+    full.append_layer(0, kv[0], kv[1], torch.zeros(1, dtype=torch.int32, device=dev),
+                      torch.tensor([ctx], dtype=torch.int32, device=dev))
+    full.commit([ctx])
+    k, v = kv[0][0].float().cpu().numpy(), kv[1][0].float().cpu().numpy()
+    del kv
+    q = rng.standard_normal((1, T, HQ, D)).astype(np.float32)
+    start = torch.tensor([ctx - T], dtype=torch.int32, device=dev)
+    out = full.attend(0, torch.from_numpy(q).to(dev), start, ctx).cpu().numpy()[0]
+    del full
+    torch.cuda.empty_cache()
+    rep = HQ // HKV
+
+    def one(h):   # one KV head and its query group at a time
+        ref = attend_blas(q[0][:, h * rep:(h + 1) * rep], k[:, h:h + 1], v[:, h:h + 1], np.arange(ctx),
+                          np.arange(ctx - T, ctx), rep)
+        np.testing.assert_allclose(out[:, h * rep:(h + 1) * rep], ref, rtol=RTOL, atol=ATOL, err_msg=f"KV head {h}")
+        return h
+
+    assert sorted(_POOL.map(one, range(HKV))) == list(range(HKV))

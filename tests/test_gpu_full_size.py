@@ -12,8 +12,8 @@ N(0, 0.02)) over a synthetic full cache written straight into shuffled
 No oracle runs a model of this size; the checks are the properties the
 reference's own tests use: greedy speculative output equals plain full-KV
 decoding on the same cache (tests/test_lossless.py:28-35), across the arm
-switch, and a temperature-1.0 run decodes valid tokens with accepted runs
-within gamma.
+switch, and temperature-0.8 (batch 32) and temperature-1.0 (batch 1) runs
+decode valid tokens with accepted runs within gamma.
 """
 
 import gc
@@ -126,6 +126,18 @@ def test_b32_ctx32k_greedy_lossless_across_arm_switches(dev, model):
     full.truncate(ctx - 1)
     base = _greedy_full_kv(model, full, toks, n_new)
     assert np.array_equal(spec, base)
+    # temperature 0.8 rejection sampling (the benchmark's operating point),
+    # longer drafts, both arms: every sequence decodes in-vocabulary tokens
+    # with accepted runs within gamma, from its own random stream
+    full.truncate(ctx - 1)
+    res = _speculative(model, full, toks, Switch(arms, 8, 2), 24, 0.8, arms, seed=11)
+    for r in res:
+        assert len(r.tokens) == ctx + 24
+        assert all(0 <= t < model.vocab_size for t in r.tokens[ctx:])
+        assert all(0 <= x.accepted <= x.gamma and x.emitted == x.accepted + 1 for x in r.rounds)
+        assert sum(x.emitted for x in r.rounds) >= 24
+    assert {x.cfg for x in res[0].rounds} == set(arms)
+    assert len({tuple(r.tokens[ctx:]) for r in res}) == b     # every sequence its own stream
     del full
     gc.collect()
     torch.cuda.empty_cache()

@@ -361,6 +361,42 @@ def test_sample_matches_numpy_choice(dev, V, T):
         assert tok[s] == sample_u(o_probs(logits[s], T), u[s]), s
 
 
+def _accept_case(ops, dev, b, gamma, V, T, seed):
+    """Target rows near a shared base, draft rows near it too, drafted tokens
+    mostly the target's argmax (long accepted runs) and sometimes not; the
+    device decision against the oracle rule for every sequence."""
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal((b, 1, V)).astype(np.float32) * 2
+    target = (base + 0.3 * rng.standard_normal((b, gamma + 1, V))).astype(np.float32)
+    draft = (base[:, :1] + 0.3 * rng.standard_normal((b, gamma, V))).astype(np.float32)
+    toks = np.zeros((b, gamma), np.int32)
+    for s in range(b):
+        for i in range(gamma):
+            toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.95 else int(rng.integers(V))
+    u = rng.random((b, gamma + 1))
+    acc, nxt, used = ops.accept(torch.from_numpy(target).to(dev), torch.from_numpy(draft).to(dev),
+                                torch.from_numpy(toks).to(dev), T, torch.from_numpy(u).to(dev))
+    acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
+    for s in range(b):
+        qs = [o_probs(draft[s, i], T) for i in range(gamma)]
+        ra, rn, ru = o_accept(target[s], toks[s].tolist(), qs, T, u[s])
+        assert (acc[s], nxt[s], used[s]) == (ra, rn, ru), (s, (acc[s], nxt[s], used[s]), (ra, rn, ru))
+    return acc
+
+
+@pytest.mark.parametrize("T", [0.0, 0.8])
+@pytest.mark.parametrize("b,gamma", [(32, 8), (32, 16), (32, 20), (4, 80)])
+def test_accept_matches_reference_rule_at_bench_points(dev, T, b, gamma):
+    """Where the benchmark runs the decision: batch 32, the Llama-3-8B
+    vocabulary (128256), gamma up to the bench's 20, greedy and T = 0.8; and
+    a draft longer than one 64-position block of the decide kernel. Accepted
+    counts, next tokens and uniforms consumed equal the oracle rule's
+    (engine.py:188-213) for every sequence."""
+    _, ops = _dk()
+    acc = _accept_case(ops, dev, b, gamma, 128256, T, 1000 + gamma + int(T * 10))
+    assert acc.max() > 0
+
+
 @pytest.mark.parametrize("T", [0.0, 0.8])
 @pytest.mark.parametrize("gamma", [1, 4, 8])
 def test_accept_matches_reference_rule(dev, T, gamma):

@@ -128,7 +128,10 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
                                              (32, 4096, 4096, True), (33, 512, 14336, False),
                                              (96, 6144, 4096, True), (200, 1024, 2048, False), (64, 272, 96, True),
                                              (544, 4096, 4096, False), (32, 28672, 4096, True),
-                                             (96, 28672, 4096, False)])
+                                             (96, 28672, 4096, False),
+                                             # W ending inside a 16-row fragment (a tied GPT-2 head: 50257 rows)
+                                             (1, 50257, 768, False), (5, 50257, 768, True), (33, 50257, 768, False),
+                                             (3, 40, 4096, True), (96, 1001, 2048, True), (17, 23, 96, True)])
 def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     """bf16 x @ W^T (+ b) against the float32 product of the same bf16 values
     (one rounding to bf16 apart), float32 output too, and every row equal to
@@ -137,8 +140,10 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     of 16 to 128 rows, several M tiles, K chunks split over workgroups
     (partials + ordered reduce) or summed inside one, the small-M kernel that
     splits K among the waves of a workgroup, 128-k blocks and the 32-k
-    tail, and the 7-wave workgroups of the 28672-row gate/up weight (whose
-    rows must equal those of the 4-wave plan at M = 96)."""
+    tail, the 7-wave workgroups of the 28672-row gate/up weight (whose
+    rows must equal those of the 4-wave plan at M = 96), and any N: a last
+    fragment of fewer than 16 W rows (odd N: element stores) in the main and
+    the small-M kernels."""
     ops = _ops()
     g = torch.Generator(device=dev).manual_seed(M + N + K)
     x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
@@ -287,7 +292,7 @@ def test_gemm_bf16_rejects_unsupported_operands(dev):
     ops = _ops()
     x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError):
-        ops.gemm_bf16(x, torch.zeros((40, 64), dtype=torch.bfloat16, device=dev))    # N % 16
+        ops.gemm_bf16(x, torch.zeros((40, 64), dtype=torch.bfloat16, device=dev), swiglu=True)   # SwiGLU: N % 16
     with pytest.raises(ValueError):
         ops.gemm_bf16(x[:, :48].contiguous(), torch.zeros((32, 48), dtype=torch.bfloat16, device=dev))   # K % 32
     with pytest.raises(ValueError):

@@ -214,6 +214,18 @@ def test_batched_long_drafts_with_uneven_progress_fit_the_caches(dev, tiny_setup
     assert max(x.gamma for r in res for x in r.rounds) >= 18
 
 
+def test_draft_longer_than_64_is_lossless(dev, tiny_setup):
+    """FixedPolicy(cfg, 80), which the reference accepts: rounds draft up to
+    80 tokens (the accept kernel decides any gamma) and the output equals
+    plain decoding."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy
+    m, prompt, _ = tiny_setup
+    base = DraftKVEngine(m, seed=0).generate_baseline(prompt, 100, 0.0)
+    r = DraftKVEngine(m, FixedPolicy(CompressionConfig(8, 1.0), 80), seed=0).generate(prompt, 100, 0.0)
+    assert r.tokens == base
+    assert r.rounds[0].gamma == 80
+
+
 class _Adaptive:
     """A test-local controller (the select/update protocol): cycles through the
     arms, lengthens the draft after a fully accepted round and shortens it
@@ -278,6 +290,29 @@ def test_bf16_greedy_output_identical(dev, attn_bias):
                        (CompressionConfig(2, 0.25), 4)):
         r = DraftKVEngine(g, FixedPolicy(cfg, gamma), seed=0).generate(prompt, 40, 0.0)
         assert r.tokens == base, f"bf16 {cfg.label()} gamma={gamma} diverged from full-KV decoding"
+
+
+def test_bf16_gpt2_tied_head_batch_invariant_and_lossless(dev):
+    """A bf16 GPT-2 of distilgpt2's width whose head is the tied 50257-row
+    embedding (gpt2.py:213): the library GEMM takes the head's last partial
+    16-row fragment, verify rows equal one-token decode rows bit for bit, and
+    greedy speculative output equals full-KV decoding."""
+    from draftkv import CompressionConfig, DraftKVEngine, FixedPolicy, gpt2
+    cfg = dict(gpt2.DISTILGPT2, n_layer=2)
+    g = gpt2.GPT2.random(cfg, seed=0, std=0.05, dtype=torch.bfloat16)
+    assert g.head is g.emb and g.head.shape[0] == 50257
+    toks = np.array(_prompt(8, 40, 50257))
+    a, b = g.new_cache(), g.new_cache()
+    g.forward(toks[:31], a, 0)
+    g.forward(toks[:31], b, 0)
+    block = g.forward(toks[31:], a, 31)
+    rows = np.stack([g.forward(toks[31 + i: 32 + i], b, 31 + i)[0] for i in range(9)])
+    assert np.array_equal(block.view(np.uint32), rows.view(np.uint32))
+    prompt = _prompt(9, 120, 50257)
+    base = DraftKVEngine(g, seed=0).generate_baseline(prompt, 24, 0.0)
+    for cfg_, gamma in ((CompressionConfig(8, 1.0), 4), (CompressionConfig(4, 0.5, group=32, scale_fp16=True), 6)):
+        r = DraftKVEngine(g, FixedPolicy(cfg_, gamma), seed=0).generate(prompt, 24, 0.0)
+        assert r.tokens == base, f"bf16 gpt2 {cfg_.label()} gamma={gamma}"
 
 
 def test_bf16_llama_runs_and_is_self_consistent(dev):

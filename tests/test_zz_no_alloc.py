@@ -57,10 +57,22 @@ def test_noalloc_equals_workspace_entry_point_twice(dev, T):
 
 
 def test_noalloc_refuses_more_than_the_scratch(dev):
+    """A request whose workspace exceeds the static scratch is refused with
+    DKV_ECAPACITY before any launch. Its inputs and outputs are real device
+    tensors of the request's sizes: what is tested is the refusal, never a
+    launch on pointers that do not hold the data."""
     from draftkv._lib import lib
     L = lib()
-    nbytes = L.dkv_accept_workspace(4096, 24, 128256)
+    b, gamma, V = 2048, 24, 4096
+    nbytes = L.dkv_accept_workspace(b, gamma, V)
     assert nbytes > (4 << 20)
-    rc = L.dkv_accept_noalloc(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), 4096, 24, 128256, 0.8,
-                              C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), None)
+    target = torch.zeros((b, gamma + 1, V), dtype=torch.float32, device=dev)
+    draft = torch.zeros((b, gamma, V), dtype=torch.float32, device=dev)
+    toks = torch.zeros((b, gamma), dtype=torch.int32, device=dev)
+    u = torch.zeros((b, gamma + 1), dtype=torch.float64, device=dev)
+    outs = [torch.zeros(b, dtype=torch.int32, device=dev) for _ in range(3)]
+    rc = L.dkv_accept_noalloc(target.data_ptr(), draft.data_ptr(), toks.data_ptr(), b, gamma, V, 0.8, u.data_ptr(),
+                              *(o.data_ptr() for o in outs), None)
+    torch.cuda.synchronize()
     assert rc == -4 and b"static scratch" in L.dkv_last_error()
+    assert all(not o.any() for o in outs)     # nothing ran
