@@ -999,10 +999,19 @@ __device__ __forceinline__ float lane_select_tr(float f, float t, uint64_t mask)
     return r;
 }
 
-template <int MF, int LPP>
+// SPLIT: a segment is cut into nb blocks of whole pages (gridDim.x = nb;
+// for batches whose segments alone do not fill the chip). A block then
+// leaves its merged partial (o, max, sum) per query head in part
+// [b][Hkv][nb][G][D+2], and instead of the per-KV-head mass the kept
+// probabilities against its merged max, per query head, in pmass
+// [b][Hkv][cap][G] (pmass may be the spill buffer: a page's 512 bytes there
+// are read, then written, by the one wave that owns it);
+// draft_seg_merge_kernel merges the blocks and adds the mass.
+template <int MF, int LPP, bool SPLIT>
 __global__ void __launch_bounds__(64 * SEG_WAVES, 1) __attribute__((amdgpu_num_vgpr(SEG_VGPRS)))
 draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* __restrict__ q, int Hq, float scale,
-                      float* __restrict__ out, float* __restrict__ spill, float* __restrict__ pmass) {
+                      float* __restrict__ out, float* __restrict__ spill, float* __restrict__ pmass, int nb,
+                      float* __restrict__ part) {
     constexpr int D = 128, CB = 4, G = 4;
     using Core = SplitCore<D, CB, MF>;
     using Regs = typename Core::Regs;
@@ -1014,20 +1023,29 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
     const int h = blockIdx.y, s = blockIdx.z;
     const int Hkv = m.n_kv_heads;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
-    const int np = (n + PAGE - 1) / PAGE;
+    const int np_seg = (n + PAGE - 1) / PAGE;
+    // the block's pages [b0, b0 + np): the whole segment, or (SPLIT) its
+    // share of ceil(np_seg / nb) pages
+    int b0 = 0, np = np_seg;
+    if constexpr (SPLIT) {
+        const int ppb = (np_seg + nb - 1) / nb;
+        b0 = blockIdx.x * ppb;
+        np = min(np_seg - b0, ppb);
+        if (np <= 0) return;   // a block past the segment's end (its partial is never read)
+    }
     // contiguous page runs; with at least 64 pages, waves 0-3 (the older
     // wave of each SIMD, which wins issue by age) take SEG_OLD/16 of them
     // (every wave keeps at least 4 pages for SEG_OLD <= 12)
     const int A = min(SEG_WAVES, np);
     const bool active = wave < A;
     auto cut = [&](int w) -> int {
-        if (A < SEG_WAVES || np < 64) return (int)(((int64_t)w * np) / A);   // every wave >= 1 page
+        if (SPLIT || A < SEG_WAVES || np < 64) return (int)(((int64_t)w * np) / A);   // every wave >= 1 page
         const int c = w <= 4 ? w * SEG_OLD : 4 * SEG_OLD + (w - 4) * (16 - SEG_OLD);   // in 64ths
         return (int)(((int64_t)c * np) / 64);
     };
-    const int pg0 = active ? cut(wave) : 0;
-    const int T = active ? cut(wave + 1) - pg0 : 0;
-    const bool tail = wave == A - 1 && n % PAGE != 0;
+    const int pg0 = active ? b0 + cut(wave) : 0;
+    const int T = active ? b0 + cut(wave + 1) - pg0 : 0;
+    const bool tail = wave == A - 1 && b0 + np == np_seg && n % PAGE != 0;
     const bool keep = pmass != nullptr;
     extern __shared__ __align__(16) char dma_smem[];
     Core c;
@@ -1189,10 +1207,21 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
             l = fmaf(lc, wt, l);
             o = fmaf(ph[w * PD + d], wt, o);
         }
-        __builtin_nontemporal_store((l > 0.0f) ? o / l : 0.0f, &out[((int64_t)s * Hq + h * G + hl) * D + d]);
-        if (d == 0) {
-            sst[2 * hl] = mm;
-            sst[2 * hl + 1] = l > 0.0f ? 1.0f / l : 0.0f;
+        if constexpr (SPLIT) {
+            float* pp = part + ((((int64_t)s * Hkv + h) * nb + blockIdx.x) * G + hl) * PD;
+            pp[d] = o;
+            if (d == 0) {
+                pp[D] = mm;
+                pp[D + 1] = l;
+                sst[2 * hl] = mm;
+                sst[2 * hl + 1] = 1.0f;   // kept values against the block's max, unnormalised
+            }
+        } else {
+            __builtin_nontemporal_store((l > 0.0f) ? o / l : 0.0f, &out[((int64_t)s * Hq + h * G + hl) * D + d]);
+            if (d == 0) {
+                sst[2 * hl] = mm;
+                sst[2 * hl + 1] = l > 0.0f ? 1.0f / l : 0.0f;
+            }
         }
     }
     if (!keep) return;
@@ -1202,6 +1231,28 @@ draft_attn_seg_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* _
     // quad of the KV head's 4 query heads (lanes hcol 0..3 of a group column);
     // the kept values are exp(logit - the wave's reference), so p is a kept
     // value times exp(reference - max) / sum
+    if constexpr (SPLIT) {
+        // every kept value against the block's max, per query head: lane
+        // (gcol, hcol, jj) holds rows 4jj + gcol and 16 + 4jj + gcol of each
+        // page for head hcol, stored at [row][hcol] (a quad's four heads of a
+        // row are 16 contiguous bytes)
+        const float fac = __expf(c.m_run - sst[2 * c.hcol]);
+        float* pr = pmass + ((int64_t)(s * Hkv + h) * m.cap + (int64_t)pg0 * PAGE + 4 * c.jj + c.gcol) * G + c.hcol;
+        const float* spill_w = spill + ((int64_t)(s * Hkv + h) * (m.cap / PAGE) + pg0) * (2 * WAVE) + 2 * lane;
+        for (int g = 0; g < T; ++g) {
+            float a, b;
+            if (g < SEG_TMAX) {
+                seg_get(2 * g, a, b);
+            } else {
+                const float2 v = *reinterpret_cast<const float2*>(spill_w + (int64_t)g * (2 * WAVE));
+                a = v.x;
+                b = v.y;
+            }
+            pr[(int64_t)g * PAGE * G] = a * fac;
+            pr[((int64_t)g * PAGE + 16) * G] = b * fac;
+        }
+        return;
+    }
     {
         const float fac = __expf(c.m_run - sst[2 * c.hcol]) * sst[2 * c.hcol + 1];
         const uint64_t hb0 = __ballot((c.hcol & 1) != 0), hb1 = __ballot((c.hcol & 2) != 0);
@@ -1297,6 +1348,111 @@ __global__ void __launch_bounds__(256) draft_mass_sum_kernel(dkv_drafter_t m, in
         for (int hk = 1; hk < m.n_kv_heads; ++hk) t += p[(int64_t)hk * m.cap + k];
         sc[k] += static_cast<double>(t);
     }
+}
+
+// The segment kernel's SPLIT mode, second half. Grid (Hkv + row blocks,
+// batch), 256 threads. Every block first turns the segment blocks' (max,
+// sum) into factors c = exp(max_b - M) / L per (KV head, block, query head)
+// in LDS (M, L: the merged max and sum). Blocks x < Hkv then write KV head
+// x's outputs, sum_b o_b * c_b over the segment blocks in order; the others
+// take SMERGE_ROWS rows each and add to each row's score the sum over KV heads (in
+// order) of that head's mass, the kept values times their block's factors
+// summed over the query heads pairwise.
+constexpr int SMERGE_ROWS = 256;    // rows per block of the mass part (one per thread)
+constexpr int SMERGE_MAX_NB = 64;    // segment blocks
+constexpr int SMERGE_MAX_HKV = 16;   // KV heads
+__global__ void __launch_bounds__(256) draft_seg_merge_kernel(dkv_drafter_t m, int layer, int nb,
+                                                              const float* __restrict__ part,
+                                                              const float* __restrict__ pk, float* __restrict__ out,
+                                                              int want_mass) {
+    constexpr int D = 128, G = 4, PD = D + 2;
+    const int s = blockIdx.y, Hkv = m.n_kv_heads, Hq = Hkv * G;
+    const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    const int np = (n + PAGE - 1) / PAGE;
+    const int ppb = (np + nb - 1) / nb;
+    const int nbl = np > 0 ? (np + ppb - 1) / ppb : 0;   // blocks that hold pages
+    const bool merge = (int)blockIdx.x < Hkv;
+    if (!merge && (!want_mass || ((int)blockIdx.x - Hkv) * SMERGE_ROWS >= n)) return;
+    __shared__ float sm[SMERGE_MAX_HKV * SMERGE_MAX_NB * G], sl[SMERGE_MAX_HKV * SMERGE_MAX_NB * G];
+    const int h_lo = merge ? blockIdx.x : 0, h_hi = merge ? blockIdx.x + 1 : Hkv;
+    const int nh = h_hi - h_lo, cnt = nh * nbl * G;   // (head, block, query head) entries
+    for (int i = threadIdx.x; i < cnt; i += blockDim.x) {
+        const int hq = i % G, b = (i / G) % nbl, hh = i / (G * nbl);
+        const float* pp = part + ((((int64_t)s * Hkv + h_lo + hh) * nb + b) * G + hq) * PD;
+        sm[i] = pp[D];
+        sl[i] = pp[D + 1];
+    }
+    __syncthreads();
+    // the merged (max, 1/sum) of each (head, query head): 4 lanes per pair
+    // (up to 64 pairs), each over every 4th block, then two xor shuffles
+    // (the same values and order in every block of the grid)
+    __shared__ float sM[SMERGE_MAX_HKV * G], siL[SMERGE_MAX_HKV * G];
+    {
+        const int pr = threadIdx.x / 4, sub = threadIdx.x % 4;
+        const bool live = pr < nh * G;
+        const int hh = live ? pr / G : 0, hq = pr % G;
+        float M = -INFINITY;
+        if (live)
+            for (int b = sub; b < nbl; b += 4) M = fmaxf(M, sm[(hh * nbl + b) * G + hq]);
+        M = fmaxf(M, __shfl_xor(M, 1));
+        M = fmaxf(M, __shfl_xor(M, 2));
+        float L = 0.0f;
+        if (live)
+            for (int b = sub; b < nbl; b += 4) {
+                const float mb = sm[(hh * nbl + b) * G + hq];
+                L = fmaf(sl[(hh * nbl + b) * G + hq], mb == -INFINITY ? 0.0f : __expf(mb - M), L);
+            }
+        L += __shfl_xor(L, 1);
+        L += __shfl_xor(L, 2);
+        if (live && sub == 0) {
+            sM[pr] = M;
+            siL[pr] = L > 0.0f ? 1.0f / L : 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < cnt; i += blockDim.x) {
+        const int hq = i % G, hh = i / (G * nbl);
+        const float mb = sm[i];
+        sm[i] = mb == -INFINITY ? 0.0f : __expf(mb - sM[hh * G + hq]) * siL[hh * G + hq];
+    }
+    __syncthreads();
+    if (merge) {
+        // outputs (query head hq, channel d) of KV head h_lo: two per thread
+        for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+            const int hq = i / D, d = i % D;
+            const float* pp = part + (((int64_t)s * Hkv + h_lo) * nb * G + hq) * PD + d;
+            float o = 0.0f;
+            int b = 0;
+            for (; b + 8 <= nbl; b += 8) {   // 8 partials' loads in flight, then their terms in order
+                float x[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) x[k] = pp[(int64_t)(b + k) * G * PD];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) o = fmaf(x[k], sm[(b + k) * G + hq], o);
+            }
+            for (; b < nbl; ++b) o = fmaf(pp[(int64_t)b * G * PD], sm[b * G + hq], o);
+            out[((int64_t)s * Hq + h_lo * G + hq) * D + d] = o;
+        }
+        return;
+    }
+    const int r = ((int)blockIdx.x - Hkv) * SMERGE_ROWS + threadIdx.x;
+    if (r >= n) return;
+    const int b = (r / PAGE) / ppb;
+    double* score = m.score + row_index(m, s, layer) + r;
+    const double old = *score;
+    // every head's kept values at once (all loads in flight), then the sums in order
+    float4 p[SMERGE_MAX_HKV];
+#pragma unroll
+    for (int hh = 0; hh < SMERGE_MAX_HKV; ++hh)
+        if (hh < Hkv) p[hh] = *reinterpret_cast<const float4*>(pk + (((int64_t)s * Hkv + hh) * m.cap + r) * G);
+    float t = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < SMERGE_MAX_HKV; ++hh)
+        if (hh < Hkv) {
+            const float* c = sm + (hh * nbl + b) * G;
+            t += (p[hh].x * c[0] + p[hh].y * c[1]) + (p[hh].z * c[2] + p[hh].w * c[3]);
+        }
+    *score = old + static_cast<double>(t);
 }
 
 // ---------------------------------------------------------------- combine + mass
@@ -1538,22 +1694,45 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     // alone fill the chip: split-K, merge and the per-KV-head mass in one
     // kernel (4-bit codes, D = 128, 4 query heads and 4 groups per KV head,
     // fp16 meta)
-    if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0 && cfg.bits <= 4 &&
-        m.head_dim == 128 && G == 4 && m.head_dim / cfg.group == 4 && cfg.meta_f16 &&
-        dma_lpp(page_fmt(cfg, 128), 128) == 5 && m.batch * m.n_kv_heads >= 256) {
-        auto kfn = draft_attn_seg_kernel<1, 5>;
-        const size_t lds = (size_t)SEG_WAVES * dma_stages(5) * 5 * 1024;
+    const bool seg_shape = fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                           cfg.bits <= 4 && m.head_dim == 128 && G == 4 && m.head_dim / cfg.group == 4 &&
+                           cfg.meta_f16 && dma_lpp(page_fmt(cfg, 128), 128) == 5;
+    const size_t seg_lds = (size_t)SEG_WAVES * dma_stages(5) * 5 * 1024;
+    if (seg_shape && m.batch * m.n_kv_heads >= 256) {
+        auto kfn = draft_attn_seg_kernel<1, 5, false>;
         static size_t lds_done[16] = {};
-        if (!reserve_lds(reinterpret_cast<const void*>(kfn), lds, lds_done))
-            return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(lds) + " B of LDS");
+        if (!reserve_lds(reinterpret_cast<const void*>(kfn), seg_lds, lds_done))
+            return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(seg_lds) + " B of LDS");
         float* pmass = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.pmass_off) : nullptr;
-        launch_splitk(kfn, dim3(1, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), lds, st, m, (int)layer, cfg, q,
-                      (int)n_q_heads, scale, out, logits, pmass);
+        launch_splitk(kfn, dim3(1, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), seg_lds, st, m, (int)layer, cfg, q,
+                      (int)n_q_heads, scale, out, logits, pmass, 1, static_cast<float*>(nullptr));
         int rc = check_launch("dkv_drafter_attention(segment)");
         if (rc || !want_mass) return rc;
         hipLaunchKernelGGL(draft_mass_sum_kernel, dim3((m.cap + 256 * MSUM_ROWS - 1) / (256 * MSUM_ROWS), m.batch),
                            dim3(256), 0, st, m, layer, pmass);
         return check_launch("dkv_drafter_attention(mass)");
+    }
+    // Segments too few to fill the chip (small batch, long context): each
+    // one cut into nb blocks, at most 256 in all (one block per CU: a second
+    // round of blocks would double the time); the blocks' partials and kept
+    // values (in the partial and logit sections) are merged, and the mass
+    // added, by draft_seg_merge_kernel.
+    // (nb is also bounded by the merge kernel's table and by the partial
+    // section, which holds ns partials per query head)
+    const int nb = std::max(1, std::min(std::min(SMERGE_MAX_NB, ns), 256 / (m.batch * m.n_kv_heads)));
+    if (seg_shape && m.n_kv_heads <= SMERGE_MAX_HKV) {
+        auto kfn = draft_attn_seg_kernel<1, 5, true>;
+        static size_t lds_done[16] = {};
+        if (!reserve_lds(reinterpret_cast<const void*>(kfn), seg_lds, lds_done))
+            return fail(DKV_ELAUNCH, "dkv_drafter_attention: cannot reserve " + std::to_string(seg_lds) + " B of LDS");
+        launch_splitk(kfn, dim3(nb, m.n_kv_heads, m.batch), dim3(64 * SEG_WAVES), seg_lds, st, m, (int)layer, cfg,
+                      q, (int)n_q_heads, scale, out, logits, want_mass ? logits : nullptr, nb, part);
+        int rc = check_launch("dkv_drafter_attention(segment split)");
+        if (rc) return rc;
+        const int row_blocks = want_mass ? (m.cap + SMERGE_ROWS - 1) / SMERGE_ROWS : 0;
+        hipLaunchKernelGGL(draft_seg_merge_kernel, dim3(m.n_kv_heads + row_blocks, m.batch), dim3(256), 0, st, m,
+                           (int)layer, nb, part, logits, out, want_mass);
+        return check_launch("dkv_drafter_attention(segment merge)");
     }
     // the fast path reads q rows with 16-byte vector loads
     if (fast_path(m, cfg, n_q_heads) && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
