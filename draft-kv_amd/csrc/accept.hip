@@ -2,7 +2,8 @@
 // Reference: draftkv/engine.py:36-41 (`_probs`), :101-106 (`_sample`),
 // :188-213 (accept loop, bonus token, residual resample).
 //
-// Pipeline (rows of `vocab` float32 logits, cut in chunks of VCH):
+// Pipeline (rows of `vocab` float32 logits, cut in chunks of VCH; every
+// exp in float64 by the table-driven dexp below):
 //   1. stats   grid (chunk, row, seq): chunk max, first argmax and
 //              sum exp(x/T - max/T) in float64.
 //   2. decide  grid (seq): merge chunk stats per row, run the accept tests
@@ -35,6 +36,50 @@ struct SeqState {
     double u;        // uniform for the final draw
 };
 
+// ---- float64 exp, Tang's table-driven method (ACM TOMS 15(2), 1989):
+// y = (64 e + j) ln2/64 + r with |r| <= ln2/128, exp(y) = 2^e 2^(j/64) exp(r),
+// 2^(j/64) from a table of correctly rounded doubles, exp(r) - 1 by its
+// degree-6 Taylor polynomial (truncation below 3e-20 relative). Within one
+// ulp of a correctly rounded exp for y in [-745, 709]; 0 below (and for
+// -inf). About 15 float64 operations against ~35 for the library's.
+__constant__ double kExp2Tab[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0};
+
+// the table in a block's LDS (callers synchronise before the first dexp)
+__device__ __forceinline__ void load_exp_tab(double* tab) {
+    for (int i = threadIdx.x; i < 64; i += blockDim.x) tab[i] = kExp2Tab[i];
+}
+
+__device__ __forceinline__ double dexp(double y, const double* tab) {
+    if (!(y > -745.5)) return 0.0;
+    const double n = __builtin_rint(y * 0x1.71547652b82fep+6);   // y * 64 / ln2, to nearest
+    double r = fma(-n, 0x1.62e42fefa0000p-7, y);                  // ln2/64 in two parts: n * hi is exact
+    r = fma(-n, 0x1.cf79abc9e3b3ap-46, r);
+    const int ni = (int)n, j = ni & 63, e = (ni - j) >> 6;
+    double q = fma(0x1.6c16c16c16c17p-10, r, 0x1.1111111111111p-7);   // 1/720, 1/120
+    q = fma(q, r, 0x1.5555555555555p-5);                              // 1/24
+    q = fma(q, r, 0x1.5555555555555p-3);                              // 1/6
+    q = fma(q, r, 0.5);
+    const double p = fma(q, r * r, r);                                // exp(r) - 1
+    const double t = tab[j];
+    return ldexp(fma(t, p, t), e);
+}
+
 __device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int s, int row, int gamma,
                                                 int vocab) {
     // rows 0..gamma: target; gamma+1..2*gamma: draft rows 0..gamma-1
@@ -53,6 +98,8 @@ __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ t
     const bool samp = T > 0.0f;
     const int n_rows = samp ? 2 * gamma + 1 : gamma + 1;
     if (row >= n_rows) return;
+    __shared__ double tab[64];
+    load_exp_tab(tab);   // (the max's barrier below precedes every use)
     const float* x = row_ptr(target, draft, s, row, gamma, vocab);
     const int i0 = chunk * VCH, i1 = min(vocab, i0 + VCH);
     __shared__ float smx[ABLK / WAVE];
@@ -98,7 +145,7 @@ __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ t
         const double iT = 1.0 / (double)T, mT = (double)mx * iT;
 #pragma unroll
         for (int k = 0; k < PER; ++k)
-            if (xv[k] > -INFINITY) sum += exp((double)xv[k] * iT - mT);
+            if (xv[k] > -INFINITY) sum += dexp((double)xv[k] * iT - mT, tab);
         sum = wave_sum_d(sum);
         if (threadIdx.x % WAVE == 0) ssum[w] = sum;
         __syncthreads();
@@ -123,8 +170,8 @@ struct RowNorm {
 
 // p(x) = exp(x/T - m) / S with x/T as x * (1/T) and the division by S as a
 // product with its reciprocal (each within an ulp of the quotient)
-__device__ __forceinline__ double prob(float x, const RowNorm& r, float T) {
-    return exp((double)x * (1.0 / (double)T) - r.m) * r.iS;
+__device__ __forceinline__ double prob(float x, const RowNorm& r, float T, const double* tab) {
+    return dexp((double)x * (1.0 / (double)T) - r.m, tab) * r.iS;
 }
 
 // One block per sequence, one wave per row (rows w, w + DECIDE_WAVES, ...):
@@ -153,6 +200,9 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
     RowNorm* nr = norms + (int64_t)s * R;
     __shared__ double sp[WAVE], sq[WAVE];
     __shared__ int sarg[WAVE];
+    __shared__ double tab[64];
+    load_exp_tab(tab);
+    __syncthreads();
     for (int r = w; r < n_rows; r += DECIDE_WAVES) {
         const ChunkStat* sr = st + (int64_t)r * n_chunks;
         float mx = -INFINITY;
@@ -175,7 +225,7 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
             const double iT = 1.0 / (double)T;
             rn.m = (double)mx * iT;
             double S = 0.0;
-            for (int c = lane; c < n_chunks; c += WAVE) S += sr[c].sum * exp((double)sr[c].mx * iT - rn.m);
+            for (int c = lane; c < n_chunks; c += WAVE) S += sr[c].sum * dexp((double)sr[c].mx * iT - rn.m, tab);
             rn.S = wave_sum_d(S);
             rn.iS = 1.0 / rn.S;
         }
@@ -193,8 +243,8 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
             if (samp) {
                 double p = 0.0, q = 0.0;
                 if (d >= 0 && d < vocab) {
-                    p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], nr[i], T);
-                    q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], nr[gamma + 1 + i], T);
+                    p = prob(row_ptr(target, draft, s, i, gamma, vocab)[d], nr[i], T, tab);
+                    q = prob(row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d], nr[gamma + 1 + i], T, tab);
                 }
                 sp[lane] = p;
                 sq[lane] = q;
@@ -246,10 +296,10 @@ __global__ void __launch_bounds__(WAVE * DECIDE_WAVES) decide_kernel(const float
 
 // probability of index i under the final distribution of sequence s
 __device__ __forceinline__ double final_mass(const float* p_row, const float* q_row, const RowNorm& pn,
-                                             const RowNorm& qn, int mode, int i, float T) {
-    const double p = prob(p_row[i], pn, T);
+                                             const RowNorm& qn, int mode, int i, float T, const double* tab) {
+    const double p = prob(p_row[i], pn, T, tab);
     if (mode == 1) return p;
-    const double r = p - prob(q_row[i], qn, T);
+    const double r = p - prob(q_row[i], qn, T, tab);
     return r > 0.0 ? r : 0.0;
 }
 
@@ -266,8 +316,11 @@ __global__ void __launch_bounds__(ABLK) sums_kernel(const float* __restrict__ ta
     const float* qr = ss.mode == 2 ? row_ptr(target, draft, s, gamma + 1 + ss.row, gamma, vocab) : pr;
     const RowNorm pn = nr[ss.row], qn = ss.mode == 2 ? nr[gamma + 1 + ss.row] : pn;
     const int i0 = chunk * VCH, i1 = min(vocab, i0 + VCH);
+    __shared__ double tab[64];
+    load_exp_tab(tab);
+    __syncthreads();
     double sum = 0.0;
-    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) sum += final_mass(pr, qr, pn, qn, ss.mode, i, T);
+    for (int i = i0 + threadIdx.x; i < i1; i += ABLK) sum += final_mass(pr, qr, pn, qn, ss.mode, i, T, tab);
     sum = wave_sum_d(sum);
     __shared__ double ssum[ABLK / WAVE];
     if (threadIdx.x % WAVE == 0) ssum[threadIdx.x / WAVE] = sum;
@@ -297,11 +350,14 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
     // the chunk masses, read (and for p, computed) by all threads at once; the
     // sums over them stay sequential in chunk order on thread 0
     __shared__ double s_cs[PICK_MAX_CHUNKS], s_pm[PICK_MAX_CHUNKS];
+    __shared__ double tab[64];
+    load_exp_tab(tab);
+    __syncthreads();
     {
         const RowNorm pn = nr[ss.row];
         for (int c = threadIdx.x; c < n_chunks; c += blockDim.x) {
             s_cs[c] = cs[c];
-            s_pm[c] = pst[c].sum * exp((double)pst[c].mx * (1.0 / (double)T) - pn.m) * pn.iS;
+            s_pm[c] = pst[c].sum * dexp((double)pst[c].mx * (1.0 / (double)T) - pn.m, tab) * pn.iS;
         }
     }
     __syncthreads();
@@ -364,7 +420,7 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = b0 + k;
-        v[k] = i < i1 ? final_mass(pr, qr, pn, qn, mode, i, T) : 0.0;
+        v[k] = i < i1 ? final_mass(pr, qr, pn, qn, mode, i, T, tab) : 0.0;
         loc += v[k];
         if (v[k] > 0.0) lastp = i;
     }
@@ -416,6 +472,7 @@ extern "C" int dkv_accept(const float* target, const float* draft, const int32_t
     DKV_REQUIRE(target && accepted && next_token && n_uniforms && u, "dkv_accept: NULL argument");
     DKV_REQUIRE(batch > 0 && gamma >= 0 && vocab > 0, "dkv_accept: bad sizes");
     DKV_REQUIRE(chunks_of(vocab) <= PICK_MAX_CHUNKS, "dkv_accept: vocab too large");
+    DKV_REQUIRE(2 * (int64_t)gamma + 1 <= 65535 && batch <= 65535, "dkv_accept: gamma or batch too large for the grid");
     DKV_REQUIRE(gamma == 0 || draft_tokens, "dkv_accept: draft_tokens is NULL");
     DKV_REQUIRE(temperature <= 0.0f || gamma == 0 || draft, "dkv_accept: draft logits needed when T > 0");
     const size_t need = dkv_accept_workspace(batch, gamma, vocab);

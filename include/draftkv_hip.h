@@ -214,8 +214,9 @@ int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t v
  * T <= 0); draft_tokens int32 [batch][gamma]; u: f64 [batch][gamma+1]
  * uniforms in the order the reference draws them (one per tested position in
  * sampling mode, then one for the bonus/residual token). Outputs int32
- * [batch]: accepted, next_token, and n_uniforms (draws consumed).
- * work: dkv_accept_workspace() bytes. */
+ * [batch]: accepted, next_token, and n_uniforms (draws consumed). Any
+ * gamma up to 32767. work: dkv_accept_workspace() bytes;
+ * calls that share a workspace must be in stream order. */
 size_t dkv_accept_workspace(int32_t batch, int32_t gamma, int32_t vocab);
 int dkv_accept(const float* target, const float* draft, const int32_t* draft_tokens,
                int32_t batch, int32_t gamma, int32_t vocab, float temperature, const double* u,
@@ -228,7 +229,7 @@ int dkv_accept(const float* target, const float* draft, const int32_t* draft_tok
  * for callers that cannot allocate device memory -- code under stream/graph
  * capture, serving loops that forbid hipMalloc. Returns DKV_ECAPACITY when
  * dkv_accept_workspace(batch, gamma, vocab) exceeds the scratch (at vocab
- * 128256 it holds batch 128 with gamma <= 24). Calls that overlap on one GPU
+ * 128256 it holds batch 128 with gamma <= 29). Calls that overlap on one GPU
  * share the array and race; calls in stream order do not. */
 #define DKV_ACCEPT_SCRATCH_BYTES ((size_t)4 << 20)
 int dkv_accept_noalloc(const float* target, const float* draft, const int32_t* draft_tokens,

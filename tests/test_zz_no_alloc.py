@@ -63,7 +63,7 @@ def test_noalloc_refuses_more_than_the_scratch(dev):
     launch on pointers that do not hold the data."""
     from draftkv._lib import lib
     L = lib()
-    b, gamma, V = 2048, 24, 4096
+    b, gamma, V = 256, 40, 65536
     nbytes = L.dkv_accept_workspace(b, gamma, V)
     assert nbytes > (4 << 20)
     target = torch.zeros((b, gamma + 1, V), dtype=torch.float32, device=dev)
