@@ -514,6 +514,11 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     p.nw = (N % 32 == 0 && K % GKB == 0 && M > 32) ? 2 : 1;
     p.mb = M <= 16 ? 1 : M <= 32 ? 2 : (M <= 64 || p.nw == 1) ? 4 : 8;
     p.m_tiles = (M + 16 * p.mb - 1) / (16 * p.mb);
+    if (p.nw == 2 && M > 64) {   // tiles of up to 128 rows, as even as 16-row fragments allow (M = 96: one tile of
+                                 // 96, not 128; M = 288: three of 96, not 128 + 128 + 32)
+        const int rows = (M + p.m_tiles - 1) / p.m_tiles;
+        p.mb = (rows + 15) / 16;
+    }
     p.n_tiles = (N + 64 * p.nw - 1) / (64 * p.nw);
     // split the chunks over workgroups only when the tiles alone leave most of the chip idle
     // (partials need whole 16-row fragments: N % 16 == 0)
@@ -577,6 +582,12 @@ static void launch_plan(const GemmPlan& p, const GemmArgs& a, dim3 grid, hipStre
     if (p.wv == 7) {   // one fragment per wave, an x tile of 16 or 32 rows, whole 128-k blocks (the plan's test)
         if (p.mb == 2) launch_gemm<1, 2, false, 7, WT>(a, grid, st);
         else launch_gemm<1, 1, false, 7, WT>(a, grid, st);
+    } else if (p.nw == 2 && p.mb == 5) {   // two fragments (K % 128 == 0), x tiles of 80 to 112 rows
+        launch_gemm<2, 5, false, 4, WT>(a, grid, st);
+    } else if (p.nw == 2 && p.mb == 6) {
+        launch_gemm<2, 6, false, 4, WT>(a, grid, st);
+    } else if (p.nw == 2 && p.mb == 7) {
+        launch_gemm<2, 7, false, 4, WT>(a, grid, st);
     } else if (p.nw == 2 && p.mb == 4) {   // K % 128 == 0 with two fragments
         launch_gemm<2, 4, false, 4, WT>(a, grid, st);
     } else if (p.nw == 2) {

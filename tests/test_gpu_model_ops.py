@@ -128,7 +128,8 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
                                              (32, 4096, 4096, True), (33, 512, 14336, False),
                                              (96, 6144, 4096, True), (200, 1024, 2048, False), (64, 272, 96, True),
                                              (544, 4096, 4096, False), (32, 28672, 4096, True),
-                                             (96, 28672, 4096, False),
+                                             (96, 28672, 4096, False), (160, 6144, 4096, False),
+                                             (288, 4096, 4096, True), (288, 28672, 4096, False),
                                              # W ending inside a 16-row fragment (a tied GPT-2 head: 50257 rows)
                                              (1, 50257, 768, False), (5, 50257, 768, True), (33, 50257, 768, False),
                                              (3, 40, 4096, True), (96, 1001, 2048, True), (17, 23, 96, True)])
@@ -141,7 +142,8 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
     (partials + ordered reduce) or summed inside one, the small-M kernel that
     splits K among the waves of a workgroup, 128-k blocks and the 32-k
     tail, the 7-wave workgroups of the 28672-row gate/up weight (whose
-    rows must equal those of the 4-wave plan at M = 96), and any N: a last
+    rows must equal those of the 4-wave plan at M = 96), x tiles cut evenly
+    (M = 96: one of 96 rows; 160: two of 80; 288: three of 96), and any N: a last
     fragment of fewer than 16 W rows (odd N: element stores) in the main and
     the small-M kernels."""
     ops = _ops()
