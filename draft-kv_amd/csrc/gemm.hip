@@ -166,6 +166,8 @@ __device__ __forceinline__ int64_t w_step_off(int k, int j) {
 // multiple of 128); otherwise every block is whole.
 template <int NW, int MB, bool MULTI, bool PARTIAL, int PD, bool XF32, int WV, bool WT>
 __global__ void __launch_bounds__(64 * WV) gemm_bf16_kernel(GemmArgs a) {
+    // x of block gb + 1 waits in registers to be staged while block gb + PD - 1 is fetched: two sets apart
+    static_assert(PD >= 3, "x needs a register set between its fetch and its staging");
     constexpr int TM = 16 * MB;
     constexpr int NT = 64 * WV;                               // threads
     constexpr int NXI = (16 * TM + NT - 1) / NT;             // x pieces (8 elements) per thread per block

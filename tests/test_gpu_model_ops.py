@@ -130,6 +130,11 @@ def test_gemm_f32_and_batch_invariance(dev, M, N, K, layout):
                                              (544, 4096, 4096, False), (32, 28672, 4096, True),
                                              (96, 28672, 4096, False), (160, 6144, 4096, False),
                                              (288, 4096, 4096, True), (288, 28672, 4096, False),
+                                             # larger verify blocks: up to six m tiles, a partial last
+                                             # fragment, the 28672-row weight at 16 fragments
+                                             (65, 4096, 4096, False), (300, 6144, 4096, True),
+                                             (352, 1024, 4096, False), (672, 4096, 1024, True),
+                                             (256, 28672, 4096, False), (130, 4096, 14336, False),
                                              # W ending inside a 16-row fragment (a tied GPT-2 head: 50257 rows)
                                              (1, 50257, 768, False), (5, 50257, 768, True), (33, 50257, 768, False),
                                              (3, 40, 4096, True), (96, 1001, 2048, True), (17, 23, 96, True)])
@@ -170,7 +175,8 @@ def test_gemm_bf16_matches_fp32_and_is_batch_invariant(dev, M, N, K, with_bias):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 96, 160), (8, 512, 14336), (32, 4096, 4096),
-                                   (96, 1024, 2048), (200, 272, 96)])
+                                   (96, 1024, 2048), (200, 272, 96), (288, 4096, 4096), (130, 6144, 4096),
+                                   (352, 1024, 1024)])
 def test_gemm_bf16_float32_x_equals_converting_first(dev, M, N, K):
     """A float32 x is rounded to bf16 (nearest even) as the kernels read it:
     the result is bit for bit that of x.to(bfloat16), for every launch plan."""
@@ -186,7 +192,7 @@ def test_gemm_bf16_float32_x_equals_converting_first(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,ff,K", [(1, 2048, 4096), (5, 48, 160), (8, 512, 2048), (32, 14336, 4096),
-                                    (96, 512, 1024), (200, 136, 96)])
+                                    (96, 512, 1024), (200, 136, 96), (288, 14336, 4096), (160, 512, 1024)])
 def test_gemm_bf16_swiglu_epilogue_equals_unfused(dev, M, ff, K):
     """The SwiGLU epilogue (interleaved gate/up rows) gives bit for bit the
     unfused result: the [gate; up] GEMM rounded to bf16, then the SwiGLU
@@ -232,7 +238,8 @@ def test_add_norm_on_deferred_partials_equals_gemm_then_add_norm(dev, M, N, K, l
         assert planned > 1, "the Llama-3-8B o projection at M = 32 should run with partials"
 
 
-@pytest.mark.parametrize("M,rope,bias", [(32, True, False), (96, True, True), (3, False, True), (32, False, False)])
+@pytest.mark.parametrize("M,rope,bias", [(32, True, False), (96, True, True), (3, False, True), (32, False, False),
+                                         (288, True, False)])
 def test_qkv_split_on_deferred_partials_equals_gemm_then_split(dev, M, rope, bias):
     """qkv_split reading the qkv GEMM's deferred partials equals the split of
     the GEMM's bf16 output bit for bit (q, k, v; RoPE and a projection bias)."""
@@ -261,7 +268,9 @@ def test_qkv_split_on_deferred_partials_equals_gemm_then_split(dev, M, rope, bia
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 4096, 4096, False), (6, 1024, 4096, True), (8, 4096, 14336, False),
                                              (17, 6144, 4096, True), (32, 4096, 4096, False),
                                              (32, 28672, 4096, False), (12, 28672, 4096, True),
-                                             (96, 6144, 4096, False), (200, 1024, 2048, True), (96, 4096, 14336, False)])
+                                             (96, 6144, 4096, False), (200, 1024, 2048, True), (96, 4096, 14336, False),
+                                             (288, 28672, 4096, False), (288, 4096, 4096, True),
+                                             (352, 6144, 4096, False)])
 def test_gemm_bf16_tiled_weights_equal_row_major(dev, M, N, K, with_bias):
     """W stored in 16x128 tiles (ops.TiledW, DKV_GEMM_WTILED) gives bit for bit
     the row-major product on every launch plan (small-M in-workgroup split, x
