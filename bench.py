@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--verify-gamma", type=int, default=8,
                     help="--workload kernels: the verify pass runs verify_gamma + 1 queries per sequence")
     ap.add_argument("--temperature", type=float, default=0.8)
+    ap.add_argument("--recompute-draft-stats", action="store_true",
+                    help="accept workload: recompute the draft rows' normalisers in the call")
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--keep", type=float, default=0.25)
     ap.add_argument("--group", type=int, default=32)
@@ -865,7 +867,11 @@ def run_accept(args):
     """Acceptance alone: one verify decision over the batch (target logits
     [batch, gamma+1, vocab] and draft logits [batch, gamma, vocab], float32
     N(0, 2^2), temperature rejection sampling), timed per call with HIP
-    events. Algorithmic bytes: every logit read once."""
+    events. As in the decode round, the draft rows' normalisers come from the
+    draft steps' samples (computed before the timed calls);
+    --recompute-draft-stats times the call that recomputes them instead.
+    Algorithmic bytes: every target logit read once, plus one draft row per
+    sequence (the residual's q; every draft logit when recomputing)."""
     import torch
     from draftkv import ops
     b, g, V = args.batch, args.gamma, 128256
@@ -877,24 +883,31 @@ def run_accept(args):
     tok = torch.randint(0, V, (b, g), generator=gen, device=dev, dtype=torch.int32)
     u = torch.rand((b, g + 1), generator=gen, device=dev, dtype=torch.float64)
     T = args.temperature
+    ds = None
+    if T > 0 and not args.recompute_draft_stats:   # what the draft steps' samples leave behind
+        ds = ops.row_stats(b, dev, (g,))
+        for i in range(g):
+            ops.sample(draft[:, i].contiguous(), T, u[:, i].contiguous(), stats_out=ds[i])
     for _ in range(args.warmup):
-        ops.accept(target, draft, tok, T, u)
+        ops.accept(target, draft, tok, T, u, ds)
     torch.cuda.synchronize()
     evs = []
     for _ in range(args.steps):
         s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s_ev.record()
-        ops.accept(target, draft, tok, T, u)
+        ops.accept(target, draft, tok, T, u, ds)
         e_ev.record()
         evs.append((s_ev, e_ev))
     torch.cuda.synchronize()
     us = 1e3 * sum(a.elapsed_time(c) for a, c in evs) / len(evs)
-    nbytes = 4.0 * b * (2 * g + 1) * V
+    nbytes = 4.0 * b * ((2 * g + 1) if ds is None else (g + 2)) * V
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"metric": f"accept (verify decision) GB/s, b={b} gamma={g} vocab={V}", "value": gbs, "unit": "GB/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": us / 1e3,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32/f64",
-            "data": "synthetic", "config": {"workload": f"accept b={b} gamma={g} T={T}"},
+            "data": "synthetic",
+            "config": {"workload": f"accept b={b} gamma={g} T={T}",
+                       "draft_stats": "recomputed" if ds is None else "from the draft samples"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_call": nbytes, "us_per_call": us},
             "cpu_baseline": None}

@@ -56,10 +56,10 @@ _SIGS = {
     "dkv_drafter_kernel_total_ms": (F32, [P]),
     "dkv_drafter_gather": (C.c_int, [PDrafter, I32, I32, QCfg, I32, P, P, P, P, P, P, P, P, P, P]),
     "dkv_sample_workspace": (SZ, [I32, I32]),
-    "dkv_sample": (C.c_int, [P, I64, I32, I32, F32, P, P, P, SZ, P]),
+    "dkv_sample": (C.c_int, [P, I64, I32, I32, F32, P, P, P, P, SZ, P]),
     "dkv_accept_workspace": (SZ, [I32, I32, I32]),
-    "dkv_accept": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P, SZ, P]),
-    "dkv_accept_noalloc": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P]),
+    "dkv_accept": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P, P, SZ, P]),
+    "dkv_accept_noalloc": (C.c_int, [P, P, P, I32, I32, I32, F32, P, P, P, P, P, P]),
     "dkv_embed": (C.c_int, [P, I32, P, I32, I32, P, P, P, P]),
     "dkv_rmsnorm": (C.c_int, [P, P, I32, I32, I32, F32, P, I32, P]),
     "dkv_layernorm": (C.c_int, [P, P, P, I32, I32, I32, F32, P, I32, P]),

@@ -487,6 +487,9 @@ class DecodeBatch:
         pending = x
         draft_tok = torch.empty((b, gamma), dtype=torch.int32, device=dev)
         draft_logits = torch.empty((b, gamma, V), dtype=torch.float32, device=dev) if T > 0 else None
+        # the draft rows' normalisers, kept from each step's sample for the decision (as the
+        # reference keeps the drafter's distributions, engine.py:176-179)
+        draft_stats = ops.row_stats(b, dev, (gamma,)) if T > 0 else None
         graph = self._draft_graph(n, act, gamma) if self.use_graphs else None
         # with a graph for this layout recorded, every step replays it; on the
         # layout's first round step 0 runs eagerly (warming every kernel and GEMM
@@ -498,13 +501,13 @@ class DecodeBatch:
             lg = model.forward_batch(x[:, None], comp, n - 1 + i, act)[:, 0]
             if draft_logits is not None:
                 draft_logits[:, i].copy_(lg)
-            x = ops.sample(lg, T, u_draft_d[i])
+            x = ops.sample(lg, T, u_draft_d[i], stats_out=None if draft_stats is None else draft_stats[i])
             draft_tok[:, i] = x
         if graph is _RECORD:
             graph = self._record_graph()
         if graph is not None:
             graph.run(x, [n - 1 + i for i in range(n_eager, gamma)], act, u_draft[n_eager:], draft_tok,
-                      draft_logits, col0=n_eager)
+                      draft_logits, col0=n_eager, draft_stats=draft_stats)
         self.last_draft = (draft_tok, draft_logits)
         if ph is not None:
             ev["d1"] = ph.event()
@@ -512,7 +515,7 @@ class DecodeBatch:
         # -- verify
         block = torch.cat([pending[:, None], draft_tok], 1).contiguous()
         logits = model.forward_batch(block, full, n - 1, act * (gamma + 1))
-        acc, nxt, used = ops.accept(logits, draft_logits, draft_tok, T, u_ver_d)
+        acc, nxt, used = ops.accept(logits, draft_logits, draft_tok, T, u_ver_d, draft_stats)
         if ph is not None:
             ev["v1"] = ph.event()
         host = torch.cat([torch.stack([acc, nxt, used], 1), draft_tok], 1).cpu().numpy()

@@ -66,6 +66,7 @@ class DraftStepGraph:
         self.count = self.inp[3 * b: 4 * b]
         self.budgets = self.inp[4 * b:].view(L, b)
         self.tok = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.stats = ops.row_stats(b, dev)   # the sampled rows' normalisers (for the verify decision)
         self.ws = ops.Workspace()
         self._rows_host: Optional[torch.Tensor] = None
         self._rows_dev: Optional[torch.Tensor] = None
@@ -79,7 +80,7 @@ class DraftStepGraph:
         with ops.private_workspace(self.ws):
             with torch.cuda.graph(self.graph, pool=pool):
                 lg = model._core(self.tok, self.start, b, 1, attn, cs, cs_len)[:, 0]
-                ops.sample(lg, self.T, self.u, out=self.tok)
+                ops.sample(lg, self.T, self.u, out=self.tok, stats_out=self.stats if self.T > 0 else None)
         self.logits = lg
 
     def _rows(self, n: int):
@@ -89,11 +90,13 @@ class DraftStepGraph:
         return self._rows_host, self._rows_dev
 
     def run(self, x0: torch.Tensor, starts: np.ndarray, act: np.ndarray, u: np.ndarray, draft_tok: torch.Tensor,
-            draft_logits: Optional[torch.Tensor], col0: int = 0) -> torch.Tensor:
+            draft_logits: Optional[torch.Tensor], col0: int = 0,
+            draft_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Run len(starts) steps from token x0 (int32 [b], device): step i
         appends at starts[i] (int [b]) the rows act (0/1 [b]) with uniforms
         u[i] ([b]); tokens go to draft_tok[:, col0 + i], logits (when given) to
-        draft_logits[:, col0 + i]. The mirror's ``seen`` advances as the eager
+        draft_logits[:, col0 + i] and the rows' normalisers (when given) to
+        draft_stats[col0 + i]. The mirror's ``seen`` advances as the eager
         steps would move it. Returns the last sampled token (a device view)."""
         steps, b = len(starts), self.b
         if steps == 0:
@@ -119,6 +122,8 @@ class DraftStepGraph:
             self.replays += 1
             if draft_logits is not None:
                 draft_logits[:, col0 + i].copy_(self.logits)
+            if draft_stats is not None:
+                draft_stats[col0 + i].copy_(self.stats)
             draft_tok[:, col0 + i].copy_(self.tok)
         return self.tok
 

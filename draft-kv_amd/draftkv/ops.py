@@ -280,22 +280,39 @@ def drafter_gather(desc: Drafter, seq: int, layer: int, cfg: QCfg, rows: int, de
 
 
 # ------------------------------------------------------------------ sampling and accept
+ROW_STATS_WORDS = 4   # dkv_row_stats_t: 32 bytes, held as 4 float64 words per row
+
+
+def row_stats(rows: int, device, lead: tuple = ()) -> torch.Tensor:
+    """A buffer of dkv_row_stats_t for ``lead + (rows,)`` rows."""
+    return torch.empty(lead + (rows, ROW_STATS_WORDS), dtype=torch.float64, device=device)
+
+
 def sample(logits: torch.Tensor, temperature: float, u: torch.Tensor,
-           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+           out: Optional[torch.Tensor] = None, stats_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One draw per row; ``stats_out`` (a ``row_stats(b)`` buffer or a view
+    of one) receives each row's normaliser, which ``accept`` takes back as
+    ``draft_stats`` instead of recomputing it."""
     _need(logits, "logits", torch.float32, 2)
     _need(u, "u", torch.float64)
     b, V = logits.shape
     if out is None:
         out = torch.empty(b, dtype=torch.int32, device=logits.device)
+    if stats_out is not None:
+        _need(stats_out, "stats_out", torch.float64, 2)
+        if stats_out.shape != (b, ROW_STATS_WORDS):
+            raise ValueError("stats_out must be a row_stats(batch) buffer")
     ws = _WS.get(logits.device, lib().dkv_sample_workspace(b, V))
     check(lib().dkv_sample(logits.data_ptr(), V, b, V, float(temperature), u.data_ptr(), out.data_ptr(),
-                           ws.data_ptr(), ws.numel(), _stream()), "dkv_sample")
+                           _ptr(stats_out), ws.data_ptr(), ws.numel(), _stream()), "dkv_sample")
     return out
 
 
 def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: torch.Tensor,
-           temperature: float, u: torch.Tensor):
-    """Returns (accepted, next_token, n_uniforms) int32 [batch] device tensors."""
+           temperature: float, u: torch.Tensor, draft_stats: Optional[torch.Tensor] = None):
+    """Returns (accepted, next_token, n_uniforms) int32 [batch] device tensors.
+    ``draft_stats``: the draft rows' normalisers from ``sample(...,
+    stats_out=)``, [gamma, batch] rows of ``row_stats`` (step-major)."""
     _need(target, "target", torch.float32, 3)
     _need(draft_tokens, "draft_tokens", torch.int32, 2)
     _need(u, "u", torch.float64, 2)
@@ -309,10 +326,14 @@ def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: to
         _need(draft, "draft", torch.float32, 3)
         if draft.shape != (b, gamma, V):
             raise ValueError("draft must be [batch, gamma, vocab]")
+    if draft_stats is not None:
+        _need(draft_stats, "draft_stats", torch.float64, 3)
+        if draft_stats.shape != (gamma, b, ROW_STATS_WORDS):
+            raise ValueError("draft_stats must be [gamma, batch] row_stats")
     res = torch.empty((3, b), dtype=torch.int32, device=target.device)
     ws = _WS.get(target.device, lib().dkv_accept_workspace(b, gamma, V))
     check(lib().dkv_accept(target.data_ptr(), _ptr(draft), draft_tokens.data_ptr(), b, gamma, V,
-                           float(temperature), u.data_ptr(), res[0].data_ptr(), res[1].data_ptr(),
+                           float(temperature), u.data_ptr(), _ptr(draft_stats), res[0].data_ptr(), res[1].data_ptr(),
                            res[2].data_ptr(), ws.data_ptr(), ws.numel(), _stream()), "dkv_accept")
     return res[0], res[1], res[2]
 

@@ -198,14 +198,28 @@ int dkv_drafter_gather(const dkv_drafter_t* mirror, int32_t seq, int32_t layer, 
                        int32_t* pos, dkv_stream_t stream);
 
 /* ---------------------------------------------------------------- sampling */
+/* A row's normaliser under temperature T > 0, as dkv_sample computes it and
+ * dkv_accept uses it: m = max(x)/T, s = the float64 sum over the row of
+ * exp(x/T - m), inv_s = 1/s (arg: the first index of the max, greedy only).
+ * The reference keeps the drafter's whole distribution q from each draft
+ * step (draftkv/engine.py:176-179, `draft_probs`) for the verify decision;
+ * these 32 bytes per row are what the decision needs of it besides the
+ * logits. */
+typedef struct {
+    double m, s, inv_s;
+    int32_t arg, reserved;
+} dkv_row_stats_t;
+
 /* One draw per row from softmax(logits/T) -- replaces draftkv/engine.py:36-41
  * (`_probs`) + :101-106 (`_sample`). logits f32 rows of length vocab at
  * row_stride; u: f64 uniforms [batch]. T <= 0: first argmax (u unused).
- * tokens: int32 [batch]. work: dkv_sample_workspace() bytes. */
+ * tokens: int32 [batch]. row_stats: NULL, or [batch] written with each
+ * row's normaliser (for dkv_accept's draft_stats). work:
+ * dkv_sample_workspace() bytes. */
 size_t dkv_sample_workspace(int32_t batch, int32_t vocab);
 int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t vocab,
-               float temperature, const double* u, int32_t* tokens, void* work,
-               size_t work_bytes, dkv_stream_t stream);
+               float temperature, const double* u, int32_t* tokens, dkv_row_stats_t* row_stats,
+               void* work, size_t work_bytes, dkv_stream_t stream);
 
 /* ---------------------------------------------------------------- accept */
 /* Verify decision of one round for every sequence -- replaces
@@ -213,15 +227,19 @@ int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t v
  * draft: f32 [batch][gamma][vocab] (the drafter's logits; unused when
  * T <= 0); draft_tokens int32 [batch][gamma]; u: f64 [batch][gamma+1]
  * uniforms in the order the reference draws them (one per tested position in
- * sampling mode, then one for the bonus/residual token). Outputs int32
- * [batch]: accepted, next_token, and n_uniforms (draws consumed). Any
- * gamma up to 32767. work: dkv_accept_workspace() bytes;
- * calls that share a workspace must be in stream order. */
+ * sampling mode, then one for the bonus/residual token). draft_stats: NULL,
+ * or [gamma][batch] (step-major, as the draft steps produce them) the draft
+ * rows' normalisers from dkv_sample on the same logits -- the draft rows'
+ * statistics are then not recomputed (the decisions are the same either
+ * way). Outputs int32 [batch]: accepted, next_token, and n_uniforms (draws
+ * consumed). Any gamma up to 32767, vocab up to 1048576.
+ * work: dkv_accept_workspace() bytes; calls that share a workspace must be in
+ * stream order. */
 size_t dkv_accept_workspace(int32_t batch, int32_t gamma, int32_t vocab);
 int dkv_accept(const float* target, const float* draft, const int32_t* draft_tokens,
                int32_t batch, int32_t gamma, int32_t vocab, float temperature, const double* u,
-               int32_t* accepted, int32_t* next_token, int32_t* n_uniforms, void* work,
-               size_t work_bytes, dkv_stream_t stream);
+               const dkv_row_stats_t* draft_stats, int32_t* accepted, int32_t* next_token,
+               int32_t* n_uniforms, void* work, size_t work_bytes, dkv_stream_t stream);
 
 /* dkv_accept with no workspace argument and no allocation: the workspace is a
  * static device array of DKV_ACCEPT_SCRATCH_BYTES inside the library (one per
@@ -229,13 +247,14 @@ int dkv_accept(const float* target, const float* draft, const int32_t* draft_tok
  * for callers that cannot allocate device memory -- code under stream/graph
  * capture, serving loops that forbid hipMalloc. Returns DKV_ECAPACITY when
  * dkv_accept_workspace(batch, gamma, vocab) exceeds the scratch (at vocab
- * 128256 it holds batch 128 with gamma <= 29). Calls that overlap on one GPU
- * share the array and race; calls in stream order do not. */
-#define DKV_ACCEPT_SCRATCH_BYTES ((size_t)4 << 20)
+ * 128256 it holds batch 32 with gamma <= 112, batch 128 with gamma <= 15).
+ * Calls that overlap on one GPU share the array and race; calls in stream
+ * order do not. */
+#define DKV_ACCEPT_SCRATCH_BYTES ((size_t)16 << 20)
 int dkv_accept_noalloc(const float* target, const float* draft, const int32_t* draft_tokens,
                        int32_t batch, int32_t gamma, int32_t vocab, float temperature,
-                       const double* u, int32_t* accepted, int32_t* next_token,
-                       int32_t* n_uniforms, dkv_stream_t stream);
+                       const double* u, const dkv_row_stats_t* draft_stats, int32_t* accepted,
+                       int32_t* next_token, int32_t* n_uniforms, dkv_stream_t stream);
 
 /* ------------------------------------------------------ model forward ops */
 /* The non-attention pieces of the model forwards (reference

@@ -58,7 +58,7 @@ def test_noalloc_accept_refuses_oversize_without_gpu():
         pytest.skip("library not built")
     L = _lib.lib()
     p = ctypes.c_void_p(16)
-    rc = L.dkv_accept_noalloc(p, p, p, 100000, 20, 128256, 0.8, p, p, p, p, None)
+    rc = L.dkv_accept_noalloc(p, p, p, 100000, 20, 128256, 0.8, p, None, p, p, p, None)
     assert rc == -4 and b"static scratch" in L.dkv_last_error()
-    rc = L.dkv_accept_noalloc(p, p, p, 0, 20, 128256, 0.8, p, p, p, p, None)
+    rc = L.dkv_accept_noalloc(p, p, p, 0, 20, 128256, 0.8, p, None, p, p, p, None)
     assert rc == -1

@@ -361,10 +361,13 @@ def test_sample_matches_numpy_choice(dev, V, T):
         assert tok[s] == sample_u(o_probs(logits[s], T), u[s]), s
 
 
-def _accept_case(ops, dev, b, gamma, V, T, seed):
+def _accept_case(ops, dev, b, gamma, V, T, seed, stats=False):
     """Target rows near a shared base, draft rows near it too, drafted tokens
     mostly the target's argmax (long accepted runs) and sometimes not; the
-    device decision against the oracle rule for every sequence."""
+    device decision against the oracle rule for every sequence. stats: the
+    draft rows' normalisers come from dkv_sample on each draft step's logits
+    (as the decode round passes them), and the decision also equals the one
+    that recomputes them."""
     rng = np.random.default_rng(seed)
     base = rng.standard_normal((b, 1, V)).astype(np.float32) * 2
     target = (base + 0.3 * rng.standard_normal((b, gamma + 1, V))).astype(np.float32)
@@ -374,9 +377,16 @@ def _accept_case(ops, dev, b, gamma, V, T, seed):
         for i in range(gamma):
             toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.95 else int(rng.integers(V))
     u = rng.random((b, gamma + 1))
-    acc, nxt, used = ops.accept(torch.from_numpy(target).to(dev), torch.from_numpy(draft).to(dev),
-                                torch.from_numpy(toks).to(dev), T, torch.from_numpy(u).to(dev))
+    t_d, d_d, k_d, u_d = (torch.from_numpy(x).to(dev) for x in (target, draft, toks, u))
+    acc, nxt, used = ops.accept(t_d, d_d, k_d, T, u_d)
     acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
+    if stats and T > 0:
+        ds = ops.row_stats(b, dev, (gamma,))
+        for i in range(gamma):
+            ops.sample(d_d[:, i].contiguous(), T, u_d[:, i].contiguous(), stats_out=ds[i])
+        got = [x.cpu().numpy() for x in ops.accept(t_d, d_d, k_d, T, u_d, ds)]
+        for x, y, name in zip((acc, nxt, used), got, ("accepted", "next_token", "n_uniforms")):
+            assert np.array_equal(x, y), name
     for s in range(b):
         qs = [o_probs(draft[s, i], T) for i in range(gamma)]
         ra, rn, ru = o_accept(target[s], toks[s].tolist(), qs, T, u[s])
@@ -393,8 +403,33 @@ def test_accept_matches_reference_rule_at_bench_points(dev, T, b, gamma):
     counts, next tokens and uniforms consumed equal the oracle rule's
     (engine.py:188-213) for every sequence."""
     _, ops = _dk()
-    acc = _accept_case(ops, dev, b, gamma, 128256, T, 1000 + gamma + int(T * 10))
+    acc = _accept_case(ops, dev, b, gamma, 128256, T, 1000 + gamma + int(T * 10), stats=True)
     assert acc.max() > 0
+
+
+@pytest.mark.parametrize("V", [128256, 50257])
+def test_sample_row_stats_are_the_float64_normaliser(dev, V):
+    """dkv_sample's row statistics: m = max(x) * (1/T), s = the sum over the
+    row of exp(x/T - m) in float64 (within 1e-13 relative of numpy's), 1/s;
+    a ragged batch of 7 rows with -inf and -30000 entries; odd vocab takes the
+    float read path."""
+    _, ops = _dk()
+    rng = np.random.default_rng(V + 3)
+    b, T = 7, 0.8
+    x = (rng.standard_normal((b, V)) * 3).astype(np.float32)
+    x[2, :50] = -np.inf
+    x[3, 7] = -30000.0
+    st = ops.row_stats(b, dev)
+    ops.sample(torch.from_numpy(x).to(dev), T, torch.from_numpy(rng.random(b)).to(dev), stats_out=st)
+    st = st.cpu().numpy()
+    iT = 1.0 / float(np.float32(T))   # the library takes T as float32
+    for s in range(b):
+        m = float(x[s].max()) * iT
+        y = x[s].astype(np.float64) * iT - m
+        S = float(np.exp(y).sum())
+        assert st[s, 0] == m, s
+        assert abs(st[s, 1] - S) <= 1e-13 * S, (s, st[s, 1], S)
+        assert abs(st[s, 2] * st[s, 1] - 1.0) <= 1e-15, s
 
 
 @pytest.mark.parametrize("T", [0.0, 0.8])
@@ -419,3 +454,44 @@ def test_accept_matches_reference_rule(dev, T, gamma):
         qs = [o_probs(draft[s, i], T) for i in range(gamma)]
         ra, rn, ru = o_accept(target[s], toks[s].tolist(), qs, T, u[s])
         assert (acc[s], nxt[s], used[s]) == (ra, rn, ru), s
+
+
+@pytest.mark.parametrize("V", [128256, 50257])
+def test_accept_all_zero_residual_falls_back_to_p(dev, V):
+    """A rejection where p and q are the same row (the drafted token's
+    probability underflows to 0, so the ratio test fails) leaves an all-zero
+    residual; the next token is then drawn from p itself (engine.py:210-211).
+    Other sequences of the batch reject with a real residual or accept every
+    position. Decisions equal the oracle rule's; a target view that starts
+    off a 16-byte boundary takes the scalar read path."""
+    _, ops = _dk()
+    rng = np.random.default_rng(V + 7)
+    b, gamma, T = 12, 3, 0.8
+    target = (rng.standard_normal((b, gamma + 1, V)) * 2).astype(np.float32)
+    draft = (target[:, :gamma] + 0.2 * rng.standard_normal((b, gamma, V))).astype(np.float32)
+    toks = np.argmax(target[:, :gamma], axis=2).astype(np.int32)
+    for s in range(0, b, 3):                        # p == q at the rejected row, p[d] = q[d] = 0
+        r = (s // 3) % gamma
+        toks[s, r] = 11
+        target[s, r, 11] = -30000.0
+        draft[s, : r + 1] = target[s, : r + 1]      # (ratio 1 before it: accepted)
+    for s in range(1, b, 3):                        # q far above p at a random token: a plain rejection
+        r, d = s % gamma, int(rng.integers(V))
+        toks[s, r] = d
+        draft[s, r, d] = target[s, r].max() + 6.0
+    u = rng.random((b, gamma + 1))
+    t_dev = torch.from_numpy(target).to(dev)
+    cases = [t_dev]
+    if V % 4 == 0:
+        flat = torch.empty(t_dev.numel() + 1, dtype=torch.float32, device=dev)
+        flat[1:].copy_(t_dev.reshape(-1))
+        cases.append(flat[1:].view(b, gamma + 1, V))   # 4 bytes past an aligned start
+    for tgt in cases:
+        acc, nxt, used = ops.accept(tgt, torch.from_numpy(draft).to(dev), torch.from_numpy(toks).to(dev), T,
+                                    torch.from_numpy(u).to(dev))
+        acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
+        for s in range(b):
+            qs = [o_probs(draft[s, i], T) for i in range(gamma)]
+            want = o_accept(target[s], toks[s].tolist(), qs, T, u[s])
+            assert (acc[s], nxt[s], used[s]) == want, (s, (acc[s], nxt[s], used[s]), want)
+        assert (acc[0::3] == (np.arange(0, b, 3) // 3) % gamma).all()

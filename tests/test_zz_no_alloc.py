@@ -33,7 +33,7 @@ def _run(fn_noalloc, target, draft, toks, u, T):
     gamma = g1 - 1
     outs = [torch.full((b,), -7, dtype=torch.int32, device=target.device) for _ in range(3)]
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    args = (target.data_ptr(), draft.data_ptr(), toks.data_ptr(), b, gamma, V, float(T), u.data_ptr(),
+    args = (target.data_ptr(), draft.data_ptr(), toks.data_ptr(), b, gamma, V, float(T), u.data_ptr(), None,
             *(o.data_ptr() for o in outs))
     if fn_noalloc:
         check(lib().dkv_accept_noalloc(*args, stream), "dkv_accept_noalloc")
@@ -65,14 +65,14 @@ def test_noalloc_refuses_more_than_the_scratch(dev):
     L = lib()
     b, gamma, V = 256, 40, 65536
     nbytes = L.dkv_accept_workspace(b, gamma, V)
-    assert nbytes > (4 << 20)
+    assert nbytes > (16 << 20)   # DKV_ACCEPT_SCRATCH_BYTES
     target = torch.zeros((b, gamma + 1, V), dtype=torch.float32, device=dev)
     draft = torch.zeros((b, gamma, V), dtype=torch.float32, device=dev)
     toks = torch.zeros((b, gamma), dtype=torch.int32, device=dev)
     u = torch.zeros((b, gamma + 1), dtype=torch.float64, device=dev)
     outs = [torch.zeros(b, dtype=torch.int32, device=dev) for _ in range(3)]
     rc = L.dkv_accept_noalloc(target.data_ptr(), draft.data_ptr(), toks.data_ptr(), b, gamma, V, 0.8, u.data_ptr(),
-                              *(o.data_ptr() for o in outs), None)
+                              None, *(o.data_ptr() for o in outs), None)
     torch.cuda.synchronize()
     assert rc == -4 and b"static scratch" in L.dkv_last_error()
     assert all(not o.any() for o in outs)     # nothing ran
