@@ -527,11 +527,13 @@ static GemmPlan gemm_plan(int M, int N, int K) {
     p.c_per = (S > 1 && (int64_t)p.n_tiles * p.m_tiles < 128 && N % 16 == 0) ? 1 : S;
     // 7-wave workgroups when they cut W into whole rounds of 256 tiles and 4-wave ones do not
     // (the Llama-3-8B gate/up weight, 28672 rows: 448 tiles of 64 leave the CUs unevenly loaded,
-    // 256 of 112 give every CU one)
-    const int r7 = 16 * p.nw * 7;
-    if (p.c_per == S && p.mb <= 2 && K % GKB == 0 && N % r7 == 0 && (N / r7 * p.m_tiles) % 256 == 0 &&
+    // 256 of 112 give every CU one); one fragment per wave, x tiles up to 128 rows (one m tile;
+    // at M = 96 the gate/up GEMM measured 49 -> 46 us against 224 two-fragment workgroups)
+    const int r7 = 16 * (p.mb <= 2 ? p.nw : 1) * 7;
+    if (p.c_per == S && (p.mb <= 2 || p.m_tiles == 1) && K % GKB == 0 && N % r7 == 0 && (N / r7 * p.m_tiles) % 256 == 0 &&
         (p.n_tiles * p.m_tiles) % 256 != 0) {
         p.wv = 7;
+        if (p.mb > 2) p.nw = 1;
         p.n_tiles = N / r7;
     }
     return p;
@@ -581,8 +583,14 @@ static void launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t st) {
 template <bool WT>
 static void launch_plan(const GemmPlan& p, const GemmArgs& a, dim3 grid, hipStream_t st) {
     const bool whole = WT || a.KC % GKB == 0;
-    if (p.wv == 7) {   // one fragment per wave, an x tile of 16 or 32 rows, whole 128-k blocks (the plan's test)
+    if (p.wv == 7) {   // one fragment per wave, an x tile of 16 to 128 rows, whole 128-k blocks (the plan's test)
         if (p.mb == 2) launch_gemm<1, 2, false, 7, WT>(a, grid, st);
+        else if (p.mb == 3) launch_gemm<1, 3, false, 7, WT>(a, grid, st);
+        else if (p.mb == 4) launch_gemm<1, 4, false, 7, WT>(a, grid, st);
+        else if (p.mb == 5) launch_gemm<1, 5, false, 7, WT>(a, grid, st);
+        else if (p.mb == 6) launch_gemm<1, 6, false, 7, WT>(a, grid, st);
+        else if (p.mb == 7) launch_gemm<1, 7, false, 7, WT>(a, grid, st);
+        else if (p.mb == 8) launch_gemm<1, 8, false, 7, WT>(a, grid, st);
         else launch_gemm<1, 1, false, 7, WT>(a, grid, st);
     } else if (p.nw == 2 && p.mb == 5) {   // two fragments (K % 128 == 0), x tiles of 80 to 112 rows
         launch_gemm<2, 5, false, 4, WT>(a, grid, st);

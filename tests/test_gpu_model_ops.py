@@ -192,7 +192,9 @@ def test_gemm_bf16_float32_x_equals_converting_first(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,ff,K", [(1, 2048, 4096), (5, 48, 160), (8, 512, 2048), (32, 14336, 4096),
-                                    (96, 512, 1024), (200, 136, 96), (288, 14336, 4096), (160, 512, 1024)])
+                                    (96, 512, 1024), (200, 136, 96), (288, 14336, 4096), (160, 512, 1024),
+                                    # 7-wave workgroups with x tiles of 48 to 128 rows (the Llama-3-8B gate/up)
+                                    (96, 14336, 4096), (65, 14336, 4096), (128, 14336, 4096), (40, 14336, 4096)])
 def test_gemm_bf16_swiglu_epilogue_equals_unfused(dev, M, ff, K):
     """The SwiGLU epilogue (interleaved gate/up rows) gives bit for bit the
     unfused result: the [gate; up] GEMM rounded to bf16, then the SwiGLU
