@@ -618,11 +618,17 @@ def run_e2e(args):
         alpha_a = st_[0] / max(st_[1], 1)
         gam = max(1, round(st_[1] / max(st_[2], 1)))
         meas = (tok / secs) / base_tps
+        # the model's best round at the measured acceptance (any gamma up to the bench's bound): what
+        # the arm could reach on this workload however fast the kernels were, next to its ceiling
+        best_g = max(range(1, args.gamma + 1), key=lambda g_: cost.speedup(arm, g_, alpha_a, ctx))
+        best = cost.speedup(arm, best_g, alpha_a, ctx)
         cost_model[arm.label()] = {
             "rounds": nr, "tok_s": tok / secs, "measured_speedup": meas,
             "ceiling": cost.ceiling(arm, ctx), "frac_of_ceiling": meas / cost.ceiling(arm, ctx),
             "modeled_speedup": cost.speedup(arm, gam, alpha_a, ctx), "gamma": gam, "alpha": alpha_a,
-            "frac_of_modeled": meas / cost.speedup(arm, gam, alpha_a, ctx)}
+            "frac_of_modeled": meas / cost.speedup(arm, gam, alpha_a, ctx),
+            "best_modeled_speedup_at_alpha": best, "best_gamma_at_alpha": best_g,
+            "best_at_alpha_frac_of_ceiling": best / cost.ceiling(arm, ctx)}
         if calibrated is not None:
             declined = st_[3] // max(b, 1)
             cost_cal[arm.label()] = {
