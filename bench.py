@@ -885,7 +885,7 @@ def run_accept(args):
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
     target = 2.0 * torch.randn((b, g + 1, V), generator=gen, device=dev)
-    draft = 2.0 * torch.randn((b, g, V), generator=gen, device=dev)
+    draft = 2.0 * torch.randn((g, b, V), generator=gen, device=dev)   # step-major, as the draft steps write it
     tok = torch.randint(0, V, (b, g), generator=gen, device=dev, dtype=torch.int32)
     u = torch.rand((b, g + 1), generator=gen, device=dev, dtype=torch.float64)
     T = args.temperature
@@ -893,7 +893,7 @@ def run_accept(args):
     if T > 0 and not args.recompute_draft_stats:   # what the draft steps' samples leave behind
         ds = ops.row_stats(b, dev, (g,))
         for i in range(g):
-            ops.sample(draft[:, i].contiguous(), T, u[:, i].contiguous(), stats_out=ds[i])
+            ops.sample(draft[i], T, u[:, i].contiguous(), stats_out=ds[i])
     for _ in range(args.warmup):
         ops.accept(target, draft, tok, T, u, ds)
     torch.cuda.synchronize()

@@ -157,11 +157,13 @@ __device__ __forceinline__ double dexp(double y, const double* tab) {
     return v;
 }
 
+// rows 0..gamma: target [batch][gamma+1][vocab]; gamma+1..2*gamma: draft rows
+// 0..gamma-1 of draft [gamma][batch][vocab] (step-major, as the draft steps
+// produce them)
 __device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int s, int row, int gamma,
-                                                int vocab) {
-    // rows 0..gamma: target; gamma+1..2*gamma: draft rows 0..gamma-1
+                                                int vocab, int batch) {
     if (row <= gamma) return target + ((int64_t)s * (gamma + 1) + row) * vocab;
-    return draft + ((int64_t)s * gamma + (row - gamma - 1)) * vocab;
+    return draft + ((int64_t)(row - gamma - 1) * batch + s) * vocab;
 }
 
 // ---- stats: one wave per chunk of SCH logits of one row, the chunk held
@@ -201,8 +203,8 @@ __device__ __forceinline__ void load_chunk(const float* x, int i0, int i1, int l
 
 template <bool VEC, bool SAMP>
 __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ target, const float* __restrict__ draft,
-                                                     int gamma, int vocab, float T, int nsc, int rows, int n_items,
-                                                     ChunkStat* __restrict__ stats) {
+                                                     int gamma, int vocab, int batch, float T, int nsc, int rows,
+                                                     int n_items, ChunkStat* __restrict__ stats) {
     constexpr int PER = SCH / WAVE;
     const int lane = threadIdx.x % WAVE;
     const int nw = gridDim.x * (ABLK / WAVE);
@@ -222,7 +224,7 @@ __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ t
     if (it < n_items) {
         int s, r, c;
         row_of(it, s, r, c);
-        load_chunk<VEC>(row_ptr(target, draft, s, r, gamma, vocab), c * SCH, min(vocab, c * SCH + SCH), lane, xn);
+        load_chunk<VEC>(row_ptr(target, draft, s, r, gamma, vocab, batch), c * SCH, min(vocab, c * SCH + SCH), lane, xn);
     }
     for (; it < n_items; it += nw) {
         float xv[PER];
@@ -231,7 +233,7 @@ __global__ void __launch_bounds__(ABLK) stats_kernel(const float* __restrict__ t
         if (it + nw < n_items) {   // the next chunk's loads are in flight while this one is reduced
             int s, r, c;
             row_of(it + nw, s, r, c);
-            load_chunk<VEC>(row_ptr(target, draft, s, r, gamma, vocab), c * SCH, min(vocab, c * SCH + SCH), lane,
+            load_chunk<VEC>(row_ptr(target, draft, s, r, gamma, vocab, batch), c * SCH, min(vocab, c * SCH + SCH), lane,
                             xn);
         }
         int s, r, c;
@@ -586,7 +588,7 @@ __global__ void __launch_bounds__(ABLK) finish_kernel(const float* __restrict__ 
                                                       int32_t* __restrict__ next_token,
                                                       int32_t* __restrict__ n_uniforms) {
     constexpr int PER = PCH / ABLK;
-    const int chunk = blockIdx.x, s = blockIdx.y;
+    const int chunk = blockIdx.x, s = blockIdx.y, batch = gridDim.y;
     const int tid = threadIdx.x, lane = tid % WAVE, w = tid / WAVE;
     const bool samp = T > 0.0f;
     const int R = 2 * gamma + 1;
@@ -627,8 +629,8 @@ __global__ void __launch_bounds__(ABLK) finish_kernel(const float* __restrict__ 
             if (lane < n) {
                 d = draft_tokens[(int64_t)s * gamma + i];
                 if (samp && d >= 0 && d < vocab) {   // never read past the row
-                    xp = row_ptr(target, draft, s, i, gamma, vocab)[d];
-                    xq = row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab)[d];
+                    xp = row_ptr(target, draft, s, i, gamma, vocab, batch)[d];
+                    xq = row_ptr(target, draft, s, gamma + 1 + i, gamma, vocab, batch)[d];
                 }
             }
         }
@@ -656,7 +658,7 @@ __global__ void __launch_bounds__(ABLK) finish_kernel(const float* __restrict__ 
             __syncthreads();
         }
         merge_sum(st, rid, nr, nsc, mm, samp, T, tab, lane, out);
-        if (samp && dstats && w == 1 && lane < n) dn[lane] = dstats[(int64_t)(base + lane) * gridDim.y + s];
+        if (samp && dstats && w == 1 && lane < n) dn[lane] = dstats[(int64_t)(base + lane) * batch + s];
         __syncthreads();
         if (w == 0 && n > 0) {
             bool ok = true;   // lanes past the round pass
@@ -715,7 +717,7 @@ __global__ void __launch_bounds__(ABLK) finish_kernel(const float* __restrict__ 
         const int c = s_chunk;
         if (c / (PCH / SCH) != chunk) return;
         const int i0 = c * SCH, i1 = min(vocab, i0 + SCH);
-        const float* pr = row_ptr(target, draft, s, acc, gamma, vocab);
+        const float* pr = row_ptr(target, draft, s, acc, gamma, vocab, batch);
         const double loc = range_masses<VEC>(pr, pr, pn, pn, 1, i0, i1, T, tab, stage, v);
         const int tok = scan_draw(v, loc, i0, i1, s_before, s_target, wsum, &found, &last_pos);
         if (tid == 0) next_token[s] = tok;
@@ -725,8 +727,8 @@ __global__ void __launch_bounds__(ABLK) finish_kernel(const float* __restrict__ 
     const RowNorm qn = dn[acc - base];
     if (chunk == 0 && tid == 0) recs[s] = PickRec{2, acc, uf, pn, qn};
     const int i0 = chunk * PCH, i1 = min(vocab, i0 + PCH);
-    const float* pr = row_ptr(target, draft, s, acc, gamma, vocab);
-    const float* qr = row_ptr(target, draft, s, gamma + 1 + acc, gamma, vocab);
+    const float* pr = row_ptr(target, draft, s, acc, gamma, vocab, batch);
+    const float* qr = row_ptr(target, draft, s, gamma + 1 + acc, gamma, vocab, batch);
     const double loc = range_masses<VEC>(pr, qr, pn, qn, 2, i0, i1, T, tab, stage, v);
     part[((int64_t)s * npc + chunk) * ABLK + tid] = loc;   // the thread's sum, for pick_kernel's scan
     double x = loc;
@@ -759,7 +761,7 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
                                                     const int32_t* __restrict__ accepted,
                                                     const PickRec* __restrict__ recs, int32_t* __restrict__ next_token) {
     constexpr int PER = PCH / ABLK;
-    const int s = blockIdx.x, tid = threadIdx.x, lane = tid % WAVE, w = tid / WAVE;
+    const int s = blockIdx.x, batch = gridDim.x, tid = threadIdx.x, lane = tid % WAVE, w = tid / WAVE;
     if (accepted[s] == gamma) return;   // drawn from p by finish_kernel
     const PickRec rec = recs[s];
     __shared__ double tab[EXP_TAB];
@@ -781,8 +783,8 @@ __global__ void __launch_bounds__(ABLK) pick_kernel(const float* __restrict__ ta
     }
     __syncthreads();
     const int mode = s_mode;
-    const float* pr = row_ptr(target, draft, s, rec.row, gamma, vocab);
-    const float* qr = row_ptr(target, draft, s, gamma + 1 + rec.row, gamma, vocab);
+    const float* pr = row_ptr(target, draft, s, rec.row, gamma, vocab, batch);
+    const float* qr = row_ptr(target, draft, s, gamma + 1 + rec.row, gamma, vocab, batch);
     if (mode == 2) {
         const int c = s_chunk, i0 = c * PCH;
         const double tgt = s_target;
@@ -920,8 +922,8 @@ static int accept_impl(const float* target, const float* draft, const int32_t* d
     const int grid = (int)std::min<int64_t>(resident[kind].load(std::memory_order_relaxed),
                                             (items + ABLK / WAVE - 1) / (ABLK / WAVE));
 #define DKV_STATS(V, S)                                                                                          \
-    hipLaunchKernelGGL((stats_kernel<V, S>), dim3(grid), dim3(ABLK), 0, st, target, draft, gamma, vocab, temperature, \
-                       nsc, rows, n_items, stats)
+    hipLaunchKernelGGL((stats_kernel<V, S>), dim3(grid), dim3(ABLK), 0, st, target, draft, gamma, vocab, batch,     \
+                       temperature, nsc, rows, n_items, stats)
     switch (kind) {
         case 0: DKV_STATS(false, false); break;
         case 1: DKV_STATS(true, false); break;

@@ -261,7 +261,7 @@ class DecodeBatch:
         self._graphs: dict = {}
         self._pool = None
         self._pending_key = None
-        self.last_draft = None            # (tokens, logits) of the last round's draft steps
+        self.last_draft = None            # (tokens [b, gamma], logits [gamma, b, V]) of the last round's draft steps
         self.phases = None                # a calibrate.PhaseLog to record per-round phase times
         # A round that declines to draft (gamma 0) does not wait for its token:
         # the next round reads it from the device (_dev_pending), and the host
@@ -486,7 +486,7 @@ class DecodeBatch:
         x = self._pending_dev()
         pending = x
         draft_tok = torch.empty((b, gamma), dtype=torch.int32, device=dev)
-        draft_logits = torch.empty((b, gamma, V), dtype=torch.float32, device=dev) if T > 0 else None
+        draft_logits = torch.empty((gamma, b, V), dtype=torch.float32, device=dev) if T > 0 else None   # step-major
         # the draft rows' normalisers, kept from each step's sample for the decision (as the
         # reference keeps the drafter's distributions, engine.py:176-179)
         draft_stats = ops.row_stats(b, dev, (gamma,)) if T > 0 else None
@@ -500,7 +500,7 @@ class DecodeBatch:
         for i in range(n_eager):
             lg = model.forward_batch(x[:, None], comp, n - 1 + i, act)[:, 0]
             if draft_logits is not None:
-                draft_logits[:, i].copy_(lg)
+                draft_logits[i].copy_(lg)
             x = ops.sample(lg, T, u_draft_d[i], stats_out=None if draft_stats is None else draft_stats[i])
             draft_tok[:, i] = x
         if graph is _RECORD:

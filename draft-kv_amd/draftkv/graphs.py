@@ -94,9 +94,10 @@ class DraftStepGraph:
             draft_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Run len(starts) steps from token x0 (int32 [b], device): step i
         appends at starts[i] (int [b]) the rows act (0/1 [b]) with uniforms
-        u[i] ([b]); tokens go to draft_tok[:, col0 + i], logits (when given) to
-        draft_logits[:, col0 + i] and the rows' normalisers (when given) to
-        draft_stats[col0 + i]. The mirror's ``seen`` advances as the eager
+        u[i] ([b]); tokens go to draft_tok[:, col0 + i], logits (when given)
+        to draft_logits[col0 + i] (step-major: one contiguous copy) and the
+        rows' normalisers (when given) to draft_stats[col0 + i]. The mirror's
+        ``seen`` advances as the eager
         steps would move it. Returns the last sampled token (a device view)."""
         steps, b = len(starts), self.b
         if steps == 0:
@@ -121,7 +122,7 @@ class DraftStepGraph:
             self.graph.replay()
             self.replays += 1
             if draft_logits is not None:
-                draft_logits[:, col0 + i].copy_(self.logits)
+                draft_logits[col0 + i].copy_(self.logits)
             if draft_stats is not None:
                 draft_stats[col0 + i].copy_(self.stats)
             draft_tok[:, col0 + i].copy_(self.tok)

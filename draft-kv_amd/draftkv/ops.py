@@ -311,8 +311,10 @@ def sample(logits: torch.Tensor, temperature: float, u: torch.Tensor,
 def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: torch.Tensor,
            temperature: float, u: torch.Tensor, draft_stats: Optional[torch.Tensor] = None):
     """Returns (accepted, next_token, n_uniforms) int32 [batch] device tensors.
-    ``draft_stats``: the draft rows' normalisers from ``sample(...,
-    stats_out=)``, [gamma, batch] rows of ``row_stats`` (step-major)."""
+    ``target`` [batch, gamma+1, vocab]; ``draft`` [gamma, batch, vocab] (the
+    draft steps' logits, step-major); ``draft_stats``: the draft rows'
+    normalisers from ``sample(..., stats_out=)``, [gamma, batch] rows of
+    ``row_stats`` (step-major)."""
     _need(target, "target", torch.float32, 3)
     _need(draft_tokens, "draft_tokens", torch.int32, 2)
     _need(u, "u", torch.float64, 2)
@@ -324,8 +326,8 @@ def accept(target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens: to
         if draft is None:
             raise ValueError("draft logits are needed when temperature > 0")
         _need(draft, "draft", torch.float32, 3)
-        if draft.shape != (b, gamma, V):
-            raise ValueError("draft must be [batch, gamma, vocab]")
+        if draft.shape != (gamma, b, V):
+            raise ValueError("draft must be [gamma, batch, vocab]")
     if draft_stats is not None:
         _need(draft_stats, "draft_stats", torch.float64, 3)
         if draft_stats.shape != (gamma, b, ROW_STATS_WORDS):

@@ -224,8 +224,9 @@ int dkv_sample(const float* logits, int64_t row_stride, int32_t batch, int32_t v
 /* ---------------------------------------------------------------- accept */
 /* Verify decision of one round for every sequence -- replaces
  * draftkv/engine.py:188-213. target: f32 [batch][gamma+1][vocab];
- * draft: f32 [batch][gamma][vocab] (the drafter's logits; unused when
- * T <= 0); draft_tokens int32 [batch][gamma]; u: f64 [batch][gamma+1]
+ * draft: f32 [gamma][batch][vocab] (the drafter's logits, step-major as the
+ * draft steps produce them; unused when T <= 0); draft_tokens int32
+ * [batch][gamma]; u: f64 [batch][gamma+1]
  * uniforms in the order the reference draws them (one per tested position in
  * sampling mode, then one for the bonus/residual token). draft_stats: NULL,
  * or [gamma][batch] (step-major, as the draft steps produce them) the draft

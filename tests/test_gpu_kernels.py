@@ -377,13 +377,15 @@ def _accept_case(ops, dev, b, gamma, V, T, seed, stats=False):
         for i in range(gamma):
             toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.95 else int(rng.integers(V))
     u = rng.random((b, gamma + 1))
-    t_d, d_d, k_d, u_d = (torch.from_numpy(x).to(dev) for x in (target, draft, toks, u))
+    # the draft steps' logits go to the library step-major: [gamma, batch, vocab]
+    t_d, d_d, k_d, u_d = (torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+                          for x in (target, draft.transpose(1, 0, 2), toks, u))
     acc, nxt, used = ops.accept(t_d, d_d, k_d, T, u_d)
     acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
     if stats and T > 0:
         ds = ops.row_stats(b, dev, (gamma,))
         for i in range(gamma):
-            ops.sample(d_d[:, i].contiguous(), T, u_d[:, i].contiguous(), stats_out=ds[i])
+            ops.sample(d_d[i], T, u_d[:, i].contiguous(), stats_out=ds[i])
         got = [x.cpu().numpy() for x in ops.accept(t_d, d_d, k_d, T, u_d, ds)]
         for x, y, name in zip((acc, nxt, used), got, ("accepted", "next_token", "n_uniforms")):
             assert np.array_equal(x, y), name
@@ -447,7 +449,8 @@ def test_accept_matches_reference_rule(dev, T, gamma):
             # mostly the target argmax so long runs get accepted, sometimes not
             toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.8 else int(rng.integers(V))
     u = rng.random((b, gamma + 1))
-    acc, nxt, used = ops.accept(torch.from_numpy(target).to(dev), torch.from_numpy(draft).to(dev),
+    acc, nxt, used = ops.accept(torch.from_numpy(target).to(dev),
+                                torch.from_numpy(np.ascontiguousarray(draft.transpose(1, 0, 2))).to(dev),
                                 torch.from_numpy(toks).to(dev), T, torch.from_numpy(u).to(dev))
     acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
     for s in range(b):
@@ -487,7 +490,8 @@ def test_accept_all_zero_residual_falls_back_to_p(dev, V):
         flat[1:].copy_(t_dev.reshape(-1))
         cases.append(flat[1:].view(b, gamma + 1, V))   # 4 bytes past an aligned start
     for tgt in cases:
-        acc, nxt, used = ops.accept(tgt, torch.from_numpy(draft).to(dev), torch.from_numpy(toks).to(dev), T,
+        acc, nxt, used = ops.accept(tgt, torch.from_numpy(np.ascontiguousarray(draft.transpose(1, 0, 2))).to(dev),
+                                    torch.from_numpy(toks).to(dev), T,
                                     torch.from_numpy(u).to(dev))
         acc, nxt, used = acc.cpu().numpy(), nxt.cpu().numpy(), used.cpu().numpy()
         for s in range(b):

@@ -24,7 +24,8 @@ def _case(seed, b, gamma, V, dev):
         for i in range(gamma):
             toks[s, i] = int(np.argmax(target[s, i])) if rng.random() < 0.8 else int(rng.integers(V))
     u = rng.random((b, gamma + 1))
-    return [torch.from_numpy(x).to(dev) for x in (target, draft, toks, u)]
+    # draft logits step-major, [gamma, batch, vocab], as the library takes them
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (target, draft.transpose(1, 0, 2), toks, u)]
 
 
 def _run(fn_noalloc, target, draft, toks, u, T):
@@ -67,7 +68,7 @@ def test_noalloc_refuses_more_than_the_scratch(dev):
     nbytes = L.dkv_accept_workspace(b, gamma, V)
     assert nbytes > (16 << 20)   # DKV_ACCEPT_SCRATCH_BYTES
     target = torch.zeros((b, gamma + 1, V), dtype=torch.float32, device=dev)
-    draft = torch.zeros((b, gamma, V), dtype=torch.float32, device=dev)
+    draft = torch.zeros((gamma, b, V), dtype=torch.float32, device=dev)
     toks = torch.zeros((b, gamma), dtype=torch.int32, device=dev)
     u = torch.zeros((b, gamma + 1), dtype=torch.float64, device=dev)
     outs = [torch.zeros(b, dtype=torch.int32, device=dev) for _ in range(3)]
