@@ -219,7 +219,7 @@ __device__ void copy_row_head(const RowCtx& c, int h, int from, int to, int lane
 
 // Keep rows with pos < thr: move survivors from [new_n, n) into the holes of
 // [0, new_n). Returns new_n. Whole block participates.
-__device__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes, int* movers) {
+__device__ __forceinline__ int compact(const RowCtx& c, int n, int32_t thr, int* red, int* holes, int* movers) {
     int keep = 0;
     for (int r = threadIdx.x; r < n; r += OP_BLK) keep += (c.pos[r] < thr);
     const int new_n = block_sum_int(keep, red);
@@ -275,7 +275,7 @@ static_assert(DEADLIST <= OP_BLK && DEADLIST <= MAXMOVE, "a list compaction rank
 // order in list[0..k). Same result as compact(): the holes are the dead
 // slots below n - k in slot order, the movers the live slots of [n - k, n)
 // in slot order, paired by rank; no pass over the other rows.
-__device__ int compact_list(const RowCtx& c, int n, int k, OpShared& sh) {
+__device__ __forceinline__ int compact_list(const RowCtx& c, int n, int k, OpShared& sh) {
     if (k == 0) return n;
     const int new_n = n - k;
     for (int i = threadIdx.x; i < k; i += OP_BLK) {
@@ -311,7 +311,8 @@ __device__ int compact_list(const RowCtx& c, int n, int k, OpShared& sh) {
 // dead list (counted past DEADLIST, not listed); when bits, the other rows'
 // positions below WIN and within WIN under maxpos set the window bitmaps.
 // Returns the dead count.
-__device__ int scan_rows(const RowCtx& c, int n, bool trunc, int32_t p0, bool bits, int32_t maxpos, OpShared& sh) {
+__device__ __forceinline__ int scan_rows(const RowCtx& c, int n, bool trunc, int32_t p0, bool bits, int32_t maxpos,
+                                         OpShared& sh) {
     if (bits)
         for (int i = threadIdx.x; i < WIN / 32; i += OP_BLK) {
             sh.bits_lo[i] = 0u;
@@ -352,7 +353,8 @@ __device__ int scan_rows(const RowCtx& c, int n, bool trunc, int32_t p0, bool bi
 // The lowest (score, position) row with sink_max < pos < recent_min, marked
 // DEAD and put in the dead list at index k; every thread gets its slot (-1
 // when no row qualifies). 16 rows per thread per step.
-__device__ int select_victim(const RowCtx& c, int n, int32_t sink_max, int32_t recent_min, int k, OpShared& sh) {
+__device__ __forceinline__ int select_victim(const RowCtx& c, int n, int32_t sink_max, int32_t recent_min, int k,
+                                             OpShared& sh) {
     double best = INFINITY;
     int32_t bpos = INT_MAX;
     int bslot = -1;
@@ -428,16 +430,116 @@ __device__ int select_victim(const RowCtx& c, int n, int32_t sink_max, int32_t r
     return bs;
 }
 
+// One victim when the protected windows are the contiguous position ranges
+// [0, sink) and [maxpos - recent + 1, maxpos] (every position in them live,
+// the usual case of a decode step): one pass over rows [0, n) counts the live
+// positions in both windows (`absent` of them are not in those rows yet: the
+// rows about to be appended) and finds the lowest (score, position) row
+// strictly between them -- the victim select_victim would pick under the
+// bounds those windows give. Returns the victim's slot, marked DEAD and
+// listed at sh.list[0]; -1 when a window is not whole or no row lies between
+// them (the caller then takes the general path; nothing was changed).
+__device__ __forceinline__ int select_fast(const RowCtx& c, int n, int sink, int recent, int32_t maxpos, int absent,
+                                           OpShared& sh) {
+    const int32_t smax = sink - 1, rmin = maxpos - recent + 1;
+    double best = INFINITY;
+    int32_t bpos = INT_MAX;
+    int bslot = -1, cnt = 0;   // cnt: live rows in the two windows
+    for (int base = 0; base < n; base += 16 * OP_BLK) {
+        int4 pv[4];
+        double2 sa[4], sb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK);
+            if (r < n) {
+                pv[j] = *reinterpret_cast<const int4*>(c.pos + r);
+                sa[j] = *reinterpret_cast<const double2*>(c.score + r);
+                sb[j] = *reinterpret_cast<const double2*>(c.score + r + 2);
+            } else {
+                pv[j] = make_int4(DEAD, DEAD, DEAD, DEAD);
+                sa[j] = sb[j] = make_double2(0.0, 0.0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int32_t pe[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+            const double se[4] = {sa[j].x, sa[j].y, sb[j].x, sb[j].y};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = base + 4 * ((int)threadIdx.x + j * OP_BLK) + e;
+                const int32_t p = pe[e];
+                if (r >= n || p == DEAD) continue;
+                if (p <= smax || (p >= rmin && p <= maxpos)) {
+                    ++cnt;
+                } else if (p > smax && p < rmin && (se[e] < best || (se[e] == best && p < bpos))) {
+                    best = se[e];
+                    bpos = p;
+                    bslot = r;
+                }
+            }
+        }
+    }
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const double ob = __shfl_xor(best, o);
+        const int32_t op = __shfl_xor(bpos, o);
+        const int os = __shfl_xor(bslot, o);
+        cnt += __shfl_xor(cnt, o);
+        if (ob < best || (ob == best && op < bpos)) {
+            best = ob;
+            bpos = op;
+            bslot = os;
+        }
+    }
+    const int w = threadIdx.x / WAVE;
+    __syncthreads();
+    if (threadIdx.x % WAVE == 0) {
+        sh.redd[w] = best;
+        sh.rpos[w] = bpos;
+        sh.rslot[w] = bslot;
+        sh.red[w] = cnt;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double b = sh.redd[0];
+        int32_t bp = sh.rpos[0];
+        int bs = sh.rslot[0], total = sh.red[0];
+        for (int i = 1; i < OP_WAVES; ++i) {
+            total += sh.red[i];
+            if (sh.redd[i] < b || (sh.redd[i] == b && sh.rpos[i] < bp)) {
+                b = sh.redd[i];
+                bp = sh.rpos[i];
+                bs = sh.rslot[i];
+            }
+        }
+        if (total != sink + recent - absent) bs = -1;   // a window is not whole: the general path decides
+        if (bs >= 0) {
+            c.pos[bs] = DEAD;
+            sh.list[0] = bs;
+        }
+        sh.count = bs;
+    }
+    __syncthreads();
+    const int bs = sh.count;
+    __syncthreads();
+    return bs;
+}
+
 // Evict down to `budget` (compress.py:159-179): protected = the `sink` lowest
 // and `recent` highest live positions (recent == 0 protects all); drop the
 // n - budget lowest (score, position) of the rest. have_bits: the window
 // bitmaps already hold every live row but the `cnt` appended at p0.. (maxpos
 // = p0 + cnt - 1).
-__device__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t p0, int cnt, bool have_bits,
-                     OpShared& sh) {
+// (every helper of the op kernel is inlined: a call would give the kernel a
+// stack in scratch, whose setup costs more than the eviction itself)
+__device__ __forceinline__ int evict(const RowCtx& c, int n, int budget, dkv_qcfg_t cfg, int32_t p0, int cnt,
+                                     bool have_bits, OpShared& sh) {
     if (n <= budget || cfg.recent == 0) return n;
     const int n_drop = n - budget;
     const int32_t maxpos = p0 + cnt - 1;
+    // the usual decode step: one victim, both windows whole (disjoint, with rows between them)
+    if (n_drop == 1 && maxpos - cfg.recent + 1 > cfg.sink &&
+        select_fast(c, n, cfg.sink, cfg.recent, maxpos, 0, sh) >= 0)
+        return compact_list(c, n, 1, sh);
     // sink-th smallest and recent-th largest live positions, from bitmaps of
     // the windows [0, WIN) and (maxpos - WIN, maxpos]
     if (have_bits) {
@@ -527,10 +629,25 @@ __global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
     }
     int cnt = want;
     if (n + cnt > m.cap) cnt = max(0, m.cap - n);   // the host sizes cap; never write past it
+    const int budget = cnt > 0 ? a.budget[a.budget_per_layer ? (L * m.batch + s) : s] : 0;
+    // The decode step (one row in, one over budget, both protected windows
+    // whole): the victim is found first, over the rows already there (the new
+    // row is the newest, protected), and the new row is written into its slot
+    // -- what the append, the eviction and the compaction that moves the new
+    // row into the hole leave, without the moves.
+    int dest = n;   // slot of the first appended row
+    bool replaced = false;
+    if (!a.do_trunc && cnt == 1 && cfg.recent != 0 && n + 1 - budget == 1 && p0 - cfg.recent + 1 > cfg.sink) {
+        const int v = select_fast(c, n, cfg.sink, cfg.recent, p0, 1, sh);
+        if (v >= 0) {
+            dest = v;
+            replaced = true;
+        }
+    }
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
     for (int h = w; h < H; h += OP_WAVES) {        // one wave per head segment
         for (int t = 0; t < cnt; ++t) {
-            const int slot = n + t;
+            const int slot = dest + t;
             uint8_t* page = page_ptr(m, s, L, h, slot / PAGE);
             const int i = slot % PAGE;
             if (a.src_full) {
@@ -553,10 +670,9 @@ __global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
         }
     }
     __syncthreads();
-    n += cnt;
-    if (cnt > 0) {
-        const int budget = a.budget[a.budget_per_layer ? (L * m.batch + s) : s];
-        n = evict(c, n, budget, cfg, p0, cnt, have_bits && cnt == want, sh);
+    if (!replaced) {
+        n += cnt;
+        if (cnt > 0) n = evict(c, n, budget, cfg, p0, cnt, have_bits && cnt == want, sh);
     }
     __syncthreads();
     if (threadIdx.x == 0) *nrows_p = n;
