@@ -252,8 +252,37 @@ struct LaneOffsets {
     uint32_t k[2], km[2], v, vm;
 };
 
+// N words as N/4 pieces of 16 bytes, piece x at src + 1024 x, non-temporal
+// (a page is read once per call; each load instruction of the wave reads 1 KB
+// of contiguous bytes, so no 64-byte segment is split between instructions,
+// which under this policy would be fetched twice)
+typedef uint32_t pu32x4_t __attribute__((ext_vector_type(4)));
+template <int N>
+__device__ __forceinline__ void load_pieces_nt(uint32_t (&dst)[N], const uint8_t* src) {
+    static_assert(N % 4 == 0, "whole 16-byte pieces");
+#pragma unroll
+    for (int x = 0; x < N / 4; ++x) {
+        const pu32x4_t w = __builtin_nontemporal_load(reinterpret_cast<const pu32x4_t*>(src + 1024 * x));
+        dst[4 * x] = w[0];
+        dst[4 * x + 1] = w[1];
+        dst[4 * x + 2] = w[2];
+        dst[4 * x + 3] = w[3];
+    }
+}
+
 template <int D, int CB, int MF>
 __device__ __forceinline__ void load_page(PageRegs<D, CB, MF>& r, const uint8_t* pg, const LaneOffsets& o) {
+    if constexpr (CB == 8) {   // K and V codes in lane load order (D % 64 == 0)
+        static_assert(D % 64 == 0, "8-bit pages in lane load order");
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            load_pieces_nt(r.k[a], pg + o.k[a]);
+            load_words(r.km[a], pg + o.km[a]);
+        }
+        load_pieces_nt(r.v, pg + o.v);
+        load_words(r.vm, pg + o.vm);
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
         load_words(r.k[a], pg + o.k[a]);
@@ -596,6 +625,11 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const PageFmt& f, int col, i
     }
     off.v = (uint32_t)(f.vc + (col * 4 + jj) * Regs::NV * 4);
     off.vm = (uint32_t)(f.vm + ((int64_t)gmeta * PAGE + jj * 8) * f.metaB);
+    if constexpr (CB == 8) {   // lane load order: the lane's first 16-byte piece
+#pragma unroll
+        for (int a = 0; a < 2; ++a) off.k[a] = (uint32_t)(f.kc + a * 16 * D + 16 * (col + 16 * jj));
+        off.v = (uint32_t)(f.vc + 16 * (col * 4 + jj));
+    }
     return off;
 }
 

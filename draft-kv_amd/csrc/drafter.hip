@@ -85,8 +85,8 @@ __device__ __forceinline__ void put_k_lane(uint8_t* page, const PageFmt& f, int 
             w0 |= static_cast<uint32_t>(lc.code[e]) << code_shift(8, e);
             w1 |= static_cast<uint32_t>(lc.code[4 + e]) << code_shift(8, e);
         }
-        sec[((int64_t)i * f.D + d0) / 4] = w0;
-        sec[((int64_t)i * f.D + d0) / 4 + 1] = w1;
+        sec[k_word(f, i, d0 / 4)] = w0;
+        sec[k_word(f, i, d0 / 4 + 1)] = w1;
     }
     if (d0 % f.group == 0) write_meta(page + k_meta_off(f, i, d0 / f.group), lc.m, f.meta_f16);
 }
@@ -191,8 +191,8 @@ __device__ void copy_row_head(const RowCtx& c, int h, int from, int to, int lane
     } else {
         const int wpr = D * f.cb / 32;   // K words per row
         for (int w = lane; w < wpr; w += WAVE)
-            reinterpret_cast<uint32_t*>(dst + f.kc)[(int64_t)ti * wpr + w] =
-                reinterpret_cast<const uint32_t*>(src + f.kc)[(int64_t)fi * wpr + w];
+            reinterpret_cast<uint32_t*>(dst + f.kc)[k_word(f, ti, w)] =
+                reinterpret_cast<const uint32_t*>(src + f.kc)[k_word(f, fi, w)];
         for (int d = lane; d < D; d += WAVE) {
             int64_t ws, wd;
             int ss, sd;
@@ -992,8 +992,8 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
                         w0 |= static_cast<uint32_t>(code[e]) << code_shift(8, e);
                         w1 |= static_cast<uint32_t>(code[4 + e]) << code_shift(8, e);
                     }
-                    sec[((int64_t)i * D + d0) / 4] = w0;
-                    sec[((int64_t)i * D + d0) / 4 + 1] = w1;
+                    sec[k_word(pf, i, d0 / 4)] = w0;
+                    sec[k_word(pf, i, d0 / 4 + 1)] = w1;
                 }
                 if (first) write_meta(pg + k_meta_off(pf, i, d0 / pf.group), gm, pf.meta_f16);
             } else {
@@ -1015,7 +1015,8 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
         __syncthreads();
 
         // ---- 3. V code words: word ((a*4 + j)*NDT + t) holds channel d = 16t + a of
-        // the rows (j, e) = {4j..4j+3, 16+4j..16+4j+3}; bytes: two words per (a, j, t)
+        // the rows (j, e) = {4j..4j+3, 16+4j..16+4j+3}; bytes: two words per (a, j, t),
+        // placed by v8_word
         uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
         const int per = pf.cb == 4 ? 8 : 4;                     // rows per word
         const int n_words = 16 * 4 * pf.NDT * (8 / per);
@@ -1033,7 +1034,7 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_page_kernel(RebuildArgs a
                 const uint32_t code = sm.vcode[i][d];
                 w |= code << (pf.cb == 4 ? code_shift(4, e) : code_shift(8, q));
             }
-            vsec[pf.cb == 4 ? base : base * 2 + half] = w;
+            vsec[pf.cb == 4 ? base : v8_word(pf, aj, t, half)] = w;
         }
     }
 }
@@ -1183,7 +1184,9 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
                             w0 |= code[e] << code_shift(8, e);
                             w1 |= code[4 + e] << code_shift(8, e);
                         }
-                        *reinterpret_cast<uint2*>(sec + i * 32 + 2 * oct) = make_uint2(w0, w1);
+                        // words 2 oct and 2 oct + 1 of the row: adjacent (and 8-byte aligned) in
+                        // the lane-order layout too
+                        *reinterpret_cast<uint2*>(sec + k_word(pf, i, 2 * oct)) = make_uint2(w0, w1);
                     }
                     if (first) write_meta(pg + k_meta_off(pf, i, oct / GL), gm, MF);
                 }
@@ -1203,8 +1206,9 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
         }
         __syncthreads();
 
-        // ---- V code words: word (a*4 + j)*8 + t holds channel d = 16t + a of the
-        // rows {4j..4j+3} (k-slots 0..3) and {16+4j..16+4j+3} (k-slots 4..7)
+        // ---- V code words: group (a*4 + j)*8 + t holds channel d = 16t + a of the
+        // rows {4j..4j+3} (k-slots 0..3) and {16+4j..16+4j+3} (k-slots 4..7); 4-bit
+        // codes one word per group, bytes two (placed by v8_word)
         uint32_t* vsec = reinterpret_cast<uint32_t*>(pg + pf.vc);
 #pragma unroll
         for (int y = 0; y < 2; ++y) {
@@ -1222,8 +1226,10 @@ __global__ void __launch_bounds__(BLK) drafter_rebuild_fast_kernel(RebuildArgs a
                           (byte(lo, 1) << 16) | (byte(lo, 3) << 20) | (byte(hi, 1) << 24) | (byte(hi, 3) << 28);
             } else {
                 // slot q of each 4-row half at code_shift(8, q): q = 0, 2, 1, 3 in bytes 0..3
-                vsec[2 * w] = byte(lo, 0) | (byte(lo, 2) << 8) | (byte(lo, 1) << 16) | (byte(lo, 3) << 24);
-                vsec[2 * w + 1] = byte(hi, 0) | (byte(hi, 2) << 8) | (byte(hi, 1) << 16) | (byte(hi, 3) << 24);
+                vsec[v8_word(pf, aj, t, 0)] =
+                    byte(lo, 0) | (byte(lo, 2) << 8) | (byte(lo, 1) << 16) | (byte(lo, 3) << 24);
+                vsec[v8_word(pf, aj, t, 1)] =
+                    byte(hi, 0) | (byte(hi, 2) << 8) | (byte(hi, 1) << 16) | (byte(hi, 3) << 24);
             }
         }
     }

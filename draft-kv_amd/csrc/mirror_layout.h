@@ -20,6 +20,16 @@
 // cb (stored code bits) = 4 for bits <= 4, 8 for bits == 8, 32 for bits == 16
 // (raw float32 values, K and V row-major, no meta). Meta pairs are float32
 // or float16. The layout needs D % 16 == 0 or D == 8.
+//
+// 8-bit codes with D % 64 == 0 keep those words in the order the attention
+// kernel's lanes load them, so that each 16-byte load instruction of a wave
+// reads 1 KB of contiguous bytes (whole 64-byte segments, which lets the
+// loads bypass the caches). In 16-row tile T of K, lane (c, g) = lane
+// c + 16 g holds the D/16 words g D/16 .. (g + 1) D/16 - 1 of row 16 T + c,
+// in pieces of 4 words, piece x at word 256 x + 4 lane of the tile (a tile
+// is 4 D words). In V, lane L = 4 a + j holds the 2 NDT words of channel
+// column a and row group j (word 2 t + half for d = 16 t + a), piece x at
+// word 256 x + 4 L. The words are the ones above, at other places.
 #pragma once
 
 #include "dkv_common.h"
@@ -62,11 +72,34 @@ __host__ __device__ inline int code_shift(int cb, int e) {
     return 8 * ((e & 1) * 2 + (e >> 1));
 }
 
+// 8-bit codes stored in lane load order (see the top of the file)
+__host__ __device__ inline bool lane_order8(const PageFmt& f) { return f.cb == 8 && f.D % 64 == 0; }
+
+// index in the K section of word w (0 .. D*cb/32 - 1) of row i
+__host__ __device__ inline int64_t k_word(const PageFmt& f, int i, int w) {
+    if (lane_order8(f)) {
+        const int wpl = f.D / 16;           // words per lane group
+        const int g = w / wpl, u = w % wpl;
+        return (int64_t)(i / 16) * (4 * f.D) + (u / 4) * 256 + (i % 16 + 16 * g) * 4 + u % 4;
+    }
+    return (int64_t)i * (f.D * f.cb / 32) + w;
+}
+
 // (word index, shift) of K code (row i, channel d) relative to the K section
 __host__ __device__ inline void k_code_loc(const PageFmt& f, int i, int d, int64_t* word, int* shift) {
     const int per = 32 / f.cb;                          // codes per word
-    *word = ((int64_t)i * f.D + d) / per;
+    *word = k_word(f, i, d / per);
     *shift = code_shift(f.cb, d % per);
+}
+
+// index in the V section of 8-bit code word `half` of the (a*4 + j, t) group
+// (channel d = 16 t + a, rows of group j; half 0: k-slots 0..3, 1: 4..7)
+__host__ __device__ inline int64_t v8_word(const PageFmt& f, int aj, int t, int half) {
+    if (lane_order8(f)) {
+        const int u = 2 * t + half;         // the word's place in the lane's run
+        return (int64_t)(u / 4) * 256 + aj * 4 + u % 4;
+    }
+    return ((int64_t)aj * f.NDT + t) * 2 + half;
 }
 
 // row i -> (lane group j, k-slot e) of the PV product
@@ -79,12 +112,11 @@ __host__ __device__ inline void v_code_loc(const PageFmt& f, int i, int d, int64
     int j, e;
     v_slot(i, &j, &e);
     const int a = d % 16, t = d / 16;
-    const int64_t base = ((int64_t)a * 4 + j) * f.NDT + t;
     if (f.cb == 4) {
-        *word = base;
+        *word = ((int64_t)a * 4 + j) * f.NDT + t;
         *shift = code_shift(4, e);
     } else {
-        *word = base * 2 + e / 4;
+        *word = v8_word(f, a * 4 + j, t, e / 4);
         *shift = code_shift(8, e % 4);
     }
 }
