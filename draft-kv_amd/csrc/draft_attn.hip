@@ -209,10 +209,12 @@ __device__ __forceinline__ f16x8_t codes_to_f16(const uint32_t* w) {
         r.w = (x >> 12) & 0x000F000Fu;
 #endif
     } else {
+        // bytes 0 and 2 by an AND; bytes 1 and 3 moved down by one byte
+        // permute (selector 0x0c: a zero byte) instead of a shift and an AND
         r.x = w[0] & 0x00FF00FFu;
-        r.y = (w[0] >> 8) & 0x00FF00FFu;
+        r.y = __builtin_amdgcn_perm(w[0], 0u, 0x0c070c05u);
         r.z = w[1] & 0x00FF00FFu;
-        r.w = (w[1] >> 8) & 0x00FF00FFu;
+        r.w = __builtin_amdgcn_perm(w[1], 0u, 0x0c070c05u);
     }
     return __builtin_bit_cast(f16x8_t, r);
 }
