@@ -30,6 +30,7 @@
 // lanes; the V page layout (mirror_layout.h) is the PV A operand.
 #include <hip/hip_ext.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "mirror_layout.h"
@@ -1609,6 +1610,27 @@ static bool fast_path(const dkv_drafter_t& m, const dkv_qcfg_t& c, int Hq) {
 
 using namespace dkv;
 
+// Workgroups of `fn` (`threads` threads, `lds` bytes of dynamic LDS) the
+// device holds at once; kept per kernel (recomputed if the LDS size changes)
+struct Resident {
+    std::atomic<size_t> lds{0};
+    std::atomic<int> blocks{0};
+};
+static int resident_blocks(const void* fn, int threads, size_t lds, Resident& r) {
+    const int b = r.blocks.load(std::memory_order_relaxed);
+    if (b > 0 && r.lds.load(std::memory_order_relaxed) == lds) return b;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess || cus <= 0 ||
+        per_cu <= 0)
+        cus = 256, per_cu = 2;
+    r.blocks.store(0, std::memory_order_relaxed);
+    r.lds.store(lds, std::memory_order_relaxed);
+    r.blocks.store(cus * per_cu, std::memory_order_relaxed);
+    return cus * per_cu;
+}
+
 static int n_splits_of(const dkv_drafter_t* m, int n_q_heads) {
     const int rps = rows_per_split(*m, n_q_heads / std::max(m->n_kv_heads, 1));
     return (m->cap + rps - 1) / rps;
@@ -1775,11 +1797,25 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
         // blocks of 4 waves; each wave walks splits blockIdx.x*4 + wave, +
         // 4*gridDim.x, ..., so any row count up to cap is covered. Both
         // kernels run one resident round: 512 blocks of the LDS-staged one
-        // (8 waves per CU), 1024 of the register-staged one (16 waves per CU;
-        // measured 8-10% faster than 1536 blocks, whose waves took uneven
-        // numbers of splits)
+        // (8 waves per CU), and for the register-staged one as many as the
+        // device holds at once by its registers and LDS (two blocks per CU
+        // above 128 VGPRs: 512 at b=32 ctx 32k int8, 359-363 against 365-372
+        // us for two rounds of 1024; a round of waves that each take the same
+        // number of splits measured 8-10% faster than 1536 blocks)
         const bool dma = cfg.bits <= 4 && m.head_dim == 128;
-        const int per_seg = std::max(1, (dma ? 512 : 1024) / std::max(1, m.n_kv_heads * m.batch));
+        const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
+        const void* rk[8] = {reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 4, 0>),
+                             reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 4, 1>),
+                             reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 8, 0>),
+                             reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 8, 1>),
+                             nullptr,
+                             nullptr,
+                             reinterpret_cast<const void*>(draft_attn_mfma_kernel<128, 8, 0>),
+                             reinterpret_cast<const void*>(draft_attn_mfma_kernel<128, 8, 1>)};
+        const size_t rlds = sizeof(float) * 4 * ((size_t)G * rps + 8 * WAVE);
+        static Resident resident[8];
+        const int round = dma ? 512 : resident_blocks(rk[key] ? rk[key] : rk[7], 256, rlds, resident[key]);
+        const int per_seg = std::max(1, round / std::max(1, m.n_kv_heads * m.batch));
         const dim3 grid(std::min((ns + 3) / 4, per_seg), m.n_kv_heads, m.batch);
         n_parts = 4 * (int)grid.x;   // one partial per wave
         if (dma) {
@@ -1819,10 +1855,8 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
 #undef DKV_DMA2
 #undef DKV_DMA
         } else {
-            const int key = (m.head_dim == 128 ? 4 : 0) | (cfg.bits == 8 ? 2 : 0) | (cfg.meta_f16 ? 1 : 0);
-            const size_t lds = sizeof(float) * 4 * ((size_t)G * rps + 8 * WAVE);
 #define DKV_LAUNCH(DD, CC, MM)                                                                                 \
-    launch_splitk(draft_attn_mfma_kernel<DD, CC, MM>, grid, dim3(256), lds, st, m, (int)layer, cfg, q,          \
+    launch_splitk(draft_attn_mfma_kernel<DD, CC, MM>, grid, dim3(256), rlds, st, m, (int)layer, cfg, q,         \
                   (int)n_q_heads, scale, rps, ns, part, logits)
             switch (key) {
                 case 0: DKV_LAUNCH(64, 4, 0); break;
