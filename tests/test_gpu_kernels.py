@@ -210,8 +210,11 @@ def _same_mirror(mo, md, L, codes=True):
         assert np.array_equal(k, ko) and np.array_equal(v, vo)
 
 
-ARMS = [Cfg(8, 1.0), Cfg(4, 0.5), Cfg(4, 0.25, group=32, meta="f16"), Cfg(2, 0.25), Cfg(3, 0.5, 2, 5),
-        Cfg(16, 0.5), Cfg(4, 0.3, 4, 0)]
+# (8-bit arms that evict: with head_dim a multiple of 64 their pages are in
+# the attention kernel's lane load order, which the appends, the compaction
+# moves and the rebuilds must all write)
+ARMS = [Cfg(8, 1.0), Cfg(8, 0.5), Cfg(8, 0.4, 2, 8, group=32, meta="f16"), Cfg(4, 0.5),
+        Cfg(4, 0.25, group=32, meta="f16"), Cfg(2, 0.25), Cfg(3, 0.5, 2, 5), Cfg(16, 0.5), Cfg(4, 0.3, 4, 0)]
 
 
 def _dcfg(c: Cfg):
@@ -235,14 +238,15 @@ def test_build_and_rebuild_match_reference(dev, arm):
     _same_mirror(mo, md, L)
 
 
+@pytest.mark.parametrize("D", [32, 64])
 @pytest.mark.parametrize("arm", ARMS, ids=lambda c: f"{c.bits}b{c.keep_frac}g{c.group}{c.meta}s{c.sink}r{c.recent}")
-def test_steady_state_eviction_truncate_and_resync(dev, arm):
+def test_steady_state_eviction_truncate_and_resync(dev, arm, D):
     """Drafting appends one row at a time with accumulated scores; the
     victims, the compaction, truncation and the per-round resync must leave
     the same rows (positions, codes, scores) as the reference."""
     draftkv, _ = _dk()
-    rng = np.random.default_rng(11 + arm.bits)
-    L, H, D, n = 2, 2, 32, 120
+    rng = np.random.default_rng(11 + arm.bits + D)
+    L, H, n = 2, 2, 120
     full_o, full_d, _, _ = _full_pair(L, H, D, n, rng, dev)
     mo = oc.CompressedKVCache(L, [arm] * L)
     md = draftkv.CompressedKVCache(L, [_dcfg(arm)] * L)
@@ -287,7 +291,8 @@ def test_steady_state_eviction_truncate_and_resync(dev, arm):
 
 
 # ------------------------------------------------------------------ drafter attention
-@pytest.mark.parametrize("arm", [Cfg(8, 1.0), Cfg(4, 0.25, group=32, meta="f16"), Cfg(16, 0.5), Cfg(2, 0.5)],
+@pytest.mark.parametrize("arm", [Cfg(8, 1.0), Cfg(8, 0.5, group=32, meta="f16"), Cfg(4, 0.25, group=32, meta="f16"),
+                                 Cfg(16, 0.5), Cfg(2, 0.5)],
                          ids=lambda c: f"{c.bits}b{c.keep_frac}")
 @pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 16), (32, 8, 128), (9, 3, 64)])
 def test_drafter_attention_and_mass(dev, arm, Hq, Hkv, D):
