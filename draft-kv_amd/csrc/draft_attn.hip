@@ -637,14 +637,22 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const PageFmt& f, int col, i
 }
 
 // ---- register-staged kernel (8-bit codes): pages loaded straight into
-// registers one page ahead; logits staged in LDS and written after the split
-template <int D, int CB, int MF>
-__global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg,
-                                                                 const float* __restrict__ q, int Hq, float scale,
-                                                                 int rps, int n_splits, float* __restrict__ part,
-                                                                 float* __restrict__ logits) {
+// registers one page ahead; logits staged in LDS and written after the split.
+// MERGE: one block of 8 waves per (sequence, KV head) segment (batches whose
+// segments alone fill the chip): the waves' partials meet in LDS and the
+// block writes the segment's output (and its rows' (max, sum)), so no
+// combine kernel runs; the partials are merged as the combine merges them
+// (the max over the waves first, then the weighted sums, waves in order).
+constexpr int MERGE_WAVES = 8;
+template <int D, int CB, int MF, bool MERGE = false>
+__global__ void __launch_bounds__(MERGE ? 64 * MERGE_WAVES : 256, MERGE ? 1 : 2)
+draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* __restrict__ q, int Hq, float scale,
+                       int rps, int n_splits, float* __restrict__ part, float* __restrict__ logits,
+                       float* __restrict__ out, float* __restrict__ stats) {
     using Core = SplitCore<D, CB, MF>;
     using Regs = typename Core::Regs;
+    constexpr int NWB = MERGE ? MERGE_WAVES : 4;   // waves per block
+    constexpr int PD = D + 2;
     // the wave index through readfirstlane: the compiler then knows it (and
     // the split, row range and page addresses) to be wave-uniform, keeps them
     // in scalar registers and runs the page loop as a scalar loop
@@ -652,23 +660,29 @@ __global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m
     const int h = blockIdx.y, s = blockIdx.z;
     const int G = Hq / m.n_kv_heads;
     const int n = m.n_rows[(int64_t)s * m.n_layers + layer];
+    extern __shared__ float dyn_smem[];
+    float* mp = dyn_smem + NWB * (G * rps + 8 * WAVE);   // MERGE: partials [G][NWB][D + 2]
     // the grid covers the splits of a few resident rounds; each wave walks
-    // splits blockIdx.x*4 + wave, + 4*gridDim.x, ... while they hold rows
-    if ((int)(blockIdx.x * 4 + wave) * rps >= n) return;
+    // splits blockIdx.x*NWB + wave, + NWB*gridDim.x, ... while they hold rows
+    const bool idle = (int)(blockIdx.x * NWB + wave) * rps >= n;
+    if (!MERGE && idle) return;
+    if (idle) {   // a neutral partial (no rows): max -inf, sum 0, output 0
+        for (int i = lane; i < G * PD; i += WAVE)
+            mp[((i / PD) * NWB + wave) * PD + i % PD] = (i % PD == D) ? -INFINITY : 0.0f;
+    } else {
     const PageFmt f = page_fmt(cfg, D);
     Core c;
     c.init(q, s, h, Hq, G, cfg.group, lane, scale);
     const LaneOffsets off = lane_offsets<D, CB, MF>(f, c.col, c.jj, c.gmeta);
-    extern __shared__ float dyn_smem[];
     float* slog = dyn_smem + wave * (G * rps + 8 * WAVE);
     const bool writer = c.cvalid && c.gcol == 0;
     const int slog_base = writer ? c.hcol * rps + 4 * c.jj : G * rps + 8 * lane;
     const int slog_step = writer ? 1 : 0, slog_second = writer ? 16 : 4;
     // one softmax state across all of the wave's splits: the wave writes a
-    // single partial, in slot blockIdx.x*4 + wave
+    // single partial, in slot blockIdx.x*NWB + wave
     c.reset();
-    const int part_slot = blockIdx.x * 4 + wave;
-    for (int split = part_slot; split < n_splits && split * rps < n; split += 4 * gridDim.x) {
+    const int part_slot = blockIdx.x * NWB + wave;
+    for (int split = part_slot; split < n_splits && split * rps < n; split += NWB * gridDim.x) {
     const int r_begin = split * rps;
     const int r_end = min(r_begin + rps, n);
 
@@ -724,7 +738,33 @@ __global__ void __launch_bounds__(256, 2) draft_attn_mfma_kernel(dkv_drafter_t m
         }
     }
     }
-    c.finish(part, s, h, Hq, G, n_splits, part_slot);
+    if constexpr (MERGE) c.finish(mp, 0, 0, G, G, NWB, wave);
+    else c.finish(part, s, h, Hq, G, n_splits, part_slot);
+    }
+    if constexpr (MERGE) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < G * D; i += 64 * NWB) {
+            const int hq = i / D, d = i % D;
+            const float* ph = mp + hq * NWB * PD;
+            float mm = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NWB; ++w) mm = fmaxf(mm, ph[w * PD + D]);
+            float l = 0.0f, o = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NWB; ++w) {
+                const float mc = ph[w * PD + D];
+                const float wt = (mc == -INFINITY) ? 0.0f : __expf(mc - mm);
+                l = fmaf(ph[w * PD + D + 1], wt, l);
+                o = fmaf(ph[w * PD + d], wt, o);
+            }
+            const int64_t row = (int64_t)s * Hq + h * G + hq;
+            out[row * D + d] = (l > 0.0f) ? o / l : 0.0f;
+            if (d == 0 && stats) {
+                stats[row * 2] = mm;
+                stats[row * 2 + 1] = l;
+            }
+        }
+    }
 }
 
 // ---- LDS-staged kernel (4-bit codes). Each wave streams its pages through a
@@ -1746,6 +1786,7 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     float* logits = want_mass ? reinterpret_cast<float*>(static_cast<char*>(work) + wl.logits_off) : nullptr;
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(m.head_dim)));
     hipStream_t st = as_stream(stream);
+    bool merged = false;   // the attention kernel merged its partials itself
     int n_parts = ns;   // partial slots written (one per split in the generic kernel)
     int unit = rps;     // rows per unit of work that owns a partial slot
     // One block of 8 waves per (sequence, KV head) segment when the segments
@@ -1855,9 +1896,34 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
 #undef DKV_DMA2
 #undef DKV_DMA
         } else {
-#define DKV_LAUNCH(DD, CC, MM)                                                                                 \
-    launch_splitk(draft_attn_mfma_kernel<DD, CC, MM>, grid, dim3(256), rlds, st, m, (int)layer, cfg, q,         \
-                  (int)n_q_heads, scale, rps, ns, part, logits)
+            // when one block per (sequence, KV head) segment fills the device,
+            // 8-wave blocks (the same waves per segment as two 4-wave blocks)
+            // merge their partials in LDS and no combine kernel runs
+            const size_t mlds = sizeof(float) * ((size_t)MERGE_WAVES * ((size_t)G * rps + 8 * WAVE) +
+                                                 (size_t)G * MERGE_WAVES * (m.head_dim + 2));
+            const void* mk[8] = {reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 4, 0, true>),
+                                 reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 4, 1, true>),
+                                 reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 8, 0, true>),
+                                 reinterpret_cast<const void*>(draft_attn_mfma_kernel<64, 8, 1, true>),
+                                 nullptr,
+                                 nullptr,
+                                 reinterpret_cast<const void*>(draft_attn_mfma_kernel<128, 8, 0, true>),
+                                 reinterpret_cast<const void*>(draft_attn_mfma_kernel<128, 8, 1, true>)};
+            const void* mfn = mk[key] ? mk[key] : mk[7];
+            static size_t mlds_done[16] = {};
+            static Resident mresident[8];
+            merged = reserve_lds(mfn, mlds, mlds_done) &&
+                     m.n_kv_heads * m.batch >= resident_blocks(mfn, 64 * MERGE_WAVES, mlds, mresident[key]);
+#define DKV_LAUNCH(DD, CC, MM)                                                                                  \
+    do {                                                                                                         \
+        if (merged)                                                                                              \
+            launch_splitk(draft_attn_mfma_kernel<DD, CC, MM, true>, dim3(1, m.n_kv_heads, m.batch),              \
+                          dim3(64 * MERGE_WAVES), mlds, st, m, (int)layer, cfg, q, (int)n_q_heads, scale, rps, ns, \
+                          part, logits, out, stats);                                                             \
+        else                                                                                                     \
+            launch_splitk(draft_attn_mfma_kernel<DD, CC, MM>, grid, dim3(256), rlds, st, m, (int)layer, cfg, q,  \
+                          (int)n_q_heads, scale, rps, ns, part, logits, out, stats);                             \
+    } while (0)
             switch (key) {
                 case 0: DKV_LAUNCH(64, 4, 0); break;
                 case 1: DKV_LAUNCH(64, 4, 1); break;
@@ -1874,11 +1940,13 @@ extern "C" int dkv_drafter_attention(const dkv_drafter_t* mirror, int32_t layer,
     }
     int rc = check_launch("dkv_drafter_attention");
     if (rc) return rc;
-    // one wave of the combine per 8 partials, up to 16 waves
-    const int comb_waves = std::min(COMB_WAVES, std::max(1, (std::min(n_parts, ns) + 7) / 8));
-    hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(WAVE * comb_waves), 0, st, m, layer,
-                       part, n_q_heads, unit, ns, n_parts, out, stats);
-    if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
+    if (!merged) {
+        // one wave of the combine per 8 partials, up to 16 waves
+        const int comb_waves = std::min(COMB_WAVES, std::max(1, (std::min(n_parts, ns) + 7) / 8));
+        hipLaunchKernelGGL(draft_combine_kernel, dim3(n_q_heads, m.batch), dim3(WAVE * comb_waves), 0, st, m, layer,
+                           part, n_q_heads, unit, ns, n_parts, out, stats);
+        if ((rc = check_launch("dkv_drafter_attention(combine)"))) return rc;
+    }
     if (want_mass) {
         const int per_block = 256 * MASS_ROWS;
         hipLaunchKernelGGL(draft_mass_kernel, dim3((m.cap + per_block - 1) / per_block, m.batch), dim3(256),
