@@ -33,13 +33,8 @@ struct LaneCodes {
     GroupMeta m;
 };
 
-template <class Load>
-__device__ __forceinline__ void quant_lane(Load ld, const PageFmt& f, int bits, int lane, LaneCodes& lc) {
-    const int d0 = 8 * lane;
-    const bool real = d0 < f.D;
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = real ? ld(d0 + e) : 0.0f;
+// codes and group meta of this lane's 8 channel values (zero past D)
+__device__ __forceinline__ void quant_vals(const float (&v)[8], const PageFmt& f, int bits, int lane, LaneCodes& lc) {
     if (f.cb == 32) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) lc.raw[e] = v[e];
@@ -61,6 +56,16 @@ __device__ __forceinline__ void quant_lane(Load ld, const PageFmt& f, int bits, 
     lc.m = group_meta(mn, mx, bits, f.meta_f16);
 #pragma unroll
     for (int e = 0; e < 8; ++e) lc.code[e] = quant_code(v[e], lc.m, bits);
+}
+
+template <class Load>
+__device__ __forceinline__ void quant_lane(Load ld, const PageFmt& f, int bits, int lane, LaneCodes& lc) {
+    const int d0 = 8 * lane;
+    const bool real = d0 < f.D;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = real ? ld(d0 + e) : 0.0f;
+    quant_vals(v, f, bits, lane, lc);
 }
 
 __device__ __forceinline__ void put_k_lane(uint8_t* page, const PageFmt& f, int i, int lane, const LaneCodes& lc) {
@@ -123,6 +128,16 @@ __device__ __forceinline__ void quant_row(LoadK ldk, LoadV ldv, const PageFmt& f
     quant_lane(ldk, f, bits, lane, lc);
     put_k_lane(page, f, i, lane, lc);
     quant_lane(ldv, f, bits, lane, lc);
+    put_v_lane(page, f, i, lane, lc);
+}
+
+// the same from this lane's 8 K and 8 V channel values, already loaded
+__device__ __forceinline__ void quant_row_vals(const float (&kv)[8], const float (&vv)[8], const PageFmt& f, int bits,
+                                               uint8_t* page, int i, int lane) {
+    LaneCodes lc;
+    quant_vals(kv, f, bits, lane, lc);
+    put_k_lane(page, f, i, lane, lc);
+    quant_vals(vv, f, bits, lane, lc);
     put_v_lane(page, f, i, lane, lc);
 }
 
@@ -612,6 +627,21 @@ __global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
     __shared__ OpShared sh;
 
     RowCtx c{&a.m, s, L, cfg.bits, page_fmt(cfg, D), m.pos + row_index(m, s, L), m.score + row_index(m, s, L)};
+    // the one-row append of a decode step: the wave that owns head w loads
+    // the row's K and V channels first, with the row count, as neither
+    // depends on the mirror's state
+    const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
+    const bool pre = !a.src_full && a.T == 1 && w < H;
+    float pk[8], pv[8];
+    if (pre) {
+        const int64_t src = ((int64_t)s * H + w) * D;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int d = 8 * lane + e;
+            pk[e] = d < D ? load_elem(a.k, src + d, a.in_dtype) : 0.0f;
+            pv[e] = d < D ? load_elem(a.v, src + d, a.in_dtype) : 0.0f;
+        }
+    }
     int32_t* nrows_p = m.n_rows + (int64_t)s * m.n_layers + L;
     int n = *nrows_p;
     const int32_t p0 = a.start[s];
@@ -644,13 +674,14 @@ __global__ void __launch_bounds__(OP_BLK) drafter_op_kernel(OpArgs a) {
             replaced = true;
         }
     }
-    const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
     for (int h = w; h < H; h += OP_WAVES) {        // one wave per head segment
         for (int t = 0; t < cnt; ++t) {
             const int slot = dest + t;
             uint8_t* page = page_ptr(m, s, L, h, slot / PAGE);
             const int i = slot % PAGE;
-            if (a.src_full) {
+            if (pre && h == w) {   // (T == 1: t == 0) the channels loaded above
+                quant_row_vals(pk, pv, c.f, cfg.bits, page, i, lane);
+            } else if (a.src_full) {
                 const dkv_paged_t& f = a.full;
                 const int pos = p0 + t;
                 const int32_t blk = paged_block(f, s, L, pos);
