@@ -699,10 +699,7 @@ draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* 
     const int np = (r_end - r_begin + PAGE - 1) / PAGE;
     const int nfull = (r_end - r_begin) / PAGE;   // pages whose 32 rows are all live
     const int pg0 = r_begin / PAGE;
-    auto fetch = [&](Regs& b, int k) {
-        // past the last page, reload the last one (no branch around the loads)
-        load_page(b, page_ptr(m, s, layer, h, pg0 + min(k, np - 1)), off);
-    };
+    auto fetch = [&](Regs& b, int k) { load_page(b, page_ptr(m, s, layer, h, pg0 + k), off); };
     // Full pages: page k+1 is in flight while page k is computed (two
     // buffers, unrolled by 2). The scheduling barriers keep each fetch ahead
     // of the page's products: left alone, the scheduler sinks the loads into
@@ -712,11 +709,13 @@ draft_attn_mfma_kernel(dkv_drafter_t m, int layer, dkv_qcfg_t cfg, const float* 
     if (nfull > 0) {
         fetch(b0, 0);
         for (int k = 0; k < nfull; k += 2) {
-            fetch(b1, k + 1);
+            // (wave-uniform tests: no fetch past the split's last page, which
+            // a split of whole pages would otherwise load twice)
+            if (k + 1 < np) fetch(b1, k + 1);
             __builtin_amdgcn_sched_barrier(0);
             c.template page<false>(b0, r_begin + k * PAGE, r_end, stage);
             if (k + 1 >= nfull) break;
-            fetch(b0, k + 2);
+            if (k + 2 < np) fetch(b0, k + 2);
             __builtin_amdgcn_sched_barrier(0);
             c.template page<false>(b1, r_begin + (k + 1) * PAGE, r_end, stage);
         }
