@@ -316,6 +316,46 @@ def test_drafter_attention_and_mass(dev, arm, Hq, Hkv, D):
     assert mass.shape == (nr,)
 
 
+@pytest.mark.parametrize("arm,D", [(Cfg(8, 1.0), 64), (Cfg(8, 0.5, group=32, meta="f16"), 64),
+                                   (Cfg(4, 0.5), 64), (Cfg(4, 0.25, group=32, meta="f16"), 64),
+                                   (Cfg(8, 1.0), 128), (Cfg(8, 0.5, group=64, meta="f16"), 128)],
+                         ids=lambda x: f"{x.bits}b{x.keep_frac}{x.meta}" if isinstance(x, Cfg) else f"D{x}")
+def test_drafter_attention_merged_blocks(dev, arm, D):
+    """512 (sequence, KV head) segments (batch 64, 8 KV heads, 32 query
+    heads): one block per segment fills the device, so the register-staged
+    kernel runs as 8-wave blocks that merge their waves' partials in LDS and
+    write the output and row statistics themselves (no combine kernel).
+    Ragged lengths (300 - 3 s rows) leave some waves of every block with no
+    page. Every sequence's output and the mass added to its kept rows match
+    the oracle's."""
+    import draftkv
+    b, Hkv, Hq = 64, 8, 32
+    lens = np.array([300 - 3 * s for s in range(b)], np.int64)
+    T = int(lens.max())
+    full = draftkv.PagedKVCache(1, Hkv, D, 16, T // 16 + 2, dtype=np.float32, batch=b, max_tokens=T + 32)
+    full.reserve(lens)
+    rng = np.random.default_rng(D + arm.bits)
+    k = rng.standard_normal((b, T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((b, T, Hkv, D)).astype(np.float32)
+    full.append_layer(0, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                      torch.zeros(b, dtype=torch.int32, device=dev), torch.tensor(lens, dtype=torch.int32, device=dev))
+    full.commit(lens)
+    md = draftkv.CompressedKVCache(1, [_dcfg(arm)], batch=b, cap=T + 32)
+    md.sync_from(full, 0)
+    q = (rng.standard_normal((b, Hq, D)) * 2.0).astype(np.float32)
+    out = md.attend(0, torch.from_numpy(q).to(dev), want_mass=True).cpu().numpy()
+    for s in range(b):
+        n = int(lens[s])
+        g = md.read_codes(0, s)
+        pos = g["pos"].astype(np.int64)
+        kq = quantize_codes(k[s][pos], arm.bits, arm.group, arm.meta)
+        vq = quantize_codes(v[s][pos], arm.bits, arm.group, arm.meta)
+        ref, _, mp = attend(q[s][None], kq[3], vq[3], pos, np.array([n]), Hq // Hkv)
+        np.testing.assert_allclose(out[s], ref[0], rtol=RTOL, atol=ATOL, err_msg=f"seq {s}")
+        np.testing.assert_allclose(g["score"], row_mass(mp).astype(np.float64), rtol=1e-4, atol=1e-7,
+                                   err_msg=f"seq {s} mass")
+
+
 def test_splitk_timing_hook_times_each_call(dev):
     """The benchmark hook records events around the split-K kernel only: its
     time is positive and below the whole call's, and off means no events."""
