@@ -1437,6 +1437,8 @@ __global__ void __launch_bounds__(256) draft_mass_sum_kernel(dkv_drafter_t m, in
 constexpr int SMERGE_ROWS = 256;    // rows per block of the mass part (one per thread)
 constexpr int SMERGE_MAX_NB = 64;    // segment blocks
 constexpr int SMERGE_MAX_HKV = 16;   // KV heads
+constexpr int SMERGE_PRE = 32;       // partial outputs per merge thread loaded with the statistics
+constexpr int SMERGE_PER = 4;        // statistics loads per thread
 __global__ void __launch_bounds__(256) draft_seg_merge_kernel(dkv_drafter_t m, int layer, int nb,
                                                               const float* __restrict__ part,
                                                               const float* __restrict__ pk, float* __restrict__ out,
@@ -1452,11 +1454,55 @@ __global__ void __launch_bounds__(256) draft_seg_merge_kernel(dkv_drafter_t m, i
     __shared__ float sm[SMERGE_MAX_HKV * SMERGE_MAX_NB * G], sl[SMERGE_MAX_HKV * SMERGE_MAX_NB * G];
     const int h_lo = merge ? blockIdx.x : 0, h_hi = merge ? blockIdx.x + 1 : Hkv;
     const int nh = h_hi - h_lo, cnt = nh * nbl * G;   // (head, block, query head) entries
-    for (int i = threadIdx.x; i < cnt; i += blockDim.x) {
-        const int hq = i % G, b = (i / G) % nbl, hh = i / (G * nbl);
-        const float* pp = part + ((((int64_t)s * Hkv + h_lo + hh) * nb + b) * G + hq) * PD;
-        sm[i] = pp[D];
-        sl[i] = pp[D + 1];
+    // The loads go out together before the first wait: what the sums need
+    // besides the factors (a merge block's partial outputs of the first
+    // SMERGE_PRE blocks, a mass block's kept values and old score) does not
+    // depend on the blocks' statistics, and the statistics are SMERGE_PER
+    // independent loads per thread (cnt <= 1024: the host keeps nb * Hkv <=
+    // 256). Clamped indices keep the loads unconditional; what they read past
+    // nbl is never used.
+    float xo[2][SMERGE_PRE];   // merge: partial outputs i = tid, tid + 256
+    float4 p[SMERGE_MAX_HKV];  // mass: kept values of row r, every KV head
+    double old = 0.0;
+    const int r = ((int)blockIdx.x - Hkv) * SMERGE_ROWS + threadIdx.x;
+    double* score = merge ? nullptr : m.score + row_index(m, s, layer) + r;
+    if (merge) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = threadIdx.x + 256 * k, hq = i / D, d = i % D;
+            const float* pp = part + (((int64_t)s * Hkv + h_lo) * nb * G + hq) * PD + d;
+#pragma unroll
+            for (int b = 0; b < SMERGE_PRE; ++b) xo[k][b] = pp[(int64_t)min(b, max(nbl - 1, 0)) * G * PD];
+        }
+    } else if (r < n) {
+        old = *score;
+#pragma unroll
+        for (int hh = 0; hh < SMERGE_MAX_HKV; ++hh)
+            if (hh < Hkv) p[hh] = *reinterpret_cast<const float4*>(pk + (((int64_t)s * Hkv + hh) * m.cap + r) * G);
+    }
+    const int nb1 = max(nbl, 1);   // (no page: the merge blocks still read one in-bounds partial)
+    auto stat_ptr = [&](int i) {
+        const int hq = i % G, b = (i / G) % nb1, hh = i / (G * nb1);
+        // (max, sum) of one partial: PD * 4 and D * 4 are multiples of 8
+        return reinterpret_cast<const float2*>(part + ((((int64_t)s * Hkv + h_lo + hh) * nb + b) * G + hq) * PD + D);
+    };
+    {
+        float2 st[SMERGE_PER];
+#pragma unroll
+        for (int k = 0; k < SMERGE_PER; ++k) st[k] = *stat_ptr(min((int)threadIdx.x + 256 * k, max(cnt - 1, 0)));
+#pragma unroll
+        for (int k = 0; k < SMERGE_PER; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < cnt) {
+                sm[i] = st[k].x;
+                sl[i] = st[k].y;
+            }
+        }
+        for (int i = threadIdx.x + 256 * SMERGE_PER; i < cnt; i += 256) {   // not reached while nb * Hkv <= 256
+            const float2 v = *stat_ptr(i);
+            sm[i] = v.x;
+            sl[i] = v.y;
+        }
     }
     __syncthreads();
     // the merged (max, 1/sum) of each (head, query head): 4 lanes per pair
@@ -1493,34 +1539,25 @@ __global__ void __launch_bounds__(256) draft_seg_merge_kernel(dkv_drafter_t m, i
     }
     __syncthreads();
     if (merge) {
-        // outputs (query head hq, channel d) of KV head h_lo: two per thread
-        for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
-            const int hq = i / D, d = i % D;
-            const float* pp = part + (((int64_t)s * Hkv + h_lo) * nb * G + hq) * PD + d;
+        // outputs (query head hq, channel d) of KV head h_lo, two per thread:
+        // the blocks' terms in block order
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = threadIdx.x + 256 * k, hq = i / D, d = i % D;
             float o = 0.0f;
-            int b = 0;
-            for (; b + 8 <= nbl; b += 8) {   // 8 partials' loads in flight, then their terms in order
-                float x[8];
+            // (a block past nbl adds its clamped copy times 0: a finite x
+            // times 0 leaves o as it is)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) x[k] = pp[(int64_t)(b + k) * G * PD];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) o = fmaf(x[k], sm[(b + k) * G + hq], o);
-            }
-            for (; b < nbl; ++b) o = fmaf(pp[(int64_t)b * G * PD], sm[b * G + hq], o);
+            for (int b = 0; b < SMERGE_PRE; ++b) o = fmaf(xo[k][b], b < nbl ? sm[b * G + hq] : 0.0f, o);
+            const float* pp = part + (((int64_t)s * Hkv + h_lo) * nb * G + hq) * PD + d;
+            for (int b = SMERGE_PRE; b < nbl; ++b) o = fmaf(pp[(int64_t)b * G * PD], sm[b * G + hq], o);
             out[((int64_t)s * Hq + h_lo * G + hq) * D + d] = o;
         }
         return;
     }
-    const int r = ((int)blockIdx.x - Hkv) * SMERGE_ROWS + threadIdx.x;
     if (r >= n) return;
     const int b = (r / PAGE) / ppb;
-    double* score = m.score + row_index(m, s, layer) + r;
-    const double old = *score;
-    // every head's kept values at once (all loads in flight), then the sums in order
-    float4 p[SMERGE_MAX_HKV];
-#pragma unroll
-    for (int hh = 0; hh < SMERGE_MAX_HKV; ++hh)
-        if (hh < Hkv) p[hh] = *reinterpret_cast<const float4*>(pk + (((int64_t)s * Hkv + hh) * m.cap + r) * G);
+    // the sums over KV heads in order
     float t = 0.0f;
 #pragma unroll
     for (int hh = 0; hh < SMERGE_MAX_HKV; ++hh)
