@@ -240,14 +240,16 @@ def test_draft_step_eviction_and_resync_match_oracle(dev, cache):
     assert md.rows()[:, LAYER].tolist() == kept
 
 
-@pytest.mark.parametrize("T", [1, 9, 17])
+@pytest.mark.parametrize("T", [1, 3, 5, 9, 17])
 def test_verify_attention_matches_oracle(dev, cache, T):
     """T query rows per sequence at positions n-T .. n-1 over keys 0 .. own
     position of the benchmark cache (ragged ~32k rows, shuffled 16-token bf16
     pages), with the key chunk the cache picks for its shape: every sequence
     within 2e-3 / 1e-3 of the oracle (llama.py:202-218 via engine.py:184-185).
-    T = 1, 9, 17 make 1, 3, 5 sixteen-row query tiles, so the kernel runs with
-    1, 4 and 8 waves per workgroup."""
+    T = 1, 3, 5, 9, 17 make 1, 1, 2, 3, 5 sixteen-row query tiles, so the
+    kernel runs with 1, 1, 2, 4 and 8 waves per workgroup; T = 3 (the verify
+    pass at gamma 2, the benchmark's usual one) leaves 4 of its tile's 16 rows
+    empty, T = 5 (gamma 4) 12 of its second tile's."""
     full, host = cache
     assert full.chunk_keys == 8192
     rng = np.random.default_rng(20 + T)
