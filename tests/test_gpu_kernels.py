@@ -442,10 +442,11 @@ def _accept_case(ops, dev, b, gamma, V, T, seed, stats=False):
 
 
 @pytest.mark.parametrize("T", [0.0, 0.8])
-@pytest.mark.parametrize("b,gamma", [(32, 8), (32, 16), (32, 20), (4, 80)])
+@pytest.mark.parametrize("b,gamma", [(32, 2), (32, 3), (32, 8), (32, 16), (32, 20), (4, 80)])
 def test_accept_matches_reference_rule_at_bench_points(dev, T, b, gamma):
     """Where the benchmark runs the decision: batch 32, the Llama-3-8B
-    vocabulary (128256), gamma up to the bench's 20, greedy and T = 0.8; and
+    vocabulary (128256), gamma from the 2-3 its controller settles on up to
+    its bound of 20, greedy and T = 0.8; and
     a draft longer than one 64-position block of the decide kernel. Accepted
     counts, next tokens and uniforms consumed equal the oracle rule's
     (engine.py:188-213) for every sequence."""
