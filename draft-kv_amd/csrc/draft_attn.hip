@@ -1545,10 +1545,9 @@ __global__ void __launch_bounds__(256) draft_seg_merge_kernel(dkv_drafter_t m, i
         for (int k = 0; k < 2; ++k) {
             const int i = threadIdx.x + 256 * k, hq = i / D, d = i % D;
             float o = 0.0f;
-            // (a block past nbl adds its clamped copy times 0: a finite x
-            // times 0 leaves o as it is)
 #pragma unroll
-            for (int b = 0; b < SMERGE_PRE; ++b) o = fmaf(xo[k][b], b < nbl ? sm[b * G + hq] : 0.0f, o);
+            for (int b = 0; b < SMERGE_PRE; ++b)
+                if (b < nbl) o = fmaf(xo[k][b], sm[b * G + hq], o);
             const float* pp = part + (((int64_t)s * Hkv + h_lo) * nb * G + hq) * PD + d;
             for (int b = SMERGE_PRE; b < nbl; ++b) o = fmaf(pp[(int64_t)b * G * PD], sm[b * G + hq], o);
             out[((int64_t)s * Hq + h_lo * G + hq) * D + d] = o;
